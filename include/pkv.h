@@ -1,0 +1,243 @@
+/*
+ * pkv.h — C ABI of the MI355X (gfx950) PersistentKV paged decode-attention engine.
+ *
+ * Every entry point takes plain device pointers, sizes and a HIP stream passed as
+ * `void*` (a hipStream_t; NULL selects the null stream).  Nothing here allocates device
+ * memory: outputs, the split workspace and the merge counters are owned by the caller,
+ * exactly as in the reference op surface.  Calls enqueue work asynchronously and never
+ * synchronise the host.  Errors are reported as a pkv_status code; a one-line message
+ * describing the last failure on the calling thread is available from pkv_last_error().
+ *
+ * Layouts (all row-major, contiguous):
+ *   q / q_source   [rows, num_q_heads, 128]                   fp16 or bf16
+ *   k_pages/v_pages[num_pages, num_kv_heads, page_size, 128]  same dtype as q
+ *   block_table    [batch, max_pages]                         int32 physical page ids
+ *   seq_lens       [batch]                                    int32 tokens per row
+ *   output         [out_rows, num_q_heads, 128]               same dtype as q
+ *   work_items     [num_tasks, 5] int32 = {row, kv_head, split, tile_begin, tile_end}
+ *                  (tiles are 32-token units, independent of page_size)
+ *   split_offsets  [batch + 1]                                int32 prefix sum of row splits
+ *   merge_counters [batch, num_kv_heads]                      int32, zero on entry and exit
+ *   workspace      fp32 [m: n][l: n][acc: n x 128] with n = batch*num_q_heads*num_splits
+ *                  (grid split) or total_partial_slots*num_q_heads (work queue).
+ *
+ * Query head h reads KV head h / G with G = num_q_heads / num_kv_heads.  The softmax
+ * scale is fixed at 1/sqrt(128).  G may be any integer in [1, 32]; the reference accepts
+ * only {1, 2, 4, 8}.  Reference citations are into ahmed123hds/persistentkv-attention.
+ */
+#ifndef PKV_H_
+#define PKV_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PKV_HEAD_DIM 128     /* kernels/persistentkv_attention.cuh:26 (PKV_D) */
+#define PKV_TILE_TOKENS 32   /* kernels/persistentkv_attention.cuh:28 (PKV_TILE) */
+#define PKV_MAX_GROUP 32     /* largest supported Hq / Hkv */
+
+typedef enum pkv_status {
+  PKV_OK = 0,
+  PKV_ERR_INVALID_ARGUMENT = 1,  /* a shape, pointer or size is inconsistent */
+  PKV_ERR_UNSUPPORTED = 2,       /* a valid request this build does not implement */
+  PKV_ERR_WORKSPACE_TOO_SMALL = 3,
+  PKV_ERR_LAUNCH = 4,            /* the HIP runtime rejected a kernel launch */
+  PKV_ERR_CAPACITY = 5           /* a host builder output buffer is too small */
+} pkv_status;
+
+typedef enum pkv_dtype { PKV_DTYPE_F16 = 0, PKV_DTYPE_BF16 = 1 } pkv_dtype;
+
+/* Text of the most recent error on this thread ("" when none). */
+const char* pkv_last_error(void);
+/* Static name of a status code. */
+const char* pkv_status_string(int status);
+/* Library version as major*10000 + minor*100 + patch. */
+int pkv_version(void);
+
+/* ---------------------------------------------------------------------------------
+ * Workspace sizing.
+ * ------------------------------------------------------------------------------- */
+
+/* Bytes of split workspace for the grid-split ops; 0 when num_splits <= 1.
+ * Replaces persistentkv_workspace_bytes, kernels/persistentkv_attention.cuh:891-898. */
+size_t pkv_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t num_splits);
+
+/* Bytes of workspace for the work-queue op (total_partial_slots partial states per head).
+ * Replaces persistentkv_partition_workqueue_workspace sizing, cuh:915-927. */
+size_t pkv_workqueue_workspace_bytes(int32_t total_partial_slots, int32_t num_q_heads);
+
+/* ---------------------------------------------------------------------------------
+ * The four ops.  Argument order follows the torch op surface of
+ * tests/persistentkv_torch_extension.cu, with the tensor shapes spelled out.
+ * ------------------------------------------------------------------------------- */
+
+/* Every row attends to exactly `context` tokens.
+ * Replaces persistentkv_paged_attention (tests/persistentkv_torch_extension.cu:35-93)
+ * and persistentkv_paged_dispatch (kernels/persistentkv_attention.cuh:1114-1136). */
+int pkv_paged_attention(
+    const void* q, const void* k_pages, const void* v_pages,
+    const int32_t* block_table, void* output,
+    void* workspace, size_t workspace_bytes,
+    int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t num_pages, int32_t page_size, int32_t max_pages,
+    int32_t context, int32_t num_splits, int32_t dtype, void* stream);
+
+/* Row b attends to seq_lens[b] tokens; bucket_context bounds num_splits.
+ * Replaces persistentkv_paged_attention_masked (extension.cu:95-157) and
+ * persistentkv_paged_masked_dispatch (cuh:1138-1161). */
+int pkv_paged_attention_masked(
+    const void* q, const void* k_pages, const void* v_pages,
+    const int32_t* block_table, const int32_t* seq_lens, void* output,
+    void* workspace, size_t workspace_bytes,
+    int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t num_pages, int32_t page_size, int32_t max_pages,
+    int32_t bucket_context, int32_t num_splits, int32_t dtype, void* stream);
+
+/* Row b reads query row q_indices[b] of q_source and writes output row out_indices[b].
+ * Replaces persistentkv_paged_attention_indexed (extension.cu:159-228) and
+ * persistentkv_paged_masked_indexed_dispatch (cuh:1163-1189). */
+int pkv_paged_attention_indexed(
+    const void* q_source, int32_t q_rows,
+    const void* k_pages, const void* v_pages,
+    const int32_t* block_table, const int32_t* seq_lens,
+    const int32_t* q_indices, const int32_t* out_indices,
+    void* output, int32_t out_rows,
+    void* workspace, size_t workspace_bytes,
+    int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t num_pages, int32_t page_size, int32_t max_pages,
+    int32_t bucket_context, int32_t num_splits, int32_t dtype, void* stream);
+
+/* Compact work queue: one partial state per work item, then a segmented LSE merge
+ * (or, with fused_merge != 0, the last work item of each (row, kv head) merges).
+ * Replaces persistentkv_paged_attention_workqueue (extension.cu:230-317) and
+ * persistentkv_paged_workqueue_indexed_dispatch (cuh:1191-1261). */
+int pkv_paged_attention_workqueue(
+    const void* q_source, int32_t q_rows,
+    const void* k_pages, const void* v_pages,
+    const int32_t* block_table, const int32_t* seq_lens,
+    const int32_t* work_items, int32_t num_tasks,
+    const int32_t* split_offsets, int32_t* merge_counters,
+    const int32_t* q_indices, const int32_t* out_indices,
+    void* output, int32_t out_rows,
+    void* workspace, size_t workspace_bytes,
+    int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t num_pages, int32_t page_size, int32_t max_pages,
+    int32_t bucket_context, int32_t total_partial_slots, int32_t fused_merge,
+    int32_t dtype, void* stream);
+
+/* The two stages of pkv_paged_attention_workqueue with fused_merge == 0, callable on
+ * their own (for per-kernel timing and for callers that overlap the merge with other
+ * work).  Running decode then merge on one stream equals the combined call.  The
+ * reference launches both from one host function (cuh:1005-1017); it has no separate
+ * entry points. */
+int pkv_workqueue_decode(
+    const void* q_source, int32_t q_rows,
+    const void* k_pages, const void* v_pages,
+    const int32_t* block_table, const int32_t* seq_lens,
+    const int32_t* work_items, int32_t num_tasks,
+    const int32_t* split_offsets, const int32_t* q_indices,
+    void* workspace, size_t workspace_bytes,
+    int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t num_pages, int32_t page_size, int32_t max_pages,
+    int32_t bucket_context, int32_t total_partial_slots, int32_t dtype, void* stream);
+
+int pkv_workqueue_merge(
+    const int32_t* seq_lens, const int32_t* split_offsets, const int32_t* out_indices,
+    void* output, int32_t out_rows,
+    const void* workspace, size_t workspace_bytes,
+    int32_t batch, int32_t num_q_heads, int32_t total_partial_slots,
+    int32_t dtype, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * Host scheduling: split policy, cost model and compact work-queue builder.
+ * Pure host code (no GPU needed).  "Reference" mode reproduces
+ * tests/benchmark_serving_trace.py bit for bit; "mi355x" mode is re-tuned for 256 CUs.
+ * ------------------------------------------------------------------------------- */
+
+typedef enum pkv_policy { PKV_POLICY_REFERENCE = 0, PKV_POLICY_MI355X = 1 } pkv_policy;
+
+typedef enum pkv_route {
+  PKV_ROUTE_FLASHINFER = 0,   /* the reference's fallback route (not provided here) */
+  PKV_ROUTE_BUCKET = 1,       /* length-bucket split grid (paged_attention_indexed) */
+  PKV_ROUTE_WORKQUEUE = 2     /* compact work queue (paged_attention_workqueue) */
+} pkv_route;
+
+/* Constants of the roofline cost model (benchmark_serving_trace.py:33-43). */
+typedef struct pkv_cost_model {
+  int32_t num_q_heads;        /* HQ */
+  int32_t num_kv_heads;       /* HKV */
+  int32_t head_dim;           /* DIM */
+  int32_t compute_units;      /* SM_COUNT */
+  double read_gbps;           /* ROOFLINE_READ_GBPS */
+  double launch_overhead_us;  /* LAUNCH_OVERHEAD_US */
+  double min_ctas_per_cu;     /* MIN_CTAS_PER_SM */
+  int32_t supported_group;    /* SUPPORTED_PERSISTENTKV_GQA; 0 accepts every G */
+  int32_t min_long_context;   /* 16384 in the reference's adaptive gate (:457) */
+  int32_t policy;             /* pkv_policy used for the split choices */
+} pkv_cost_model;
+
+/* Fills *model with the reference constants (RTX 3060) or the MI355X constants. */
+void pkv_cost_model_preset(int32_t policy, pkv_cost_model* model);
+
+/* choose_workqueue_row_splits, benchmark_serving_trace.py:370-393. */
+int32_t pkv_choose_workqueue_row_splits(
+    int32_t length, int32_t active_count, int32_t requested_splits,
+    int32_t auto_splits, int32_t num_kv_heads, int32_t policy);
+
+/* choose_splits, benchmark_serving_trace.py:328-367. */
+int32_t pkv_choose_splits(
+    const int32_t* lengths, int32_t count, int32_t requested_splits,
+    int32_t auto_splits, int32_t single_bucket, int32_t num_kv_heads, int32_t policy);
+
+/* model_bucket_splits / model_workqueue_splits, benchmark_serving_trace.py:396-415. */
+int32_t pkv_model_bucket_splits(
+    const int32_t* lengths, int32_t count, int32_t num_kv_heads, int32_t policy);
+int32_t pkv_model_workqueue_splits(
+    const int32_t* lengths, int32_t count, int32_t num_kv_heads, int32_t policy);
+
+/* estimate_route_ms, benchmark_serving_trace.py:418-442.  `lengths` are the active
+ * rows' current lengths. */
+double pkv_estimate_route_ms(
+    const int32_t* lengths, int32_t count, int32_t route, int32_t splits,
+    const pkv_cost_model* model);
+
+/* choose_adaptive_route_cost_model, benchmark_serving_trace.py:445-488.  Returns the
+ * chosen pkv_route and writes its split count and estimate. */
+int32_t pkv_choose_adaptive_route(
+    const int32_t* lengths, int32_t count, const pkv_cost_model* model,
+    int32_t* out_splits, double* out_estimated_ms);
+
+/* Sizes the compact work queue for one decode step without building it. */
+int pkv_workqueue_size(
+    const int32_t* lengths, int32_t count, int32_t requested_splits,
+    int32_t auto_splits, int32_t num_kv_heads, int32_t policy,
+    int32_t* out_num_tasks, int32_t* out_total_partial_slots);
+
+/* Builds one decode step's work-queue metadata, bit-exact with the work-queue branch of
+ * compile_persistentkv_metadata (benchmark_serving_trace.py:668-729).
+ *   lengths[count], request_ids[count]: the active rows in step order.
+ *   page_indptr[count+1], page_ids[]: each active row's reserved physical pages (CSR).
+ * Outputs (host buffers):
+ *   block_table[count * table_cols]: row r = its first ceil(max_len/page_size) pages,
+ *     padded with its last reserved page; *out_table_cols receives the width.
+ *   seq_lens[count], q_indices[count] (= request_ids), out_indices[count] (= r),
+ *   work_items[5 * work_capacity], split_offsets[count + 1].
+ * Returns PKV_ERR_CAPACITY (with the needed sizes written) when a buffer is too small. */
+int pkv_build_workqueue(
+    const int32_t* lengths, const int32_t* request_ids, int32_t count,
+    const int32_t* page_indptr, const int32_t* page_ids,
+    int32_t page_size, int32_t requested_splits, int32_t auto_splits,
+    int32_t num_kv_heads, int32_t policy,
+    int32_t* block_table, int32_t table_capacity, int32_t* out_table_cols,
+    int32_t* seq_lens, int32_t* q_indices, int32_t* out_indices,
+    int32_t* work_items, int32_t work_capacity, int32_t* out_num_tasks,
+    int32_t* split_offsets, int32_t* out_total_partial_slots);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* PKV_H_ */

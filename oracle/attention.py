@@ -1,0 +1,150 @@
+"""Reference outputs for paged decode attention (CPU; test infrastructure only).
+
+The reference defines correctness as "gather the row's pages, repack them to contiguous
+K/V, run fp32 scaled-dot-product attention with GQA" (tests/benchmark_torch_paged_sdpa.py
+:90-103 for the HND page layout, tests/benchmark_native_paged_baselines.py:83-94 and
+:268-287 for the SDPA call).  This module restates that, plus an fp64 brute force and
+the split-K partial states / log-sum-exp merge of kernels/persistentkv_attention.cuh.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+HEAD_DIM = 128
+TILE = 32                       # kernels/persistentkv_attention.cuh:28
+SCALE = 1.0 / math.sqrt(HEAD_DIM)  # cuh:944
+NEG_FLT_MAX = -np.finfo(np.float32).max
+
+
+def _cpu(t):
+    return t.detach().cpu() if isinstance(t, torch.Tensor) else torch.as_tensor(t)
+
+
+def gather_row(k_pages, v_pages, table_row, length):
+    """Contiguous ``[Hkv, length, 128]`` K and V of one row.
+
+    Follows benchmark_torch_paged_sdpa.py:90-103: ``index_select`` over the page axis of
+    the ``[pages, Hkv, page_size, 128]`` pool, permute to ``[Hkv, pages, page_size, 128]``,
+    flatten the tokens and trim to the row length.
+    """
+    k_pages, v_pages = _cpu(k_pages), _cpu(v_pages)
+    hkv, ps = k_pages.shape[1], k_pages.shape[2]
+    n_pages = -(-int(length) // ps)
+    idx = _cpu(table_row)[:n_pages].long()
+    k = k_pages.index_select(0, idx).permute(1, 0, 2, 3).reshape(hkv, n_pages * ps, HEAD_DIM)
+    v = v_pages.index_select(0, idx).permute(1, 0, 2, 3).reshape(hkv, n_pages * ps, HEAD_DIM)
+    return k[:, :length], v[:, :length]
+
+
+def sdpa_row(q_row, k, v):
+    """fp32 SDPA with ``enable_gqa`` for one query row: q ``[Hq,128]``, k/v ``[Hkv,L,128]``.
+
+    benchmark_native_paged_baselines.py:83-94 (query head h reads KV head h // G).
+    """
+    qf = _cpu(q_row).float().unsqueeze(0).unsqueeze(2)
+    kf = _cpu(k).float().unsqueeze(0)
+    vf = _cpu(v).float().unsqueeze(0)
+    out = F.scaled_dot_product_attention(qf, kf, vf, is_causal=False, enable_gqa=True)
+    return out.squeeze(0).squeeze(1)
+
+
+def paged_decode(q, k_pages, v_pages, block_table, seq_lens, q_indices=None,
+                 out_indices=None, out_rows=None):
+    """Reference result of the four ops as float32 ``[out_rows, Hq, 128]``.
+
+    Row ``b`` reads query row ``q_indices[b]`` (default ``b``), attends to its first
+    ``seq_lens[b]`` tokens and writes output row ``out_indices[b]`` (default ``b``).
+    Rows that no ``b`` writes stay NaN; zero-length rows are 0 (the merge's L == 0 rule,
+    cuh:749-750).
+    """
+    q = _cpu(q)
+    block_table = _cpu(block_table)
+    seq_lens = [int(x) for x in _cpu(seq_lens).tolist()]
+    batch = len(seq_lens)
+    q_idx = list(range(batch)) if q_indices is None else [int(x) for x in _cpu(q_indices).tolist()]
+    o_idx = list(range(batch)) if out_indices is None else [int(x) for x in _cpu(out_indices).tolist()]
+    rows = batch if out_rows is None else out_rows
+    hq = q.shape[1]
+    out = torch.full((rows, hq, HEAD_DIM), float("nan"), dtype=torch.float32)
+    for b in range(batch):
+        if seq_lens[b] <= 0:
+            out[o_idx[b]] = 0.0
+            continue
+        k, v = gather_row(k_pages, v_pages, block_table[b], seq_lens[b])
+        out[o_idx[b]] = sdpa_row(q[q_idx[b]], k, v)
+    return out
+
+
+def attention_fp64(q_row, k, v):
+    """Textbook softmax attention in float64: q ``[Hq,128]``, k/v ``[Hkv,L,128]``."""
+    q = np.asarray(_cpu(q_row).double().numpy())
+    k = np.asarray(_cpu(k).double().numpy())
+    v = np.asarray(_cpu(v).double().numpy())
+    hq, hkv = q.shape[0], k.shape[0]
+    g = hq // hkv
+    out = np.zeros((hq, HEAD_DIM))
+    for h in range(hq):
+        s = k[h // g] @ q[h] * SCALE
+        s = s - s.max()
+        p = np.exp(s)
+        out[h] = (p @ v[h // g]) / p.sum()
+    return out
+
+
+def split_bounds(total_tiles, num_splits):
+    """Row-local split ranges in 32-token tiles, cuh:330-337."""
+    return [((total_tiles * s) // num_splits, (total_tiles * (s + 1)) // num_splits)
+            for s in range(num_splits)]
+
+
+def split_partials(q_row, k, v, ranges):
+    """Partial states ``(m, l, acc)`` of each tile range, float64.
+
+    ``m`` is the max of ``score * scale`` over the range (natural-log units), ``l`` is
+    ``sum exp(s - m)`` and ``acc`` is ``sum exp(s - m) v``; an empty range gives the
+    neutral state ``(-FLT_MAX, 0, 0)`` (cuh:340-363, :615-632).  Shapes ``[Hq, S]``,
+    ``[Hq, S]``, ``[Hq, S, 128]``.
+    """
+    q = np.asarray(_cpu(q_row).double().numpy())
+    k = np.asarray(_cpu(k).double().numpy())
+    v = np.asarray(_cpu(v).double().numpy())
+    hq, hkv, length = q.shape[0], k.shape[0], k.shape[1]
+    g = hq // hkv
+    n = len(ranges)
+    m = np.full((hq, n), float(NEG_FLT_MAX))
+    l = np.zeros((hq, n))
+    acc = np.zeros((hq, n, HEAD_DIM))
+    for h in range(hq):
+        s_all = k[h // g] @ q[h] * SCALE
+        for i, (tb, te) in enumerate(ranges):
+            lo, hi = tb * TILE, min(te * TILE, length)
+            if hi <= lo:
+                continue
+            s = s_all[lo:hi]
+            m[h, i] = s.max()
+            p = np.exp(s - m[h, i])
+            l[h, i] = p.sum()
+            acc[h, i] = p @ v[h // g, lo:hi]
+    return m, l, acc
+
+
+def lse_merge(m, l, acc):
+    """Log-sum-exp merge over the last split axis (cuh:719-751); 0 where L == 0."""
+    big_m = m.max(axis=-1, keepdims=True)
+    w = np.exp(m - big_m)
+    big_l = (w * l).sum(axis=-1)
+    a = (w[..., None] * acc).sum(axis=-2)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        out = np.where(big_l[..., None] > 0, a / big_l[..., None], 0.0)
+    return out
+
+
+def canonical_block_table(context, page_size=16):
+    """``(405 * p + 17) mod (2 * pages)`` (benchmark_native_paged_baselines.py:38-42)."""
+    logical = context // page_size
+    physical = logical * 2
+    return [(405 * p + 17) % physical for p in range(logical)]

@@ -1,0 +1,1105 @@
+// pkv_decode.hip — paged GQA decode attention for MI355X (gfx950, CDNA4).
+//
+// One workgroup (4 wave64s) owns one unit of work: a (row, kv head) pair and a range
+// of 32-token tiles.  The unit is a whole row (direct op), one sequence split of a row
+// (grid-split ops) or one compact work item (work-queue op).  The four waves stream
+// disjoint sub-ranges of the unit's tiles, so one K/V fetch from HBM serves all G query
+// heads of the KV group, then combine their online-softmax states through LDS.
+//
+// Per wave and 32-token tile:
+//   * K and V rows are read straight into VGPRs in MFMA operand layout with 16-byte
+//     buffer loads.  Each 16-token block of a page gets its own buffer descriptor whose
+//     size covers only the block's valid rows, so rows at or past seq_len read as zero
+//     and no access can leave the page.
+//   * S^T[token, head] = K * Q^T with v_mfma_f32_16x16x32 (heads padded to 16 per block).
+//   * Online softmax in base 2 (v_exp_f32); the running max is wave-uniform per head.
+//   * O[head, dim] += P * V with the same MFMA; V is transposed in registers by byte
+//     permutes so that each lane holds 8 tokens of one dim (the MFMA k operand).
+// Partial states keep the reference's workspace format: m in natural-log units of the
+// scaled score, l = sum exp(s - m), acc = sum exp(s - m) v.
+//
+// Reference: kernels/persistentkv_attention.cuh (decode kernel :270-717, merges
+// :719-784, launches :929-1261), tests/persistentkv_torch_extension.cu (op checks).
+
+#include <hip/hip_runtime.h>
+
+#include <float.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "pkv.h"
+
+namespace pkv {
+
+constexpr int kD = 128;              // head dim (cuh:26)
+constexpr int kTile = 32;            // work-item tile in tokens (cuh:28)
+constexpr int kWaves = 4;            // waves per workgroup
+constexpr int kThreads = 64 * kWaves;
+constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit data format (gfx9 family)
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+// softmax scale 1/sqrt(128) (cuh:944) folded with log2(e) for exp2-based softmax.
+constexpr float kScaleLog2 = 0.08838834764831845f * 1.4426950408889634f;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+enum Mode : int { kDirect = 0, kSplit = 1, kQueue = 2 };
+
+// ---------------------------------------------------------------------------------
+// Element types.  P (softmax weights) enters the PV product in the KV dtype; bf16 keeps
+// 8 mantissa bits, so its P is split into hi + lo terms (two MFMAs) to stay well inside
+// the 2e-3 tolerance.
+// ---------------------------------------------------------------------------------
+struct Half {
+  static constexpr int kPasses = 1;
+  __device__ static inline f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  __device__ static inline uint32_t bits(float x) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
+  }
+  __device__ static inline float value(uint32_t b) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)b);
+  }
+};
+
+struct BFloat {
+  static constexpr int kPasses = 2;
+  __device__ static inline f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  __device__ static inline uint32_t bits(float x) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x);
+  }
+  __device__ static inline float value(uint32_t b) {
+    return (float)__builtin_bit_cast(__bf16, (uint16_t)b);
+  }
+};
+
+struct DecodeArgs {
+  const uint8_t* q;           // [q_rows, Hq, 128]
+  const uint8_t* k_pages;     // [num_pages, Hkv, ps, 128]
+  const uint8_t* v_pages;
+  const int32_t* block_table; // [B, max_pages]
+  const int32_t* seq_lens;    // [B] or null: every row has `context` tokens
+  const int32_t* q_indices;   // [B] or null
+  const int32_t* out_indices; // [B] or null
+  const int32_t* work_items;  // [num_tasks, 5] (queue mode)
+  const int32_t* split_offsets;  // [B + 1] (queue mode)
+  int32_t* merge_counters;    // [B, Hkv] or null (queue mode, fused merge)
+  uint8_t* out;               // [out_rows, Hq, 128] (direct mode, fused merge)
+  float* part_m;              // workspace partition (split / queue modes)
+  float* part_l;
+  float* part_acc;
+  int32_t batch, hq, hkv, group;
+  int32_t q_rows, out_rows;
+  int32_t context;            // tokens per row when seq_lens is null
+  int32_t page_size, page_shift;  // page_shift = log2(page_size) or -1
+  int32_t max_pages, num_pages;
+  int32_t num_splits;         // split mode
+  int32_t num_tasks, total_slots;  // queue mode
+};
+
+// ---------------------------------------------------------------------------------
+// Small device helpers.
+// ---------------------------------------------------------------------------------
+__device__ inline int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+__device__ inline int row_length(const DecodeArgs& a, int row) {
+  int len = a.seq_lens ? a.seq_lens[row] : a.context;
+  // The reference trusts seq_lens (cuh:217-219); clamping to the table width keeps
+  // every page lookup inside the row for any input.
+  const long cap = (long)a.max_pages * a.page_size;
+  if (len > cap) len = (int)cap;
+  return len < 0 ? 0 : len;
+}
+
+__device__ inline int clamp_page(const DecodeArgs& a, int page) {
+  // Out-of-range table entries are clamped into the pool (the reference reads
+  // whatever the entry addresses); valid tables are unaffected.
+  return (unsigned)page < (unsigned)a.num_pages ? page : (page < 0 ? 0 : a.num_pages - 1);
+}
+
+__device__ inline void page_of(const DecodeArgs& a, int token, int& logical, int& offset) {
+  if (a.page_shift >= 0) {
+    logical = token >> a.page_shift;
+    offset = token & (a.page_size - 1);
+  } else {
+    logical = token / a.page_size;
+    offset = token - logical * a.page_size;
+  }
+}
+
+// Token held by V-operand slot j (0..7) of lane group g within a 32-token tile.  It
+// matches the token order of the score fragments: slots 0-3 are S^T rows 4g..4g+3 of
+// the first 16-token block, slots 4-7 the same rows of the second block.
+__device__ inline int v_slot_token(int g, int j) { return (j >> 2) * 16 + 4 * g + (j & 3); }
+
+// ---------------------------------------------------------------------------------
+// Page loaders.  FastPager handles page sizes that are multiples of 16: a 16-token
+// block then lies inside one page, so its page id is wave-uniform (scalar load) and a
+// per-block buffer descriptor bounds every lane's access.  GenericPager handles any
+// other page size with per-lane table lookups and predicated loads.
+// ---------------------------------------------------------------------------------
+struct FastPager {
+  struct Tile {
+    __amdgpu_buffer_rsrc_t k[2];
+    __amdgpu_buffer_rsrc_t v[2];
+  };
+  const DecodeArgs& a;
+  const int32_t* trow;
+  int len;
+  long head_bytes;   // kvh * ps * 256
+  long page_bytes;   // Hkv * ps * 256
+  uint32_t koff[4];  // per-lane byte offsets inside a block, K (per 32-dim step)
+  uint32_t voff[8];  // per-lane byte offsets inside a block, V (per token slot)
+
+  __device__ FastPager(const DecodeArgs& args, int row, int kvh, int length, int lane)
+      : a(args), len(length) {
+    trow = a.block_table + (long)row * a.max_pages;
+    head_bytes = (long)kvh * a.page_size * (kD * 2);
+    page_bytes = (long)a.hkv * a.page_size * (kD * 2);
+    const int c = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) koff[kk] = c * 256 + kk * 64 + g * 16;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) voff[j] = (4 * g + (j & 3)) * 256 + c * 16;
+  }
+
+  __device__ inline void prepare(int tile, Tile& t) const {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int tok0 = tile * kTile + b * 16;
+      int nvalid = len - tok0;
+      nvalid = nvalid < 0 ? 0 : (nvalid > 16 ? 16 : nvalid);
+      long off = 0;
+      if (nvalid > 0) {
+        int logical, in_page;
+        page_of(a, tok0, logical, in_page);
+        const int page = clamp_page(a, uniform(trow[logical]));
+        off = (long)page * page_bytes + head_bytes + (long)in_page * (kD * 2);
+      }
+      t.k[b] = __builtin_amdgcn_make_buffer_rsrc((void*)(a.k_pages + off), (short)0,
+                                                 nvalid * (kD * 2), kRsrcWord3);
+      t.v[b] = __builtin_amdgcn_make_buffer_rsrc((void*)(a.v_pages + off), (short)0,
+                                                 nvalid * (kD * 2), kRsrcWord3);
+    }
+  }
+  __device__ inline u32x4 load_k(const Tile& t, int b, int kk) const {
+    return __builtin_amdgcn_raw_buffer_load_b128(t.k[b], koff[kk], 0, 0);
+  }
+  __device__ inline u32x4 load_v(const Tile& t, int j) const {
+    return __builtin_amdgcn_raw_buffer_load_b128(t.v[j >> 2], voff[j], 0, 0);
+  }
+};
+
+struct GenericPager {
+  struct Tile {
+    long k[2];  // byte offset of this lane's K chunk per block, or -1
+    long v[8];  // byte offset of this lane's V chunk per slot, or -1
+  };
+  const DecodeArgs& a;
+  const int32_t* trow;
+  int len;
+  long head_bytes, page_bytes;
+  int c, g;
+
+  __device__ GenericPager(const DecodeArgs& args, int row, int kvh, int length, int lane)
+      : a(args), len(length) {
+    trow = a.block_table + (long)row * a.max_pages;
+    head_bytes = (long)kvh * a.page_size * (kD * 2);
+    page_bytes = (long)a.hkv * a.page_size * (kD * 2);
+    c = lane & 15;
+    g = lane >> 4;
+  }
+  __device__ inline long row_offset(int token) const {
+    if (token >= len) return -1;
+    int logical, in_page;
+    page_of(a, token, logical, in_page);
+    const int page = clamp_page(a, trow[logical]);
+    return (long)page * page_bytes + head_bytes + (long)in_page * (kD * 2);
+  }
+  __device__ inline void prepare(int tile, Tile& t) const {
+    const int tok0 = tile * kTile;
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const long o = row_offset(tok0 + b * 16 + c);
+      t.k[b] = o < 0 ? -1 : o + g * 16;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const long o = row_offset(tok0 + v_slot_token(g, j));
+      t.v[j] = o < 0 ? -1 : o + c * 16;
+    }
+  }
+  __device__ inline u32x4 load_k(const Tile& t, int b, int kk) const {
+    u32x4 z = {0u, 0u, 0u, 0u};
+    return t.k[b] < 0 ? z : *(const u32x4*)(a.k_pages + t.k[b] + kk * 64);
+  }
+  __device__ inline u32x4 load_v(const Tile& t, int j) const {
+    u32x4 z = {0u, 0u, 0u, 0u};
+    return t.v[j] < 0 ? z : *(const u32x4*)(a.v_pages + t.v[j]);
+  }
+};
+
+// ---------------------------------------------------------------------------------
+// Per-wave streaming state and tile step.
+// ---------------------------------------------------------------------------------
+template <int HB>
+struct WaveState {
+  f32x4 o[HB][8];  // o[hb][jj][i] = O[head hb*16 + 4g + i][dim 8c + jj]
+  float m[HB];     // running max (log2 units) of head hb*16 + c
+  float l[HB];     // lane-partial running sum of exp2(x - m)
+};
+
+struct TileRegs {
+  u32x4 k[2][4];
+  u32x4 v[8];
+};
+
+template <class Pager>
+__device__ inline void issue_tile(const Pager& pg, int tile, TileRegs& r) {
+  typename Pager::Tile t;
+  pg.prepare(tile, t);
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) r.k[b][kk] = pg.load_k(t, b, kk);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r.v[j] = pg.load_v(t, j);
+}
+
+template <class Elem, int HB>
+__device__ inline void compute_tile(WaveState<HB>& st, const TileRegs& r,
+                                    const u32x4 (&qf)[HB][4], int tile, int len, int lane) {
+  const int g = lane >> 4;
+  // V transpose: vt[jj] holds, for dim 8c + jj, the 8 tokens of this lane's slots.
+  u32x4 vt[8];
+#pragma unroll
+  for (int jj = 0; jj < 8; ++jj) {
+    const int w = jj >> 1;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t lo = r.v[2 * q][w], hi = r.v[2 * q + 1][w];
+      vt[jj][q] = (jj & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+    }
+  }
+  const int tok_base = tile * kTile + 4 * g;
+#pragma unroll
+  for (int hb = 0; hb < HB; ++hb) {
+    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      s0 = Elem::mma(r.k[0][kk], qf[hb][kk], s0);
+      s1 = Elem::mma(r.k[1][kk], qf[hb][kk], s1);
+    }
+    float x[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[i] = (tok_base + i < len) ? s0[i] * kScaleLog2 : -INFINITY;
+      x[4 + i] = (tok_base + 16 + i < len) ? s1[i] * kScaleLog2 : -INFINITY;
+    }
+    float mx = x[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) mx = fmaxf(mx, x[j]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(st.m[hb], mx);
+    const float corr = __builtin_amdgcn_exp2f(st.m[hb] - m_new);
+    st.m[hb] = m_new;
+    float p[8], psum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      p[j] = __builtin_amdgcn_exp2f(x[j] - m_new);
+      psum += p[j];
+    }
+    st.l[hb] = st.l[hb] * corr + psum;
+    // Rescale O rows (heads hb*16 + 4g + i); lane 4g + i holds that head's factor.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float ci = __shfl(corr, 4 * g + i);
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) st.o[hb][jj][i] *= ci;
+    }
+#pragma unroll
+    for (int pass = 0; pass < Elem::kPasses; ++pass) {
+      u32x4 pa;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float a0 = p[2 * q], a1 = p[2 * q + 1];
+        if (pass == 1) {  // residual of the first rounding
+          a0 -= Elem::value(Elem::bits(a0));
+          a1 -= Elem::value(Elem::bits(a1));
+        }
+        pa[q] = Elem::bits(a0) | (Elem::bits(a1) << 16);
+      }
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) st.o[hb][jj] = Elem::mma(pa, vt[jj], st.o[hb][jj]);
+    }
+  }
+}
+
+// Streams tiles [t0, t1) of one (row, kv head) into the wave state, two tiles in flight.
+template <class Elem, int HB, class Pager>
+__device__ inline void stream_range(WaveState<HB>& st, const Pager& pg, const u32x4 (&qf)[HB][4],
+                                    int t0, int t1, int len, int lane) {
+  if (t0 >= t1) return;
+  TileRegs ra, rb;
+  issue_tile(pg, t0, ra);
+  int t = t0;
+  while (true) {
+    if (t + 1 < t1) issue_tile(pg, t + 1, rb);
+    compute_tile<Elem, HB>(st, ra, qf, t, len, lane);
+    if (++t >= t1) break;
+    if (t + 1 < t1) issue_tile(pg, t + 1, ra);
+    compute_tile<Elem, HB>(st, rb, qf, t, len, lane);
+    if (++t >= t1) break;
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Work-unit resolution.
+// ---------------------------------------------------------------------------------
+struct Unit {
+  int row, kvh, split, tb, te, len, slot_base;  // slot_base: queue-mode slot of split 0
+  bool valid;
+};
+
+__device__ inline int ceil_tiles(int len) { return (len + kTile - 1) / kTile; }
+
+template <int MODE>
+__device__ inline Unit resolve_unit(const DecodeArgs& a) {
+  Unit u;
+  u.valid = true;
+  u.slot_base = 0;
+  const int idx = blockIdx.x;
+  if (MODE == kDirect) {
+    u.row = idx / a.hkv;
+    u.kvh = idx - u.row * a.hkv;
+    u.split = 0;
+    u.len = row_length(a, u.row);
+    u.tb = 0;
+    u.te = ceil_tiles(u.len);
+  } else if (MODE == kSplit) {
+    const int per_row = a.hkv * a.num_splits;
+    u.row = idx / per_row;
+    const int rem = idx - u.row * per_row;
+    u.kvh = rem / a.num_splits;
+    u.split = rem - u.kvh * a.num_splits;
+    u.len = row_length(a, u.row);
+    const int total = ceil_tiles(u.len);
+    // Row-local split bounds, cuh:330-337.
+    u.tb = (int)(((long)total * u.split) / a.num_splits);
+    u.te = (int)(((long)total * (u.split + 1)) / a.num_splits);
+  } else {
+    const int32_t* w = a.work_items + (long)idx * 5;
+    u.row = uniform(w[0]);
+    u.kvh = uniform(w[1]);
+    u.split = uniform(w[2]);
+    u.tb = uniform(w[3]);
+    u.te = uniform(w[4]);
+    // Malformed items are skipped instead of addressing outside the buffers.
+    if (u.row < 0 || u.row >= a.batch || u.kvh < 0 || u.kvh >= a.hkv || u.split < 0) {
+      u.valid = false;
+      return u;
+    }
+    u.len = row_length(a, u.row);
+    u.slot_base = uniform(a.split_offsets[u.row]);
+    const int row_splits = uniform(a.split_offsets[u.row + 1]) - u.slot_base;
+    const int total = ceil_tiles(u.len);
+    if (u.split >= row_splits) u.valid = false;
+    if (u.tb < 0) u.tb = 0;
+    if (u.te > total) u.te = total;
+    if (u.slot_base < 0 || u.slot_base + u.split >= a.total_slots) u.valid = false;
+  }
+  return u;
+}
+
+// Neutral partial state of an empty split (cuh:340-363): m = -FLT_MAX, l = 0, acc = 0.
+__device__ inline void write_neutral(const DecodeArgs& a, long state0, long state_stride,
+                                     int G, int tid) {
+  for (int idx = tid; idx < G * (kD / 4); idx += kThreads) {
+    const int h = idx / (kD / 4), d = (idx % (kD / 4)) * 4;
+    const long s = state0 + (long)h * state_stride;
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    *(f32x4*)(a.part_acc + s * kD + d) = z;
+    if (d == 0) {
+      a.part_m[s] = -FLT_MAX;
+      a.part_l[s] = 0.f;
+    }
+  }
+}
+
+template <class Elem>
+__device__ inline void store_out4(uint8_t* out, long elem, f32x4 v) {
+  u32x2 w;
+  w[0] = Elem::bits(v[0]) | (Elem::bits(v[1]) << 16);
+  w[1] = Elem::bits(v[2]) | (Elem::bits(v[3]) << 16);
+  *(u32x2*)(out + elem * 2) = w;
+}
+
+// Last-arriver merge of one (row, kv head) group's partial states (fused merge,
+// cuh:648-716).  Slots of empty splits are skipped by recomputing the builder's split
+// bounds, so rows with more splits than tiles are merged correctly.
+template <class Elem>
+__device__ void fused_merge_group(const DecodeArgs& a, const Unit& u, int qh0, int G, int tid) {
+  const int s_begin = a.split_offsets[u.row];
+  const int s_end = a.split_offsets[u.row + 1];
+  const int nsplit = s_end - s_begin;
+  const int total = ceil_tiles(u.len);
+  const int out_row = a.out_indices ? a.out_indices[u.row] : u.row;
+  if (out_row < 0 || out_row >= a.out_rows) return;
+  if (s_begin < 0 || s_end > a.total_slots || nsplit <= 0) return;  // malformed offsets
+  for (int idx = tid; idx < G * (kD / 4); idx += kThreads) {
+    const int h = idx / (kD / 4), d = (idx % (kD / 4)) * 4;
+    const int qh = qh0 + h;
+    float M = -FLT_MAX;
+    for (int s = 0; s < nsplit; ++s) {
+      if ((long)total * s / nsplit == (long)total * (s + 1) / nsplit) continue;
+      const long st = (long)(s_begin + s) * a.hq + qh;
+      M = fmaxf(M, __hip_atomic_load(a.part_m + st, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    }
+    float L = 0.f;
+    f32x4 A = {0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < nsplit; ++s) {
+      if ((long)total * s / nsplit == (long)total * (s + 1) / nsplit) continue;
+      const long st = (long)(s_begin + s) * a.hq + qh;
+      const float ms = __hip_atomic_load(a.part_m + st, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const float ls = __hip_atomic_load(a.part_l + st, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const float w = __builtin_amdgcn_exp2f((ms - M) * kLog2e);
+      L += w * ls;
+      const f32x4 acc = *(const f32x4*)(a.part_acc + st * kD + d);
+      A += w * acc;
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    store_out4<Elem>(a.out, ((long)out_row * a.hq + qh) * kD + d, A * inv);
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// The decode kernel.
+// ---------------------------------------------------------------------------------
+// G <= 16 (one head block) keeps two waves per SIMD (<= 256 registers each); G <= 32
+// doubles the accumulators and runs one wave per SIMD with the AGPR file available.
+template <class Elem, int HB, bool FAST, int MODE>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(HB == 1 ? 2 : 1)))
+void decode_kernel(DecodeArgs a) {
+  extern __shared__ float lds[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = uniform(tid >> 6);
+  const int c = lane & 15, g = lane >> 4;
+  const int G = a.group;
+
+  const Unit u = resolve_unit<MODE>(a);
+  if (!u.valid) return;
+  const int qh0 = u.kvh * G;
+
+  // Partial-state addressing: state index of head h is state0 + h * state_stride.
+  long state0 = 0, state_stride = 1;
+  if (MODE == kSplit) {
+    state0 = ((long)u.row * a.hq + qh0) * a.num_splits + u.split;
+    state_stride = a.num_splits;
+  } else if (MODE == kQueue) {
+    state0 = (long)(u.slot_base + u.split) * a.hq + qh0;
+    state_stride = 1;
+  }
+
+  if (MODE != kDirect && u.tb >= u.te) {
+    write_neutral(a, state0, state_stride, G, tid);
+    return;
+  }
+
+  // Q^T operand: lane (g, c) holds head hb*16 + c, dims 32kk + 8g .. +8.
+  int q_row = a.q_indices ? a.q_indices[u.row] : u.row;
+  q_row = q_row < 0 ? 0 : (q_row >= a.q_rows ? a.q_rows - 1 : q_row);
+  u32x4 qf[HB][4];
+#pragma unroll
+  for (int hb = 0; hb < HB; ++hb) {
+    const int h = hb * 16 + c;
+    const uint8_t* qp = a.q + (((long)q_row * a.hq + qh0 + h) * kD + 8 * g) * 2;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      qf[hb][kk] = h < G ? *(const u32x4*)(qp + kk * 64) : z;
+    }
+  }
+
+  WaveState<HB> st;
+#pragma unroll
+  for (int hb = 0; hb < HB; ++hb) {
+    st.m[hb] = -FLT_MAX;
+    st.l[hb] = 0.f;
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) st.o[hb][jj] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // Contiguous sub-range of the unit's tiles for this wave.
+  const int n = u.te - u.tb;
+  const int w0 = u.tb + (n * wave) / kWaves;
+  const int w1 = u.tb + (n * (wave + 1)) / kWaves;
+  if (FAST) {
+    FastPager pg(a, u.row, u.kvh, u.len, lane);
+    stream_range<Elem, HB>(st, pg, qf, w0, w1, u.len, lane);
+  } else {
+    GenericPager pg(a, u.row, u.kvh, u.len, lane);
+    stream_range<Elem, HB>(st, pg, qf, w0, w1, u.len, lane);
+  }
+#pragma unroll
+  for (int hb = 0; hb < HB; ++hb) {
+    st.l[hb] += __shfl_xor(st.l[hb], 16);
+    st.l[hb] += __shfl_xor(st.l[hb], 32);
+  }
+
+  // Combine the four waves, one 16-head block at a time.
+  // LDS: m[w][32], l[w][32], o[w][16][128] (33 KB for any G).
+  float* sm_m = lds;
+  float* sm_l = lds + kWaves * 32;
+  float* sm_o = lds + 2 * kWaves * 32;
+  if (g == 0) {
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) {
+      const int h = hb * 16 + c;
+      if (h < G) {
+        sm_m[wave * 32 + h] = st.m[hb];
+        sm_l[wave * 32 + h] = st.l[hb];
+      }
+    }
+  }
+  int out_row = 0;
+  if (MODE == kDirect) out_row = a.out_indices ? a.out_indices[u.row] : u.row;
+#pragma unroll
+  for (int hb = 0; hb < HB; ++hb) {
+    const int h0 = hb * 16;
+    const int nh = G - h0 < 16 ? G - h0 : 16;
+    if (hb > 0) __syncthreads();  // the previous block's readers are done with sm_o
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int hh = 4 * g + i;
+      if (hh < nh) {
+        float* dst = sm_o + ((long)wave * 16 + hh) * kD + 8 * c;
+        *(f32x4*)dst = f32x4{st.o[hb][0][i], st.o[hb][1][i], st.o[hb][2][i], st.o[hb][3][i]};
+        *(f32x4*)(dst + 4) = f32x4{st.o[hb][4][i], st.o[hb][5][i], st.o[hb][6][i], st.o[hb][7][i]};
+      }
+    }
+    __syncthreads();
+    for (int idx = tid; idx < nh * (kD / 4); idx += kThreads) {
+      const int hh = idx / (kD / 4), d = (idx % (kD / 4)) * 4;
+      const int h = h0 + hh;
+      float M = -FLT_MAX;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w * 32 + h]);
+      float L = 0.f;
+      f32x4 A = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const float e = __builtin_amdgcn_exp2f(sm_m[w * 32 + h] - M);
+        L += e * sm_l[w * 32 + h];
+        A += e * *(const f32x4*)(sm_o + ((long)w * 16 + hh) * kD + d);
+      }
+      if (MODE == kDirect) {
+        if (out_row >= 0 && out_row < a.out_rows) {
+          const float inv = L > 0.f ? 1.f / L : 0.f;
+          store_out4<Elem>(a.out, ((long)out_row * a.hq + qh0 + h) * kD + d, A * inv);
+        }
+      } else {
+        const long s = state0 + (long)h * state_stride;
+        *(f32x4*)(a.part_acc + s * kD + d) = A;
+        if (d == 0) {
+          a.part_m[s] = M * kLn2;
+          a.part_l[s] = L;
+        }
+      }
+    }
+  }
+
+  if (MODE == kQueue && a.merge_counters != nullptr) {
+    __shared__ int last;
+    __syncthreads();
+    if (tid == 0) {
+      const int nsplit = a.split_offsets[u.row + 1] - a.split_offsets[u.row];
+      const int total = ceil_tiles(u.len);
+      const int expected = nsplit < total ? nsplit : total;  // non-empty splits
+      __threadfence();
+      const int old = atomicAdd(a.merge_counters + (long)u.row * a.hkv + u.kvh, 1);
+      last = (old == expected - 1);
+    }
+    __syncthreads();
+    if (last) {
+      __threadfence();
+      fused_merge_group<Elem>(a, u, qh0, G, tid);
+      __syncthreads();
+      if (tid == 0) a.merge_counters[(long)u.row * a.hkv + u.kvh] = 0;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Segmented LSE merge: one wave per (row, query head); lane owns dims 2*lane, 2*lane+1.
+// Grid-split slots are ((row*Hq + qh)*S + s) (cuh:719-751); work-queue slots are
+// (split_offsets[row] + s)*Hq + qh (cuh:753-784), skipping splits the builder leaves
+// empty (the reference reads those slots uninitialised).
+// ---------------------------------------------------------------------------------
+struct MergeArgs {
+  const float* part_m;
+  const float* part_l;
+  const float* part_acc;
+  const int32_t* seq_lens;       // queue mode
+  const int32_t* split_offsets;  // queue mode
+  const int32_t* out_indices;
+  uint8_t* out;
+  int32_t batch, hq, out_rows;
+  int32_t num_splits;            // split mode
+  int32_t total_slots;           // queue mode
+  int32_t context, max_tokens;   // split mode length fallback / clamp
+};
+
+template <class Elem, bool QUEUE>
+__global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
+  const int wave_id = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (wave_id >= a.batch * a.hq) return;
+  const int row = wave_id / a.hq;
+  const int qh = wave_id - row * a.hq;
+  int first, count, total = 0;
+  long stride;
+  if (QUEUE) {
+    int s0 = a.split_offsets[row], s1 = a.split_offsets[row + 1];
+    if (s0 < 0) s0 = 0;
+    if (s1 > a.total_slots) s1 = a.total_slots;
+    first = s0;
+    count = s1 - s0;
+    int len = a.seq_lens[row];
+    if (len > a.max_tokens) len = a.max_tokens;
+    total = ceil_tiles(len < 0 ? 0 : len);
+    stride = a.hq;
+  } else {
+    first = 0;
+    count = a.num_splits;
+    stride = 1;
+  }
+  const long base = QUEUE ? (long)first * a.hq + qh : ((long)row * a.hq + qh) * a.num_splits;
+  const int nsplit = QUEUE ? (a.split_offsets[row + 1] - a.split_offsets[row]) : count;
+  float M = -FLT_MAX;
+  for (int s = 0; s < count; ++s) {
+    if (QUEUE && (long)total * s / nsplit == (long)total * (s + 1) / nsplit) continue;
+    M = fmaxf(M, a.part_m[base + s * stride]);
+  }
+  float L = 0.f;
+  f32x2 A = {0.f, 0.f};
+  for (int s = 0; s < count; ++s) {
+    if (QUEUE && (long)total * s / nsplit == (long)total * (s + 1) / nsplit) continue;
+    const long st = base + s * stride;
+    const float w = __builtin_amdgcn_exp2f((a.part_m[st] - M) * kLog2e);
+    L += w * a.part_l[st];
+    A += w * *(const f32x2*)(a.part_acc + st * kD + 2 * lane);
+  }
+  const int out_row = a.out_indices ? a.out_indices[row] : row;
+  if (out_row < 0 || out_row >= a.out_rows) return;
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  const uint32_t word = Elem::bits(A[0] * inv) | (Elem::bits(A[1] * inv) << 16);
+  *(uint32_t*)(a.out + (((long)out_row * a.hq + qh) * kD + 2 * lane) * 2) = word;
+}
+
+// ---------------------------------------------------------------------------------
+// Host side: validation, dispatch and launch.
+// ---------------------------------------------------------------------------------
+thread_local char g_error[512] = "";
+
+int fail(int status, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+  return status;
+}
+
+int ok() {
+  g_error[0] = '\0';
+  return PKV_OK;
+}
+
+int log2_exact(int x) {
+  if (x <= 0 || (x & (x - 1))) return -1;
+  int s = 0;
+  while ((1 << s) < x) ++s;
+  return s;
+}
+
+size_t lds_bytes(int G) {
+  return (size_t)(2 * kWaves * 32 + kWaves * (G < 16 ? G : 16) * kD) * sizeof(float);
+}
+
+struct Geometry {
+  int batch, hq, hkv, head_dim, num_pages, page_size, max_pages, dtype;
+};
+
+int check_geometry(const Geometry& g, const void* q, const void* k, const void* v,
+                   const void* table, const void* out) {
+  if (g.head_dim != kD)
+    return fail(PKV_ERR_UNSUPPORTED, "PersistentKV extension currently requires d=128");
+  if (g.dtype != PKV_DTYPE_F16 && g.dtype != PKV_DTYPE_BF16)
+    return fail(PKV_ERR_UNSUPPORTED, "dtype must be fp16 or bf16");
+  if (g.hkv <= 0) return fail(PKV_ERR_INVALID_ARGUMENT, "Hkv must be positive");
+  if (g.hq % g.hkv != 0) return fail(PKV_ERR_INVALID_ARGUMENT, "Hq must be divisible by Hkv");
+  const int G = g.hq / g.hkv;
+  if (G < 1 || G > PKV_MAX_GROUP)
+    return fail(PKV_ERR_UNSUPPORTED, "PersistentKV supports G=Hq/Hkv in [1,32]; got G=%d from Hq=%d Hkv=%d",
+                G, g.hq, g.hkv);
+  if (g.page_size <= 0) return fail(PKV_ERR_INVALID_ARGUMENT, "page_size must be positive");
+  if (g.batch < 0) return fail(PKV_ERR_INVALID_ARGUMENT, "batch must be non-negative");
+  if (g.num_pages <= 0) return fail(PKV_ERR_INVALID_ARGUMENT, "k_pages must hold at least one page");
+  if (g.max_pages <= 0) return fail(PKV_ERR_INVALID_ARGUMENT, "block_table must have at least one column");
+  if (g.batch > 0 && (!q || !k || !v || !table || !out))
+    return fail(PKV_ERR_INVALID_ARGUMENT, "a required pointer is null");
+  if ((long)g.hkv * g.page_size * kD * 2 > 0x7fffffffL)
+    return fail(PKV_ERR_UNSUPPORTED, "page too large (Hkv*page_size*256 must fit in 31 bits)");
+  return PKV_OK;
+}
+
+template <class Elem, int HB, bool FAST, int MODE>
+hipError_t launch_decode(const DecodeArgs& a, int grid, hipStream_t stream) {
+  decode_kernel<Elem, HB, FAST, MODE><<<dim3(grid), dim3(kThreads), lds_bytes(a.group), stream>>>(a);
+  return hipGetLastError();
+}
+
+template <int MODE>
+int dispatch_decode(const DecodeArgs& a, int dtype, int grid, hipStream_t stream) {
+  const bool fast = (a.page_size % 16) == 0;
+  const int hb = a.group <= 16 ? 1 : 2;
+  hipError_t e;
+  if (dtype == PKV_DTYPE_F16) {
+    if (hb == 1) e = fast ? launch_decode<Half, 1, true, MODE>(a, grid, stream)
+                          : launch_decode<Half, 1, false, MODE>(a, grid, stream);
+    else e = fast ? launch_decode<Half, 2, true, MODE>(a, grid, stream)
+                  : launch_decode<Half, 2, false, MODE>(a, grid, stream);
+  } else {
+    if (hb == 1) e = fast ? launch_decode<BFloat, 1, true, MODE>(a, grid, stream)
+                          : launch_decode<BFloat, 1, false, MODE>(a, grid, stream);
+    else e = fast ? launch_decode<BFloat, 2, true, MODE>(a, grid, stream)
+                  : launch_decode<BFloat, 2, false, MODE>(a, grid, stream);
+  }
+  if (e != hipSuccess) return fail(PKV_ERR_LAUNCH, "decode launch failed: %s", hipGetErrorString(e));
+  return PKV_OK;
+}
+
+int dispatch_merge(const MergeArgs& m, bool queue, int dtype, hipStream_t stream) {
+  const int waves = m.batch * m.hq;
+  const int grid = (waves + 3) / 4;
+  if (grid == 0) return PKV_OK;
+  if (dtype == PKV_DTYPE_F16) {
+    if (queue) merge_kernel<Half, true><<<grid, 256, 0, stream>>>(m);
+    else merge_kernel<Half, false><<<grid, 256, 0, stream>>>(m);
+  } else {
+    if (queue) merge_kernel<BFloat, true><<<grid, 256, 0, stream>>>(m);
+    else merge_kernel<BFloat, false><<<grid, 256, 0, stream>>>(m);
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(PKV_ERR_LAUNCH, "merge launch failed: %s", hipGetErrorString(e));
+  return PKV_OK;
+}
+
+DecodeArgs base_args(const Geometry& g, const void* q, int q_rows, const void* k, const void* v,
+                     const int32_t* table, void* out, int out_rows) {
+  DecodeArgs a = {};
+  a.q = (const uint8_t*)q;
+  a.k_pages = (const uint8_t*)k;
+  a.v_pages = (const uint8_t*)v;
+  a.block_table = table;
+  a.out = (uint8_t*)out;
+  a.batch = g.batch;
+  a.hq = g.hq;
+  a.hkv = g.hkv;
+  a.group = g.hq / g.hkv;
+  a.q_rows = q_rows;
+  a.out_rows = out_rows;
+  a.page_size = g.page_size;
+  a.page_shift = log2_exact(g.page_size);
+  a.max_pages = g.max_pages;
+  a.num_pages = g.num_pages;
+  return a;
+}
+
+// Shared body of the three grid ops (cuh:929-974 persistentkv_launch).
+int run_grid(const Geometry& g, const void* q, int q_rows, const void* k, const void* v,
+             const int32_t* table, const int32_t* seq_lens, const int32_t* q_idx,
+             const int32_t* out_idx, void* out, int out_rows, void* ws, size_t ws_bytes,
+             int context, int num_splits, void* stream_ptr) {
+  int st = check_geometry(g, q, k, v, table, out);
+  if (st != PKV_OK) return st;
+  if (context <= 0) return fail(PKV_ERR_INVALID_ARGUMENT, "context must be positive");
+  if (num_splits <= 0) return fail(PKV_ERR_INVALID_ARGUMENT, "num_splits must be positive");
+  const int total_tiles = (context + kTile - 1) / kTile;
+  if (num_splits > total_tiles)  // cuh:1042-1043
+    return fail(PKV_ERR_INVALID_ARGUMENT, "num_splits=%d exceeds ceil(context/32)=%d", num_splits,
+                total_tiles);
+  if ((long)g.max_pages * g.page_size < context)  // cuh:1131
+    return fail(PKV_ERR_INVALID_ARGUMENT, "block_table has %d pages of %d tokens, fewer than context=%d",
+                g.max_pages, g.page_size, context);
+  if (q_rows <= 0 && g.batch > 0) return fail(PKV_ERR_INVALID_ARGUMENT, "q has no rows");
+  if (g.batch == 0) return ok();
+  hipStream_t stream = (hipStream_t)stream_ptr;
+  DecodeArgs a = base_args(g, q, q_rows, k, v, table, out, out_rows);
+  a.seq_lens = seq_lens;
+  a.q_indices = q_idx;
+  a.out_indices = out_idx;
+  a.context = context;
+  a.num_splits = num_splits;
+  if (num_splits == 1) {
+    st = dispatch_decode<kDirect>(a, g.dtype, g.batch * g.hkv, stream);
+    return st == PKV_OK ? ok() : st;
+  }
+  const size_t need = pkv_workspace_bytes(g.batch, g.hq, num_splits);
+  if (!ws || ws_bytes < need)
+    return fail(PKV_ERR_WORKSPACE_TOO_SMALL, "split dispatch requires a workspace of %zu bytes (got %zu)",
+                need, ws ? ws_bytes : (size_t)0);
+  const long states = (long)g.batch * g.hq * num_splits;
+  a.part_m = (float*)ws;
+  a.part_l = a.part_m + states;
+  a.part_acc = a.part_l + states;
+  st = dispatch_decode<kSplit>(a, g.dtype, g.batch * g.hkv * num_splits, stream);
+  if (st != PKV_OK) return st;
+  MergeArgs m = {};
+  m.part_m = a.part_m;
+  m.part_l = a.part_l;
+  m.part_acc = a.part_acc;
+  m.out_indices = out_idx;
+  m.out = (uint8_t*)out;
+  m.batch = g.batch;
+  m.hq = g.hq;
+  m.out_rows = out_rows;
+  m.num_splits = num_splits;
+  st = dispatch_merge(m, false, g.dtype, stream);
+  return st == PKV_OK ? ok() : st;
+}
+
+struct QueueCall {
+  Geometry g;
+  const void *q, *k, *v;
+  int q_rows;
+  const int32_t *table, *seq_lens, *items, *offsets, *q_idx, *out_idx;
+  int32_t* counters;
+  void* out;
+  int out_rows;
+  void* ws;
+  size_t ws_bytes;
+  int bucket_context, num_tasks, total_slots;
+};
+
+int check_queue(const QueueCall& c, bool need_out) {
+  int st = check_geometry(c.g, c.q, c.k, c.v, c.table, need_out ? c.out : (const void*)1);
+  if (st != PKV_OK) return st;
+  if (c.bucket_context <= 0) return fail(PKV_ERR_INVALID_ARGUMENT, "bucket_context must be positive");
+  if (c.num_tasks <= 0) return fail(PKV_ERR_INVALID_ARGUMENT, "work_items must not be empty");
+  if (c.total_slots <= 0) return fail(PKV_ERR_INVALID_ARGUMENT, "total_partial_slots must be positive");
+  if (!c.items || !c.offsets || !c.seq_lens)
+    return fail(PKV_ERR_INVALID_ARGUMENT, "work-queue metadata pointer is null");
+  if (c.q_rows <= 0) return fail(PKV_ERR_INVALID_ARGUMENT, "q_source has no rows");
+  const size_t need = pkv_workqueue_workspace_bytes(c.total_slots, c.g.hq);
+  if (!c.ws || c.ws_bytes < need)
+    return fail(PKV_ERR_WORKSPACE_TOO_SMALL, "work-queue dispatch requires a workspace of %zu bytes (got %zu)",
+                need, c.ws ? c.ws_bytes : (size_t)0);
+  return PKV_OK;
+}
+
+DecodeArgs queue_args(const QueueCall& c) {
+  DecodeArgs a = base_args(c.g, c.q, c.q_rows, c.k, c.v, c.table, c.out, c.out_rows);
+  a.seq_lens = c.seq_lens;
+  a.q_indices = c.q_idx;
+  a.out_indices = c.out_idx;
+  a.work_items = c.items;
+  a.split_offsets = c.offsets;
+  a.context = c.bucket_context;
+  a.num_tasks = c.num_tasks;
+  a.total_slots = c.total_slots;
+  const long states = (long)c.total_slots * c.g.hq;
+  a.part_m = (float*)c.ws;
+  a.part_l = a.part_m + states;
+  a.part_acc = a.part_l + states;
+  return a;
+}
+
+MergeArgs queue_merge_args(const DecodeArgs& a) {
+  MergeArgs m = {};
+  m.part_m = a.part_m;
+  m.part_l = a.part_l;
+  m.part_acc = a.part_acc;
+  m.seq_lens = a.seq_lens;
+  m.split_offsets = a.split_offsets;
+  m.out_indices = a.out_indices;
+  m.out = a.out;
+  m.batch = a.batch;
+  m.hq = a.hq;
+  m.out_rows = a.out_rows;
+  m.total_slots = a.total_slots;
+  m.max_tokens = (int)((long)a.max_pages * a.page_size > 0x7fffffffL ? 0x7fffffff
+                                                                     : (long)a.max_pages * a.page_size);
+  return m;
+}
+
+}  // namespace pkv
+
+using namespace pkv;
+
+extern "C" {
+
+const char* pkv_last_error(void) { return g_error; }
+
+const char* pkv_status_string(int status) {
+  switch (status) {
+    case PKV_OK: return "PKV_OK";
+    case PKV_ERR_INVALID_ARGUMENT: return "PKV_ERR_INVALID_ARGUMENT";
+    case PKV_ERR_UNSUPPORTED: return "PKV_ERR_UNSUPPORTED";
+    case PKV_ERR_WORKSPACE_TOO_SMALL: return "PKV_ERR_WORKSPACE_TOO_SMALL";
+    case PKV_ERR_LAUNCH: return "PKV_ERR_LAUNCH";
+    case PKV_ERR_CAPACITY: return "PKV_ERR_CAPACITY";
+    default: return "PKV_ERR_UNKNOWN";
+  }
+}
+
+int pkv_version(void) { return 100; }
+
+size_t pkv_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t num_splits) {
+  if (num_splits <= 1 || batch <= 0 || num_q_heads <= 0) return 0;
+  return (size_t)batch * num_q_heads * num_splits * (kD + 2) * sizeof(float);
+}
+
+size_t pkv_workqueue_workspace_bytes(int32_t total_partial_slots, int32_t num_q_heads) {
+  if (total_partial_slots <= 0 || num_q_heads <= 0) return 0;
+  return (size_t)total_partial_slots * num_q_heads * (kD + 2) * sizeof(float);
+}
+
+int pkv_paged_attention(const void* q, const void* k_pages, const void* v_pages,
+                        const int32_t* block_table, void* output, void* workspace,
+                        size_t workspace_bytes, int32_t batch, int32_t num_q_heads,
+                        int32_t num_kv_heads, int32_t head_dim, int32_t num_pages,
+                        int32_t page_size, int32_t max_pages, int32_t context,
+                        int32_t num_splits, int32_t dtype, void* stream) {
+  const Geometry g{batch, num_q_heads, num_kv_heads, head_dim, num_pages, page_size, max_pages, dtype};
+  return run_grid(g, q, batch, k_pages, v_pages, block_table, nullptr, nullptr, nullptr, output,
+                  batch, workspace, workspace_bytes, context, num_splits, stream);
+}
+
+int pkv_paged_attention_masked(const void* q, const void* k_pages, const void* v_pages,
+                               const int32_t* block_table, const int32_t* seq_lens, void* output,
+                               void* workspace, size_t workspace_bytes, int32_t batch,
+                               int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                               int32_t num_pages, int32_t page_size, int32_t max_pages,
+                               int32_t bucket_context, int32_t num_splits, int32_t dtype,
+                               void* stream) {
+  if (batch > 0 && !seq_lens) return fail(PKV_ERR_INVALID_ARGUMENT, "seq_lens is null");
+  const Geometry g{batch, num_q_heads, num_kv_heads, head_dim, num_pages, page_size, max_pages, dtype};
+  return run_grid(g, q, batch, k_pages, v_pages, block_table, seq_lens, nullptr, nullptr, output,
+                  batch, workspace, workspace_bytes, bucket_context, num_splits, stream);
+}
+
+int pkv_paged_attention_indexed(const void* q_source, int32_t q_rows, const void* k_pages,
+                                const void* v_pages, const int32_t* block_table,
+                                const int32_t* seq_lens, const int32_t* q_indices,
+                                const int32_t* out_indices, void* output, int32_t out_rows,
+                                void* workspace, size_t workspace_bytes, int32_t batch,
+                                int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                int32_t num_pages, int32_t page_size, int32_t max_pages,
+                                int32_t bucket_context, int32_t num_splits, int32_t dtype,
+                                void* stream) {
+  if (batch > 0 && (!seq_lens || !q_indices || !out_indices))
+    return fail(PKV_ERR_INVALID_ARGUMENT, "seq_lens, q_indices and out_indices must be non-null");
+  if (batch > 0 && out_rows <= 0) return fail(PKV_ERR_INVALID_ARGUMENT, "output has no rows");
+  const Geometry g{batch, num_q_heads, num_kv_heads, head_dim, num_pages, page_size, max_pages, dtype};
+  return run_grid(g, q_source, q_rows, k_pages, v_pages, block_table, seq_lens, q_indices,
+                  out_indices, output, out_rows, workspace, workspace_bytes, bucket_context,
+                  num_splits, stream);
+}
+
+int pkv_paged_attention_workqueue(
+    const void* q_source, int32_t q_rows, const void* k_pages, const void* v_pages,
+    const int32_t* block_table, const int32_t* seq_lens, const int32_t* work_items,
+    int32_t num_tasks, const int32_t* split_offsets, int32_t* merge_counters,
+    const int32_t* q_indices, const int32_t* out_indices, void* output, int32_t out_rows,
+    void* workspace, size_t workspace_bytes, int32_t batch, int32_t num_q_heads,
+    int32_t num_kv_heads, int32_t head_dim, int32_t num_pages, int32_t page_size,
+    int32_t max_pages, int32_t bucket_context, int32_t total_partial_slots,
+    int32_t fused_merge, int32_t dtype, void* stream) {
+  QueueCall c{{batch, num_q_heads, num_kv_heads, head_dim, num_pages, page_size, max_pages, dtype},
+              q_source, k_pages, v_pages, q_rows, block_table, seq_lens, work_items, split_offsets,
+              q_indices, out_indices, merge_counters, output, out_rows, workspace, workspace_bytes,
+              bucket_context, num_tasks, total_partial_slots};
+  int st = check_queue(c, true);
+  if (st != PKV_OK) return st;
+  if (out_rows <= 0) return fail(PKV_ERR_INVALID_ARGUMENT, "output has no rows");
+  if (fused_merge && !merge_counters) return fail(PKV_ERR_INVALID_ARGUMENT, "merge_counters is null");
+  if (batch == 0) return ok();
+  DecodeArgs a = queue_args(c);
+  a.merge_counters = fused_merge ? merge_counters : nullptr;
+  hipStream_t hs = (hipStream_t)stream;
+  st = dispatch_decode<kQueue>(a, dtype, num_tasks, hs);
+  if (st != PKV_OK) return st;
+  if (!fused_merge) {
+    st = dispatch_merge(queue_merge_args(a), true, dtype, hs);
+    if (st != PKV_OK) return st;
+  }
+  return ok();
+}
+
+int pkv_workqueue_decode(const void* q_source, int32_t q_rows, const void* k_pages,
+                         const void* v_pages, const int32_t* block_table, const int32_t* seq_lens,
+                         const int32_t* work_items, int32_t num_tasks,
+                         const int32_t* split_offsets, const int32_t* q_indices, void* workspace,
+                         size_t workspace_bytes, int32_t batch, int32_t num_q_heads,
+                         int32_t num_kv_heads, int32_t head_dim, int32_t num_pages,
+                         int32_t page_size, int32_t max_pages, int32_t bucket_context,
+                         int32_t total_partial_slots, int32_t dtype, void* stream) {
+  QueueCall c{{batch, num_q_heads, num_kv_heads, head_dim, num_pages, page_size, max_pages, dtype},
+              q_source, k_pages, v_pages, q_rows, block_table, seq_lens, work_items, split_offsets,
+              q_indices, nullptr, nullptr, nullptr, 0, workspace, workspace_bytes,
+              bucket_context, num_tasks, total_partial_slots};
+  int st = check_queue(c, false);
+  if (st != PKV_OK) return st;
+  if (batch == 0) return ok();
+  st = dispatch_decode<kQueue>(queue_args(c), dtype, num_tasks, (hipStream_t)stream);
+  return st == PKV_OK ? ok() : st;
+}
+
+int pkv_workqueue_merge(const int32_t* seq_lens, const int32_t* split_offsets,
+                        const int32_t* out_indices, void* output, int32_t out_rows,
+                        const void* workspace, size_t workspace_bytes, int32_t batch,
+                        int32_t num_q_heads, int32_t total_partial_slots, int32_t dtype,
+                        void* stream) {
+  if (dtype != PKV_DTYPE_F16 && dtype != PKV_DTYPE_BF16)
+    return fail(PKV_ERR_UNSUPPORTED, "dtype must be fp16 or bf16");
+  if (batch < 0 || num_q_heads <= 0) return fail(PKV_ERR_INVALID_ARGUMENT, "bad batch or head count");
+  if (total_partial_slots <= 0)
+    return fail(PKV_ERR_INVALID_ARGUMENT, "total_partial_slots must be positive");
+  if (batch > 0 && (!seq_lens || !split_offsets || !output || out_rows <= 0))
+    return fail(PKV_ERR_INVALID_ARGUMENT, "merge metadata or output is missing");
+  const size_t need = pkv_workqueue_workspace_bytes(total_partial_slots, num_q_heads);
+  if (!workspace || workspace_bytes < need)
+    return fail(PKV_ERR_WORKSPACE_TOO_SMALL, "merge requires a workspace of %zu bytes", need);
+  if (batch == 0) return ok();
+  const long states = (long)total_partial_slots * num_q_heads;
+  MergeArgs m = {};
+  m.part_m = (const float*)workspace;
+  m.part_l = m.part_m + states;
+  m.part_acc = m.part_l + states;
+  m.seq_lens = seq_lens;
+  m.split_offsets = split_offsets;
+  m.out_indices = out_indices;
+  m.out = (uint8_t*)output;
+  m.batch = batch;
+  m.hq = num_q_heads;
+  m.out_rows = out_rows;
+  m.total_slots = total_partial_slots;
+  m.max_tokens = 0x7fffffff;
+  const int st = dispatch_merge(m, true, dtype, (hipStream_t)stream);
+  return st == PKV_OK ? ok() : st;
+}
+
+}  // extern "C"

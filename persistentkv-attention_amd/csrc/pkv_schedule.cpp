@@ -1,0 +1,338 @@
+// pkv_schedule.cpp — host scheduling for the PersistentKV decode engine: split policy,
+// roofline cost-model router and the compact work-queue builder.
+//
+// PKV_POLICY_REFERENCE reproduces tests/benchmark_serving_trace.py bit for bit (integer
+// results exactly; floating-point estimates with the same operation order in IEEE
+// double, which is what CPython's float is).  PKV_POLICY_MI355X re-targets the split
+// choice at 256 compute units: it sizes work items from the whole step's tile count so
+// that every CU holds several workgroups, instead of the reference's fixed CTA target
+// calibrated for a 28-SM RTX 3060.
+//
+// Pure host code: no HIP calls.
+
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <cmath>
+#include <set>
+#include <vector>
+
+#include "pkv.h"
+
+namespace {
+
+constexpr int kTileTokens = 32;
+
+// Python floor division for the non-negative operands used here; negative lengths are
+// mapped through Python's floor semantics explicitly where the reference can see them.
+inline int64_t floordiv(int64_t a, int64_t b) {
+  int64_t q = a / b, r = a % b;
+  return (r != 0 && ((r < 0) != (b < 0))) ? q - 1 : q;
+}
+
+inline int64_t ceil_div_pos(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+inline int32_t round_up4(int64_t v) { return (int32_t)(floordiv(v + 3, 4) * 4); }  // :324-325
+
+inline int64_t tiles_of(int64_t length) { return floordiv(length + 31, 32); }
+
+// MI355X targets: 256 CUs, two resident 4-wave workgroups per CU, and at least this
+// many 32-token tiles per work item so the per-item Q load, LDS combine and partial
+// write stay small next to the K/V stream.
+constexpr int kMiComputeUnits = 256;
+constexpr int kMiItemsPerCu = 4;
+constexpr int kMiMinTilesPerItem = 8;
+constexpr int kMiMaxSplits = 128;
+
+}  // namespace
+
+extern "C" {
+
+void pkv_cost_model_preset(int32_t policy, pkv_cost_model* m) {
+  if (!m) return;
+  m->num_q_heads = 32;       // HQ, benchmark_serving_trace.py:33
+  m->num_kv_heads = 8;       // HKV, :34
+  m->head_dim = 128;         // DIM, :35
+  m->min_long_context = 16384;  // adaptive gate, :457
+  m->policy = policy;
+  if (policy == PKV_POLICY_MI355X) {
+    m->compute_units = kMiComputeUnits;
+    m->read_gbps = 8000.0 * 0.70;   // 70 % of the 8 TB/s HBM3E peak
+    m->launch_overhead_us = 4.0;
+    m->min_ctas_per_cu = 2.0;
+    m->supported_group = 0;         // every G runs natively
+  } else {
+    m->compute_units = 28;          // SM_COUNT, :39
+    m->read_gbps = 302.0;           // ROOFLINE_READ_GBPS, :40
+    m->launch_overhead_us = 8.0;    // LAUNCH_OVERHEAD_US, :41
+    m->min_ctas_per_cu = 4.0;       // MIN_CTAS_PER_SM, :42
+    m->supported_group = 4;         // SUPPORTED_PERSISTENTKV_GQA, :43
+  }
+}
+
+// choose_workqueue_row_splits, benchmark_serving_trace.py:370-393.
+int32_t pkv_choose_workqueue_row_splits(int32_t length, int32_t active_count,
+                                        int32_t requested_splits, int32_t auto_splits,
+                                        int32_t num_kv_heads, int32_t policy) {
+  if (!auto_splits) return requested_splits;
+  const int64_t tiles = std::max<int64_t>(1, tiles_of(length));
+  const int64_t hkv = num_kv_heads > 0 ? num_kv_heads : 1;
+  const int64_t active = std::max<int32_t>(1, active_count);
+  if (policy == PKV_POLICY_MI355X) {
+    // Per-row view of the joint planner: assume the other rows are as long as this one.
+    const int64_t target = (int64_t)kMiComputeUnits * kMiItemsPerCu;
+    const int64_t per_item = std::max<int64_t>(kMiMinTilesPerItem,
+                                               ceil_div_pos(tiles * active * hkv, target));
+    const int64_t s = ceil_div_pos(tiles, per_item);
+    return (int32_t)std::max<int64_t>(1, std::min<int64_t>(s, kMiMaxSplits));
+  }
+  const int32_t occupancy_floor = round_up4(ceil_div_pos(256, hkv * active));
+  const int32_t length_target = round_up4(ceil_div_pos(tiles, 64));
+  int32_t splits = std::max(occupancy_floor, length_target);
+  if (active_count >= 8) splits = std::min(splits, 24);
+  else if (active_count >= 4) splits = std::min(splits, 32);
+  else if (active_count == 2) splits = std::min(splits, 40);
+  else splits = std::min(splits, 48);
+  return (int32_t)std::max<int64_t>(4, std::min<int64_t>(std::min(splits, 48), tiles));
+}
+
+// choose_splits, benchmark_serving_trace.py:328-367.
+int32_t pkv_choose_splits(const int32_t* lengths, int32_t count, int32_t requested_splits,
+                          int32_t auto_splits, int32_t single_bucket, int32_t num_kv_heads,
+                          int32_t policy) {
+  if (!auto_splits) return requested_splits;
+  if (!lengths || count <= 0) return requested_splits;
+  int64_t t_max = INT64_MIN, t_min = INT64_MAX;
+  for (int i = 0; i < count; ++i) {
+    const int64_t t = tiles_of(lengths[i]);
+    t_max = std::max(t_max, t);
+    t_min = std::min(t_min, t);
+  }
+  const int64_t batch = count;
+  const int64_t hkv = num_kv_heads > 0 ? num_kv_heads : 1;
+  auto clamp4 = [&](int64_t cap) { return (int32_t)std::max<int64_t>(4, std::min(cap, t_min)); };
+  if (policy == PKV_POLICY_MI355X) {
+    // One split count for the whole bucket: enough items for every CU, at least
+    // kMiMinTilesPerItem tiles per item on the shortest row.
+    const int64_t target = (int64_t)kMiComputeUnits * kMiItemsPerCu;
+    int64_t s = ceil_div_pos(target, hkv * batch);
+    s = std::min<int64_t>(s, std::max<int64_t>(1, t_min / kMiMinTilesPerItem));
+    return (int32_t)std::max<int64_t>(1, std::min<int64_t>(s, std::min<int64_t>(kMiMaxSplits, t_min)));
+  }
+  if (single_bucket) {
+    if (batch >= 8) return clamp4(40);
+    if (batch == 4) return clamp4(16);
+    if (batch == 2) return clamp4(24);
+    if (t_max >= 1024) return clamp4(36);
+    return clamp4(24);
+  }
+  if (batch >= 8) return clamp4(24);
+  if (batch == 4) return clamp4(28);
+  if (batch == 2 && t_max >= 1024) return clamp4(32);
+  const int64_t occupancy = ceil_div_pos(320, hkv * batch);
+  const int64_t length_based = (int64_t)std::ceil((double)t_max / 32.0);
+  int64_t splits = round_up4(std::max(occupancy, length_based));
+  if (t_max <= 384) splits = std::min<int64_t>(splits, 24);
+  if (batch >= 8) splits = std::min<int64_t>(splits, 40);
+  if (batch <= 2 && t_max >= 1024) splits = std::max<int64_t>(splits, 32);
+  return (int32_t)std::max<int64_t>(4, std::min(std::min<int64_t>(splits, 48), t_min));
+}
+
+// model_bucket_splits, benchmark_serving_trace.py:396-402.
+int32_t pkv_model_bucket_splits(const int32_t* lengths, int32_t count, int32_t num_kv_heads,
+                                int32_t policy) {
+  if (!lengths || count <= 0) return 4;
+  int64_t t_max = INT64_MIN, t_min = INT64_MAX;
+  for (int i = 0; i < count; ++i) {
+    const int64_t t = tiles_of(lengths[i]);
+    t_max = std::max(t_max, t);
+    t_min = std::min(t_min, t);
+  }
+  const int64_t hkv = num_kv_heads > 0 ? num_kv_heads : 1;
+  if (policy == PKV_POLICY_MI355X) return pkv_choose_splits(lengths, count, 1, 1, 0, num_kv_heads, policy);
+  const int64_t occupancy = ceil_div_pos(256, hkv * std::max<int64_t>(1, count));
+  const int64_t length_based = (int64_t)std::ceil((double)t_max / 96.0);
+  const int64_t r = round_up4(std::max(occupancy, length_based));
+  return (int32_t)std::max<int64_t>(4, std::min(std::min<int64_t>(r, 48), t_min));
+}
+
+// model_workqueue_splits, benchmark_serving_trace.py:405-415.
+int32_t pkv_model_workqueue_splits(const int32_t* lengths, int32_t count, int32_t num_kv_heads,
+                                   int32_t policy) {
+  int32_t best = INT32_MIN;
+  for (int i = 0; i < count; ++i)
+    best = std::max(best, pkv_choose_workqueue_row_splits(lengths[i], count, 1, 1, num_kv_heads, policy));
+  return best;
+}
+
+// estimate_route_ms, benchmark_serving_trace.py:418-442 (and useful_kv_mb_for_state :511-513).
+double pkv_estimate_route_ms(const int32_t* lengths, int32_t count, int32_t route, int32_t splits,
+                             const pkv_cost_model* m) {
+  if (!m || (!lengths && count > 0)) return NAN;
+  int64_t sum_len = 0;
+  std::set<int32_t> unique;
+  for (int i = 0; i < count; ++i) {
+    sum_len += lengths[i];
+    unique.insert(lengths[i]);
+  }
+  const int64_t bytes_read = sum_len * m->num_kv_heads * m->head_dim * 2 * 2;
+  const double kv_mb = (double)bytes_read / (1024.0 * 1024.0);
+  const double kv_ms = kv_mb / m->read_gbps;
+  const int64_t active = count;
+  double ctas_per_cu;
+  int64_t launch_count;
+  double merge_mb;
+  const int64_t merge_bytes = active * m->num_q_heads * (int64_t)splits * (2 + m->head_dim) * 4;
+  if (route == PKV_ROUTE_FLASHINFER) {
+    ctas_per_cu = (double)(active * m->num_kv_heads) / (double)m->compute_units;
+    launch_count = 1;
+    merge_mb = 0.0;
+  } else if (route == PKV_ROUTE_BUCKET) {
+    ctas_per_cu = (double)(active * m->num_kv_heads * splits) / (double)m->compute_units;
+    launch_count = 2 * (int64_t)unique.size();
+    merge_mb = (double)merge_bytes / (1024.0 * 1024.0);
+  } else if (route == PKV_ROUTE_WORKQUEUE) {
+    ctas_per_cu = (double)(active * m->num_kv_heads * splits) / (double)m->compute_units;
+    launch_count = 2;
+    merge_mb = (double)merge_bytes / (1024.0 * 1024.0);
+  } else {
+    return NAN;
+  }
+  const double occupancy_penalty = std::max(1.0, m->min_ctas_per_cu / std::max(ctas_per_cu, 1e-6));
+  const double launch_ms = (double)launch_count * m->launch_overhead_us / 1000.0;
+  const double merge_ms = merge_mb / m->read_gbps;
+  return kv_ms * occupancy_penalty + merge_ms + launch_ms;
+}
+
+// choose_adaptive_route_cost_model, benchmark_serving_trace.py:445-488.  The reference
+// falls back to FlashInfer for unsupported G and short contexts; with supported_group
+// == 0 every G stays on the native routes.
+int32_t pkv_choose_adaptive_route(const int32_t* lengths, int32_t count, const pkv_cost_model* m,
+                                  int32_t* out_splits, double* out_ms) {
+  if (!m || !lengths || count <= 0) return -1;
+  const int32_t g = m->num_kv_heads > 0 ? m->num_q_heads / m->num_kv_heads : 0;
+  int32_t route = PKV_ROUTE_FLASHINFER, splits = 1;
+  double best = pkv_estimate_route_ms(lengths, count, PKV_ROUTE_FLASHINFER, 1, m);
+  const int32_t max_len = *std::max_element(lengths, lengths + count);
+  const bool gate = (m->supported_group != 0 && g != m->supported_group) || max_len < m->min_long_context;
+  if (!gate) {
+    if (count <= 1) {
+      const int32_t s = pkv_model_bucket_splits(lengths, count, m->num_kv_heads, m->policy);
+      const double e = pkv_estimate_route_ms(lengths, count, PKV_ROUTE_BUCKET, s, m);
+      if (e < best) { best = e; route = PKV_ROUTE_BUCKET; splits = s; }
+    }
+    if (count >= 8) {
+      const int32_t s = pkv_model_workqueue_splits(lengths, count, m->num_kv_heads, m->policy);
+      const double e = pkv_estimate_route_ms(lengths, count, PKV_ROUTE_WORKQUEUE, s, m);
+      if (e < best) { best = e; route = PKV_ROUTE_WORKQUEUE; splits = s; }
+    }
+  }
+  if (out_splits) *out_splits = splits;
+  if (out_ms) *out_ms = best;
+  return route;
+}
+
+static void plan_row_splits(const int32_t* lengths, int32_t count, int32_t requested_splits,
+                            int32_t auto_splits, int32_t num_kv_heads, int32_t policy,
+                            std::vector<int32_t>& out) {
+  out.resize(count);
+  if (auto_splits && policy == PKV_POLICY_MI355X) {
+    // Joint plan: size items from the step's total tile count.
+    int64_t total = 0;
+    for (int i = 0; i < count; ++i) total += std::max<int64_t>(1, tiles_of(lengths[i]));
+    const int64_t hkv = num_kv_heads > 0 ? num_kv_heads : 1;
+    const int64_t target = (int64_t)kMiComputeUnits * kMiItemsPerCu;
+    const int64_t per_item = std::max<int64_t>(kMiMinTilesPerItem, ceil_div_pos(total * hkv, target));
+    for (int i = 0; i < count; ++i) {
+      const int64_t tiles = std::max<int64_t>(1, tiles_of(lengths[i]));
+      out[i] = (int32_t)std::max<int64_t>(1, std::min<int64_t>(ceil_div_pos(tiles, per_item), kMiMaxSplits));
+    }
+    return;
+  }
+  for (int i = 0; i < count; ++i)
+    out[i] = pkv_choose_workqueue_row_splits(lengths[i], count, requested_splits, auto_splits,
+                                             num_kv_heads, policy);
+}
+
+int pkv_workqueue_size(const int32_t* lengths, int32_t count, int32_t requested_splits,
+                       int32_t auto_splits, int32_t num_kv_heads, int32_t policy,
+                       int32_t* out_num_tasks, int32_t* out_total_partial_slots) {
+  if ((!lengths && count > 0) || count < 0 || num_kv_heads <= 0) return PKV_ERR_INVALID_ARGUMENT;
+  std::vector<int32_t> splits;
+  plan_row_splits(lengths, count, requested_splits, auto_splits, num_kv_heads, policy, splits);
+  int64_t tasks = 0, slots = 0;
+  for (int r = 0; r < count; ++r) {
+    const int64_t total_tiles = tiles_of(lengths[r]);
+    const int64_t s = splits[r];
+    for (int64_t sp = 0; sp < s; ++sp)
+      if (floordiv(total_tiles * sp, s) < floordiv(total_tiles * (sp + 1), s)) tasks += num_kv_heads;
+    slots += s;
+  }
+  if (tasks > INT32_MAX || slots > INT32_MAX) return PKV_ERR_CAPACITY;
+  if (out_num_tasks) *out_num_tasks = (int32_t)tasks;
+  if (out_total_partial_slots) *out_total_partial_slots = (int32_t)slots;
+  return PKV_OK;
+}
+
+// Work-queue branch of compile_persistentkv_metadata, benchmark_serving_trace.py:668-729.
+int pkv_build_workqueue(const int32_t* lengths, const int32_t* request_ids, int32_t count,
+                        const int32_t* page_indptr, const int32_t* page_ids, int32_t page_size,
+                        int32_t requested_splits, int32_t auto_splits, int32_t num_kv_heads,
+                        int32_t policy, int32_t* block_table, int32_t table_capacity,
+                        int32_t* out_table_cols, int32_t* seq_lens, int32_t* q_indices,
+                        int32_t* out_indices, int32_t* work_items, int32_t work_capacity,
+                        int32_t* out_num_tasks, int32_t* split_offsets,
+                        int32_t* out_total_partial_slots) {
+  if (count <= 0 || !lengths || !request_ids || !page_indptr || !page_ids || page_size <= 0 ||
+      num_kv_heads <= 0)
+    return PKV_ERR_INVALID_ARGUMENT;
+  const int32_t bucket_length = *std::max_element(lengths, lengths + count);  // :669
+  const int64_t page_count = bucket_length > 0 ? ceil_div_pos(bucket_length, page_size) : 0;  // :670
+  int32_t tasks = 0, slots = 0;
+  int st = pkv_workqueue_size(lengths, count, requested_splits, auto_splits, num_kv_heads, policy,
+                              &tasks, &slots);
+  if (st != PKV_OK) return st;
+  if (out_table_cols) *out_table_cols = (int32_t)page_count;
+  if (out_num_tasks) *out_num_tasks = tasks;
+  if (out_total_partial_slots) *out_total_partial_slots = slots;
+  if ((int64_t)count * page_count > table_capacity || tasks > work_capacity) return PKV_ERR_CAPACITY;
+  if (!block_table || !seq_lens || !q_indices || !out_indices || !split_offsets ||
+      (tasks > 0 && !work_items))
+    return PKV_ERR_INVALID_ARGUMENT;
+  std::vector<int32_t> splits;
+  plan_row_splits(lengths, count, requested_splits, auto_splits, num_kv_heads, policy, splits);
+  int32_t n = 0;
+  split_offsets[0] = 0;
+  for (int32_t r = 0; r < count; ++r) {
+    const int32_t p0 = page_indptr[r], p1 = page_indptr[r + 1];
+    if (p1 < p0) return PKV_ERR_INVALID_ARGUMENT;
+    if (p1 == p0 && page_count > 0) return PKV_ERR_INVALID_ARGUMENT;  // reference indexes [-1]
+    int32_t* row = block_table + (int64_t)r * page_count;
+    for (int64_t c = 0; c < page_count; ++c)  // :679-683 pad with the last reserved page
+      row[c] = (c < p1 - p0) ? page_ids[p0 + c] : page_ids[p1 - 1];
+    seq_lens[r] = lengths[r];
+    q_indices[r] = request_ids[r];
+    out_indices[r] = r;
+    const int64_t s = splits[r];
+    const int64_t total_tiles = tiles_of(lengths[r]);  // :695
+    for (int64_t sp = 0; sp < s; ++sp) {
+      const int64_t tb = floordiv(total_tiles * sp, s), te = floordiv(total_tiles * (sp + 1), s);
+      if (tb >= te) continue;  // :699-700
+      for (int32_t kvh = 0; kvh < num_kv_heads; ++kvh) {
+        int32_t* w = work_items + (int64_t)n * 5;
+        w[0] = r;
+        w[1] = kvh;
+        w[2] = (int32_t)sp;
+        w[3] = (int32_t)tb;
+        w[4] = (int32_t)te;
+        ++n;
+      }
+    }
+    split_offsets[r + 1] = split_offsets[r] + (int32_t)s;  // :703 counts empty splits too
+  }
+  return PKV_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,312 @@
+// pkv_torch_ext.cpp — PyTorch op surface of the PersistentKV engine, over the C ABI.
+//
+// Same op names, positional arguments, validation messages and in-place `None` return
+// as tests/persistentkv_torch_extension.cu (:9-31 checks, :35-317 ops, :319-336
+// bindings), so tests/benchmark_serving_trace.py can call it unchanged.  Differences:
+//   * q / pages / output may be fp16 or bf16 (all four the same dtype);
+//   * G = Hq / Hkv may be any integer in [1, 32] (the reference accepts {1, 2, 4, 8});
+//   * launch failures raise RuntimeError instead of terminating the process.
+// Work is enqueued on the current HIP stream of the tensors' device without a host sync,
+// so the ops can be captured in HIP graphs.
+
+#include <torch/extension.h>
+
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+
+#include "pkv.h"
+
+namespace {
+
+void check_tensor(const torch::Tensor& tensor, const char* name, at::ScalarType dtype, int64_t dims) {
+  TORCH_CHECK(tensor.is_cuda(), name, " must be a CUDA tensor");
+  TORCH_CHECK(tensor.scalar_type() == dtype, name, " has wrong dtype");
+  TORCH_CHECK(tensor.dim() == dims, name, " has wrong rank");
+  TORCH_CHECK(tensor.is_contiguous(), name, " must be contiguous");
+}
+
+// The activation dtype is taken from q and must be fp16 or bf16.
+at::ScalarType activation_dtype(const torch::Tensor& q, const char* name) {
+  TORCH_CHECK(q.scalar_type() == at::kHalf || q.scalar_type() == at::kBFloat16, name,
+              " has wrong dtype");
+  return q.scalar_type();
+}
+
+int32_t pkv_dtype_of(at::ScalarType t) { return t == at::kBFloat16 ? PKV_DTYPE_BF16 : PKV_DTYPE_F16; }
+
+void check_supported_gqa(int Hq, int Hkv) {
+  TORCH_CHECK(Hkv > 0, "Hkv must be positive");
+  TORCH_CHECK(Hq % Hkv == 0, "Hq must be divisible by Hkv");
+  const int G = Hq / Hkv;
+  TORCH_CHECK(G >= 1 && G <= PKV_MAX_GROUP, "PersistentKV supports G=Hq/Hkv in [1,32]; got G=", G,
+              " from Hq=", Hq, " Hkv=", Hkv);
+}
+
+void check_workspace(const torch::Tensor& workspace) {
+  TORCH_CHECK(workspace.is_cuda(), "workspace must be a CUDA tensor");
+  TORCH_CHECK(workspace.is_contiguous(), "workspace must be contiguous");
+}
+
+void check_pages(const torch::Tensor& k_pages, const torch::Tensor& v_pages, int64_t page_size, int d) {
+  const int64_t physical_pages = k_pages.size(0);
+  const int64_t Hkv = k_pages.size(1);
+  TORCH_CHECK(v_pages.size(0) == physical_pages && v_pages.size(1) == Hkv &&
+                  v_pages.size(2) == page_size && v_pages.size(3) == d,
+              "v_pages shape mismatch");
+  TORCH_CHECK(k_pages.size(2) == page_size && k_pages.size(3) == d, "k_pages shape mismatch");
+}
+
+void* ws_ptr(const torch::Tensor& w) { return w.numel() > 0 ? w.data_ptr() : nullptr; }
+size_t ws_bytes(const torch::Tensor& w) { return w.numel() > 0 ? (size_t)w.nbytes() : 0; }
+void* stream_of(const torch::Tensor& t) {
+  return (void*)c10::hip::getCurrentHIPStream(t.device().index()).stream();
+}
+int32_t i32(int64_t v, const char* name) {
+  TORCH_CHECK(v >= INT32_MIN && v <= INT32_MAX, name, " does not fit in int32");
+  return (int32_t)v;
+}
+void raise_on(int status) { TORCH_CHECK(status == PKV_OK, pkv_last_error()); }
+
+}  // namespace
+
+// tests/persistentkv_torch_extension.cu:35-93
+void persistentkv_paged_attention(torch::Tensor q, torch::Tensor k_pages, torch::Tensor v_pages,
+                                  torch::Tensor block_table, torch::Tensor output,
+                                  torch::Tensor workspace, int64_t context, int64_t page_size,
+                                  int64_t num_splits) {
+  const auto dt = activation_dtype(q, "q");
+  check_tensor(q, "q", dt, 3);
+  check_tensor(k_pages, "k_pages", dt, 4);
+  check_tensor(v_pages, "v_pages", dt, 4);
+  check_tensor(block_table, "block_table", at::kInt, 2);
+  check_tensor(output, "output", dt, 3);
+  check_workspace(workspace);
+  const int B = (int)q.size(0), Hq = (int)q.size(1), d = (int)q.size(2);
+  const int Hkv = (int)k_pages.size(1);
+  TORCH_CHECK(d == PKV_HEAD_DIM, "PersistentKV extension currently requires d=128");
+  TORCH_CHECK(output.size(0) == B && output.size(1) == Hq && output.size(2) == d,
+              "output shape must match q");
+  check_pages(k_pages, v_pages, page_size, d);
+  TORCH_CHECK(block_table.size(0) == B, "block_table batch mismatch");
+  check_supported_gqa(Hq, Hkv);
+  TORCH_CHECK(context > 0, "context must be positive");
+  TORCH_CHECK(page_size > 0, "page_size must be positive");
+  TORCH_CHECK(num_splits > 0, "num_splits must be positive");
+  const c10::DeviceGuard guard(q.device());
+  raise_on(pkv_paged_attention(
+      q.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(), block_table.data_ptr<int>(),
+      output.data_ptr(), ws_ptr(workspace), ws_bytes(workspace), B, Hq, Hkv, d,
+      i32(k_pages.size(0), "k_pages.size(0)"), i32(page_size, "page_size"),
+      i32(block_table.size(1), "block_table.size(1)"), i32(context, "context"),
+      i32(num_splits, "num_splits"), pkv_dtype_of(dt), stream_of(q)));
+}
+
+// tests/persistentkv_torch_extension.cu:95-157
+void persistentkv_paged_attention_masked(torch::Tensor q, torch::Tensor k_pages,
+                                         torch::Tensor v_pages, torch::Tensor block_table,
+                                         torch::Tensor seq_lens, torch::Tensor output,
+                                         torch::Tensor workspace, int64_t bucket_context,
+                                         int64_t page_size, int64_t num_splits) {
+  const auto dt = activation_dtype(q, "q");
+  check_tensor(q, "q", dt, 3);
+  check_tensor(k_pages, "k_pages", dt, 4);
+  check_tensor(v_pages, "v_pages", dt, 4);
+  check_tensor(block_table, "block_table", at::kInt, 2);
+  check_tensor(seq_lens, "seq_lens", at::kInt, 1);
+  check_tensor(output, "output", dt, 3);
+  check_workspace(workspace);
+  const int B = (int)q.size(0), Hq = (int)q.size(1), d = (int)q.size(2);
+  const int Hkv = (int)k_pages.size(1);
+  TORCH_CHECK(d == PKV_HEAD_DIM, "PersistentKV extension currently requires d=128");
+  TORCH_CHECK(output.size(0) == B && output.size(1) == Hq && output.size(2) == d,
+              "output shape must match q");
+  TORCH_CHECK(seq_lens.size(0) == B, "seq_lens batch mismatch");
+  check_pages(k_pages, v_pages, page_size, d);
+  TORCH_CHECK(block_table.size(0) == B, "block_table batch mismatch");
+  check_supported_gqa(Hq, Hkv);
+  TORCH_CHECK(bucket_context > 0, "bucket_context must be positive");
+  TORCH_CHECK(page_size > 0, "page_size must be positive");
+  TORCH_CHECK(num_splits > 0, "num_splits must be positive");
+  const c10::DeviceGuard guard(q.device());
+  raise_on(pkv_paged_attention_masked(
+      q.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(), block_table.data_ptr<int>(),
+      seq_lens.data_ptr<int>(), output.data_ptr(), ws_ptr(workspace), ws_bytes(workspace), B, Hq,
+      Hkv, d, i32(k_pages.size(0), "k_pages.size(0)"), i32(page_size, "page_size"),
+      i32(block_table.size(1), "block_table.size(1)"), i32(bucket_context, "bucket_context"),
+      i32(num_splits, "num_splits"), pkv_dtype_of(dt), stream_of(q)));
+}
+
+// tests/persistentkv_torch_extension.cu:159-228
+void persistentkv_paged_attention_indexed(torch::Tensor q_source, torch::Tensor k_pages,
+                                          torch::Tensor v_pages, torch::Tensor block_table,
+                                          torch::Tensor seq_lens, torch::Tensor q_indices,
+                                          torch::Tensor out_indices, torch::Tensor output,
+                                          torch::Tensor workspace, int64_t bucket_context,
+                                          int64_t page_size, int64_t num_splits) {
+  const auto dt = activation_dtype(q_source, "q_source");
+  check_tensor(q_source, "q_source", dt, 3);
+  check_tensor(k_pages, "k_pages", dt, 4);
+  check_tensor(v_pages, "v_pages", dt, 4);
+  check_tensor(block_table, "block_table", at::kInt, 2);
+  check_tensor(seq_lens, "seq_lens", at::kInt, 1);
+  check_tensor(q_indices, "q_indices", at::kInt, 1);
+  check_tensor(out_indices, "out_indices", at::kInt, 1);
+  check_tensor(output, "output", dt, 3);
+  check_workspace(workspace);
+  const int B = (int)block_table.size(0), Hq = (int)q_source.size(1), d = (int)q_source.size(2);
+  const int Hkv = (int)k_pages.size(1);
+  TORCH_CHECK(d == PKV_HEAD_DIM, "PersistentKV extension currently requires d=128");
+  TORCH_CHECK(output.size(1) == Hq && output.size(2) == d,
+              "output shape must match q head dimensions");
+  TORCH_CHECK(seq_lens.size(0) == B, "seq_lens batch mismatch");
+  TORCH_CHECK(q_indices.size(0) == B, "q_indices batch mismatch");
+  TORCH_CHECK(out_indices.size(0) == B, "out_indices batch mismatch");
+  check_pages(k_pages, v_pages, page_size, d);
+  check_supported_gqa(Hq, Hkv);
+  TORCH_CHECK(bucket_context > 0, "bucket_context must be positive");
+  TORCH_CHECK(page_size > 0, "page_size must be positive");
+  TORCH_CHECK(num_splits > 0, "num_splits must be positive");
+  const c10::DeviceGuard guard(q_source.device());
+  raise_on(pkv_paged_attention_indexed(
+      q_source.data_ptr(), i32(q_source.size(0), "q_source.size(0)"), k_pages.data_ptr(),
+      v_pages.data_ptr(), block_table.data_ptr<int>(), seq_lens.data_ptr<int>(),
+      q_indices.data_ptr<int>(), out_indices.data_ptr<int>(), output.data_ptr(),
+      i32(output.size(0), "output.size(0)"), ws_ptr(workspace), ws_bytes(workspace), B, Hq, Hkv, d,
+      i32(k_pages.size(0), "k_pages.size(0)"), i32(page_size, "page_size"),
+      i32(block_table.size(1), "block_table.size(1)"), i32(bucket_context, "bucket_context"),
+      i32(num_splits, "num_splits"), pkv_dtype_of(dt), stream_of(q_source)));
+}
+
+namespace {
+
+struct QueueTensors {
+  int B, Hq, Hkv, d;
+  at::ScalarType dt;
+};
+
+QueueTensors check_queue_tensors(const torch::Tensor& q_source, const torch::Tensor& k_pages,
+                                 const torch::Tensor& v_pages, const torch::Tensor& block_table,
+                                 const torch::Tensor& seq_lens, const torch::Tensor& work_items,
+                                 const torch::Tensor& split_offsets, const torch::Tensor& q_indices,
+                                 const torch::Tensor& workspace, int64_t bucket_context,
+                                 int64_t page_size, int64_t total_partial_slots) {
+  QueueTensors t;
+  t.dt = activation_dtype(q_source, "q_source");
+  check_tensor(q_source, "q_source", t.dt, 3);
+  check_tensor(k_pages, "k_pages", t.dt, 4);
+  check_tensor(v_pages, "v_pages", t.dt, 4);
+  check_tensor(block_table, "block_table", at::kInt, 2);
+  check_tensor(seq_lens, "seq_lens", at::kInt, 1);
+  check_tensor(work_items, "work_items", at::kInt, 2);
+  check_tensor(split_offsets, "split_offsets", at::kInt, 1);
+  check_tensor(q_indices, "q_indices", at::kInt, 1);
+  check_workspace(workspace);
+  t.B = (int)block_table.size(0);
+  t.Hq = (int)q_source.size(1);
+  t.d = (int)q_source.size(2);
+  t.Hkv = (int)k_pages.size(1);
+  TORCH_CHECK(t.d == PKV_HEAD_DIM, "PersistentKV extension currently requires d=128");
+  TORCH_CHECK(work_items.size(1) == 5, "work_items must have shape [T, 5]");
+  TORCH_CHECK(split_offsets.size(0) == t.B + 1, "split_offsets batch mismatch");
+  TORCH_CHECK(seq_lens.size(0) == t.B, "seq_lens batch mismatch");
+  TORCH_CHECK(q_indices.size(0) == t.B, "q_indices batch mismatch");
+  check_pages(k_pages, v_pages, page_size, t.d);
+  check_supported_gqa(t.Hq, t.Hkv);
+  TORCH_CHECK(bucket_context > 0, "bucket_context must be positive");
+  TORCH_CHECK(page_size > 0, "page_size must be positive");
+  TORCH_CHECK(work_items.size(0) > 0, "work_items must not be empty");
+  TORCH_CHECK(total_partial_slots > 0, "total_partial_slots must be positive");
+  return t;
+}
+
+}  // namespace
+
+// tests/persistentkv_torch_extension.cu:230-317
+void persistentkv_paged_attention_workqueue(
+    torch::Tensor q_source, torch::Tensor k_pages, torch::Tensor v_pages, torch::Tensor block_table,
+    torch::Tensor seq_lens, torch::Tensor work_items, torch::Tensor split_offsets,
+    torch::Tensor merge_counters, torch::Tensor q_indices, torch::Tensor out_indices,
+    torch::Tensor output, torch::Tensor workspace, int64_t bucket_context, int64_t page_size,
+    int64_t total_partial_slots, bool fused_merge) {
+  const QueueTensors t = check_queue_tensors(q_source, k_pages, v_pages, block_table, seq_lens,
+                                             work_items, split_offsets, q_indices, workspace,
+                                             bucket_context, page_size, total_partial_slots);
+  check_tensor(merge_counters, "merge_counters", at::kInt, 2);
+  check_tensor(out_indices, "out_indices", at::kInt, 1);
+  check_tensor(output, "output", t.dt, 3);
+  TORCH_CHECK(merge_counters.size(0) == t.B && merge_counters.size(1) == t.Hkv,
+              "merge_counters shape mismatch");
+  TORCH_CHECK(output.size(1) == t.Hq && output.size(2) == t.d,
+              "output shape must match q head dimensions");
+  TORCH_CHECK(out_indices.size(0) == t.B, "out_indices batch mismatch");
+  const c10::DeviceGuard guard(q_source.device());
+  raise_on(pkv_paged_attention_workqueue(
+      q_source.data_ptr(), i32(q_source.size(0), "q_source.size(0)"), k_pages.data_ptr(),
+      v_pages.data_ptr(), block_table.data_ptr<int>(), seq_lens.data_ptr<int>(),
+      work_items.data_ptr<int>(), i32(work_items.size(0), "work_items.size(0)"),
+      split_offsets.data_ptr<int>(), fused_merge ? merge_counters.data_ptr<int>() : nullptr,
+      q_indices.data_ptr<int>(), out_indices.data_ptr<int>(), output.data_ptr(),
+      i32(output.size(0), "output.size(0)"), ws_ptr(workspace), ws_bytes(workspace), t.B, t.Hq,
+      t.Hkv, t.d, i32(k_pages.size(0), "k_pages.size(0)"), i32(page_size, "page_size"),
+      i32(block_table.size(1), "block_table.size(1)"), i32(bucket_context, "bucket_context"),
+      i32(total_partial_slots, "total_partial_slots"), fused_merge ? 1 : 0, pkv_dtype_of(t.dt),
+      stream_of(q_source)));
+}
+
+// Stage 1 of the work-queue op: the decode kernel alone, writing partial states.
+void persistentkv_workqueue_decode(torch::Tensor q_source, torch::Tensor k_pages,
+                                   torch::Tensor v_pages, torch::Tensor block_table,
+                                   torch::Tensor seq_lens, torch::Tensor work_items,
+                                   torch::Tensor split_offsets, torch::Tensor q_indices,
+                                   torch::Tensor workspace, int64_t bucket_context,
+                                   int64_t page_size, int64_t total_partial_slots) {
+  const QueueTensors t = check_queue_tensors(q_source, k_pages, v_pages, block_table, seq_lens,
+                                             work_items, split_offsets, q_indices, workspace,
+                                             bucket_context, page_size, total_partial_slots);
+  const c10::DeviceGuard guard(q_source.device());
+  raise_on(pkv_workqueue_decode(
+      q_source.data_ptr(), i32(q_source.size(0), "q_source.size(0)"), k_pages.data_ptr(),
+      v_pages.data_ptr(), block_table.data_ptr<int>(), seq_lens.data_ptr<int>(),
+      work_items.data_ptr<int>(), i32(work_items.size(0), "work_items.size(0)"),
+      split_offsets.data_ptr<int>(), q_indices.data_ptr<int>(), ws_ptr(workspace),
+      ws_bytes(workspace), t.B, t.Hq, t.Hkv, t.d, i32(k_pages.size(0), "k_pages.size(0)"),
+      i32(page_size, "page_size"), i32(block_table.size(1), "block_table.size(1)"),
+      i32(bucket_context, "bucket_context"), i32(total_partial_slots, "total_partial_slots"),
+      pkv_dtype_of(t.dt), stream_of(q_source)));
+}
+
+// Stage 2 of the work-queue op: the segmented LSE merge alone.
+void persistentkv_workqueue_merge(torch::Tensor seq_lens, torch::Tensor split_offsets,
+                                  torch::Tensor out_indices, torch::Tensor output,
+                                  torch::Tensor workspace, int64_t total_partial_slots) {
+  const auto dt = activation_dtype(output, "output");
+  check_tensor(seq_lens, "seq_lens", at::kInt, 1);
+  check_tensor(split_offsets, "split_offsets", at::kInt, 1);
+  check_tensor(out_indices, "out_indices", at::kInt, 1);
+  check_tensor(output, "output", dt, 3);
+  check_workspace(workspace);
+  const int B = (int)seq_lens.size(0);
+  TORCH_CHECK(split_offsets.size(0) == B + 1, "split_offsets batch mismatch");
+  TORCH_CHECK(out_indices.size(0) == B, "out_indices batch mismatch");
+  TORCH_CHECK(output.size(2) == PKV_HEAD_DIM, "PersistentKV extension currently requires d=128");
+  const c10::DeviceGuard guard(output.device());
+  raise_on(pkv_workqueue_merge(
+      seq_lens.data_ptr<int>(), split_offsets.data_ptr<int>(), out_indices.data_ptr<int>(),
+      output.data_ptr(), i32(output.size(0), "output.size(0)"), ws_ptr(workspace),
+      ws_bytes(workspace), B, i32(output.size(1), "output.size(1)"),
+      i32(total_partial_slots, "total_partial_slots"), pkv_dtype_of(dt), stream_of(output)));
+}
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("paged_attention", &persistentkv_paged_attention, "PersistentKV native paged attention");
+  m.def("paged_attention_masked", &persistentkv_paged_attention_masked,
+        "PersistentKV native paged attention with per-request sequence lengths");
+  m.def("paged_attention_indexed", &persistentkv_paged_attention_indexed,
+        "PersistentKV native paged attention with indexed Q/O rows");
+  m.def("paged_attention_workqueue", &persistentkv_paged_attention_workqueue,
+        "PersistentKV native paged attention with compact work queue");
+  m.def("workqueue_decode", &persistentkv_workqueue_decode,
+        "Work-queue decode stage only (partial states into the workspace)");
+  m.def("workqueue_merge", &persistentkv_workqueue_merge,
+        "Work-queue segmented LSE merge stage only");
+}

@@ -1,0 +1,66 @@
+"""PersistentKV paged decode attention for MI355X — PyTorch op surface.
+
+Drop-in for the module that tests/benchmark_serving_trace.py builds with
+``torch.utils.cpp_extension.load(name="persistentkv_torch_ext", ...)`` (:133-156): the
+same four ops with the same positional arguments, checks and in-place ``None`` return
+(tests/persistentkv_torch_extension.cu:319-336), backed by the HIP engine in
+``libpkv.so``.  Import it after adding this directory to ``sys.path``.
+
+``import torch`` comes first so that the native library binds to the HIP runtime torch
+already loaded.  There is no CPU fallback: importing fails if the native extension has
+not been built.
+"""
+from __future__ import annotations
+
+import importlib.util
+import os
+import sysconfig
+
+import torch  # noqa: F401  (must precede the native library, see the docstring)
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+EXTENSION_PATH = os.path.join(_HERE, "_pkv_torch" + sysconfig.get_config_var("EXT_SUFFIX"))
+LIBRARY_PATH = os.path.join(_HERE, "libpkv.so")
+
+
+def _load():
+    for path in (LIBRARY_PATH, EXTENSION_PATH):
+        if not os.path.exists(path):
+            raise ImportError(
+                f"PersistentKV native code is not built ({path} missing); run "
+                "`python -c 'import __graft_entry__ as g; g.build()'` or "
+                "`make -C persistentkv-attention_amd/csrc`")
+    spec = importlib.util.spec_from_file_location("_pkv_torch", EXTENSION_PATH)
+    module = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(module)
+    return module
+
+
+_ext = _load()
+
+paged_attention = _ext.paged_attention
+paged_attention_masked = _ext.paged_attention_masked
+paged_attention_indexed = _ext.paged_attention_indexed
+paged_attention_workqueue = _ext.paged_attention_workqueue
+workqueue_decode = _ext.workqueue_decode
+workqueue_merge = _ext.workqueue_merge
+
+HEAD_DIM = 128
+TILE_TOKENS = 32
+
+
+def workspace_floats(batch: int, num_q_heads: int, num_splits: int) -> int:
+    """fp32 workspace elements for a split launch (cuh:891-898; 0 when unsplit)."""
+    return 0 if num_splits <= 1 else batch * num_q_heads * num_splits * (2 + HEAD_DIM)
+
+
+def workqueue_workspace_floats(total_partial_slots: int, num_q_heads: int) -> int:
+    """fp32 workspace elements for a work-queue launch (cuh:915-927)."""
+    return total_partial_slots * num_q_heads * (2 + HEAD_DIM)
+
+
+__all__ = [
+    "paged_attention", "paged_attention_masked", "paged_attention_indexed",
+    "paged_attention_workqueue", "workqueue_decode", "workqueue_merge", "workspace_floats",
+    "workqueue_workspace_floats", "EXTENSION_PATH", "LIBRARY_PATH",
+]

@@ -1,0 +1,399 @@
+"""Serving-trace workloads for the PersistentKV engine (host side of the harness).
+
+Restates the trace mechanics of tests/benchmark_serving_trace.py (rounded_length :159-160,
+make_lengths :163-195, build_requests :232-282, build_steps :285-298, make_q_pool
+:301-309, the KV pool :1242-1251) and adds the five configurations the engine is
+measured on:
+
+  c1  B=1 paged decode, ctx 2048, G=4, fp16, page 16, no split (paged_attention)
+  c2  B=8 MHA (G=1), lengths U[1024, 8192], page 16, split 8 (paged_attention_masked)
+  c3  B=1 long-context trace, ctx {16384, 32768}, split 32, one token appended to the
+      tail page per step (paged_attention_indexed)
+  c4  B=8 bimodal continuous-batching trace, 20 work-queue splits (paged_attention_workqueue)
+  c5  B=64 Zipf(1.1) lengths, G=32 or 8, bf16, page 32, cost-model splits (work queue)
+
+Per-step metadata comes from the C++ builder in libpkv.so (pkv_native.build_workqueue);
+random values come from torch generators with the reference's seed offsets (pages +99,
+Q +2026, KV +7) so that every run of a configuration sees identical inputs.
+"""
+from __future__ import annotations
+
+import math
+from collections import deque
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+import pkv_native
+
+HEAD_DIM = 128
+DEFAULT_SEED = 20260623  # held-out seed of the reference's review runs
+
+
+@dataclass(frozen=True)
+class Request:
+    request_id: int
+    arrival: int
+    prompt_len: int
+    decode_len: int
+    physical_pages: tuple
+
+
+@dataclass(frozen=True)
+class StepState:
+    step: int
+    active_ids: tuple
+    lengths: tuple
+
+
+# ---------------------------------------------------------------------------------
+# Reference trace mechanics.
+# ---------------------------------------------------------------------------------
+def rounded_length(value: int, page_size: int = 16) -> int:
+    """benchmark_serving_trace.py:159-160."""
+    return max(page_size, ((value + page_size - 1) // page_size) * page_size)
+
+
+def _randint(gen, lo, hi_inclusive):
+    return int(torch.randint(lo, hi_inclusive + 1, (1,), generator=gen).item())
+
+
+def make_lengths(trace: str, requests: int, seed: int, page_size: int = 16):
+    """``[(prompt_len, decode_len)]`` per request; the reference's families
+    (benchmark_serving_trace.py:163-195) plus the c3/c4 families of this engine's
+    configurations, drawn with the same generator mechanics."""
+    gen = torch.Generator(device="cpu")
+    gen.manual_seed(seed)
+    result = []
+    for index in range(requests):
+        if trace == "uniform":
+            prompt = _randint(gen, 4096, 32768)
+            decode = _randint(gen, 16, 96)
+        elif trace == "bimodal":
+            if index % 4 == 0:
+                prompt = _randint(gen, 24576, 65536)
+                decode = _randint(gen, 32, 128)
+            else:
+                prompt = _randint(gen, 2048, 12288)
+                decode = _randint(gen, 8, 64)
+        elif trace == "zipf":
+            rank = _randint(gen, 1, 32)
+            prompt = int(2048 + 65536 / math.sqrt(rank))
+            jitter = _randint(gen, -512, 512)
+            prompt = max(1024, prompt + jitter)
+            decode = _randint(gen, 8, 128)
+        elif trace == "bucketed":
+            prompt = [8192, 16384, 32768, 65536][index % 4]
+            decode = _randint(gen, 32, 96)
+        elif trace == "homogeneous":
+            prompt = 32768
+            decode = _randint(gen, 32, 96)
+        elif trace == "bimodal_c4":
+            # 25 % long rows U[16384, 32768] (every 4th request, as in the reference's
+            # bimodal family), 75 % short rows U[256, 1024]; decode lengths as there.
+            if index % 4 == 0:
+                prompt = _randint(gen, 16384, 32768)
+                decode = _randint(gen, 32, 128)
+            else:
+                prompt = _randint(gen, 256, 1024)
+                decode = _randint(gen, 8, 64)
+        elif trace == "bucketed_c3":
+            prompt = [16384, 32768][index % 2]
+            decode = _randint(gen, 32, 96)
+        else:
+            raise ValueError(f"unknown trace: {trace}")
+        result.append((rounded_length(prompt, page_size), decode))
+    return result
+
+
+def build_requests(lengths, max_active, seed, hole_fraction, page_size=16, bucket_tokens=0,
+                   extra_tokens=0):
+    """Page allocation of benchmark_serving_trace.py:232-282: each request reserves its
+    rounded final length in pages; the pool holds ``ceil(total / (1 - holes))`` pages and
+    requests take consecutive slices of ``randperm(pool)`` drawn with ``seed + 99``.
+    ``extra_tokens`` reserves room for that many tokens beyond prompt + decode."""
+    logical = []
+    for prompt, decode in lengths:
+        exact = prompt + decode + extra_tokens
+        if bucket_tokens > 0:
+            reserved = rounded_length(((exact + bucket_tokens - 1) // bucket_tokens) * bucket_tokens,
+                                      page_size)
+        else:
+            reserved = rounded_length(exact, page_size)
+        logical.append(math.ceil(reserved / page_size))
+    total = sum(logical)
+    physical_pages = math.ceil(total / max(1e-6, 1.0 - hole_fraction))
+    ids = torch.randperm(physical_pages, generator=torch.Generator().manual_seed(seed + 99))
+    built, cursor = [], 0
+    for request_id, ((prompt, decode), pages) in enumerate(zip(lengths, logical)):
+        assigned = tuple(int(x) for x in ids[cursor:cursor + pages].tolist())
+        cursor += pages
+        built.append(Request(request_id, request_id // max_active, prompt, decode, assigned))
+    return built, physical_pages
+
+
+def build_steps(requests, max_active):
+    """Reference admission rule (benchmark_serving_trace.py:285-298): request i arrives at
+    ``i // max_active`` and ages from then on; each step serves the first ``max_active``
+    requests (by id) that are within their decode window."""
+    steps = []
+    max_step = max(req.arrival + req.decode_len for req in requests)
+    for step in range(max_step):
+        candidates = []
+        for req in requests:
+            generated = step - req.arrival
+            if 0 <= generated < req.decode_len:
+                candidates.append((req.request_id, req.prompt_len + generated))
+        candidates = candidates[:max_active]
+        if candidates:
+            active_ids, lengths = zip(*candidates)
+            steps.append(StepState(step, tuple(active_ids), tuple(lengths)))
+    return steps
+
+
+def build_steps_continuous(requests, max_active, max_steps):
+    """Continuous batching: every request is waiting at step 0; up to ``max_active`` are
+    served per step; a request retires after ``decode_len`` tokens and the next waiting
+    request is admitted at the following step."""
+    waiting = deque(requests)
+    active, generated, steps = [], {}, []
+    for step in range(max_steps):
+        while len(active) < max_active and waiting:
+            req = waiting.popleft()
+            active.append(req)
+            generated[req.request_id] = 0
+        if not active:
+            break
+        steps.append(StepState(step, tuple(r.request_id for r in active),
+                               tuple(r.prompt_len + generated[r.request_id] for r in active)))
+        for r in active:
+            generated[r.request_id] += 1
+        active = [r for r in active if generated[r.request_id] < r.decode_len]
+    return steps
+
+
+def zipf_lengths(count, seed, s=1.1, lo=128, hi=65536):
+    """``count`` lengths with P(L) proportional to L^-s on [lo, hi] (inverse CDF with a
+    float64 torch uniform drawn from ``seed``)."""
+    support = np.arange(lo, hi + 1, dtype=np.float64)
+    cdf = np.cumsum(support ** (-s))
+    cdf /= cdf[-1]
+    gen = torch.Generator().manual_seed(seed)
+    u = torch.rand(count, generator=gen, dtype=torch.float64).numpy()
+    return [int(support[min(int(np.searchsorted(cdf, x)), len(support) - 1)]) for x in u]
+
+
+# ---------------------------------------------------------------------------------
+# Configurations.
+# ---------------------------------------------------------------------------------
+@dataclass
+class Workload:
+    name: str
+    op: str                 # paged_attention | paged_attention_masked | _indexed | _workqueue
+    hq: int
+    hkv: int
+    page_size: int
+    dtype: torch.dtype
+    seed: int
+    requests: list
+    steps: list
+    physical_pages: int
+    splits: int = 1
+    auto_splits: bool = False
+    policy: int = pkv_native.POLICY_REFERENCE
+    append_kv: bool = False
+    fused_merge: bool = False
+    extra: dict = field(default_factory=dict)
+
+    @property
+    def group(self):
+        return self.hq // self.hkv
+
+    def kv_bytes(self, step_index):
+        """Algorithmic K+V bytes of one decode step:
+        sum(lengths) * Hkv * 128 * 2 (K and V) * element bytes (the reference's
+        useful_kv_mb_for_state, benchmark_serving_trace.py:511-513, in bytes)."""
+        elem = 2
+        return sum(self.steps[step_index].lengths) * self.hkv * HEAD_DIM * 2 * elem
+
+
+def config_c1(seed=DEFAULT_SEED):
+    """B=1, Hq 32 / Hkv 8, ctx 2048, page 16, 128 pages drawn from a 4096-page pool."""
+    gen = torch.Generator().manual_seed(seed + 99)
+    pages = tuple(int(x) for x in torch.randperm(4096, generator=gen)[:128].tolist())
+    req = Request(0, 0, 2048, 1, pages)
+    return Workload("c1", "paged_attention", 32, 8, 16, torch.float16, seed, [req],
+                    [StepState(0, (0,), (2048,))], 4096, splits=1)
+
+
+def config_c2(seed=DEFAULT_SEED):
+    """B=8 MHA (Hq = Hkv = 32), lengths U[1024, 8192], pool 1.5x the used pages, split 8."""
+    gen = torch.Generator().manual_seed(seed)
+    lengths = [int(x) for x in torch.randint(1024, 8193, (8,), generator=gen).tolist()]
+    pages = [math.ceil(n / 16) for n in lengths]
+    physical = math.ceil(1.5 * sum(pages))
+    ids = torch.randperm(physical, generator=torch.Generator().manual_seed(seed + 99))
+    reqs, cursor = [], 0
+    for i, (n, p) in enumerate(zip(lengths, pages)):
+        reqs.append(Request(i, 0, n, 1, tuple(int(x) for x in ids[cursor:cursor + p].tolist())))
+        cursor += p
+    return Workload("c2", "paged_attention_masked", 32, 32, 16, torch.float16, seed, reqs,
+                    [StepState(0, tuple(range(8)), tuple(lengths))], physical, splits=8)
+
+
+def config_c3(seed=DEFAULT_SEED, steps=64):
+    """B=1 long-context trace: 16 requests with prompts alternating 16384 / 32768 served one
+    at a time, 64 steps, split 32, each step appending one token's K/V."""
+    lengths = make_lengths("bucketed_c3", 16, seed)
+    reqs, physical = build_requests(lengths, 1, seed, 0.0)
+    st = build_steps_continuous(reqs, 1, steps)
+    return Workload("c3", "paged_attention_indexed", 32, 8, 16, torch.float16, seed, reqs, st,
+                    physical, splits=32, append_kv=True)
+
+
+def config_c4(seed=DEFAULT_SEED, steps=48, fused_merge=False):
+    """B=8 bimodal continuous batching: 24 requests (every 4th long, U[16384, 32768];
+    others U[256, 1024]), max-active 8, 48 steps, 20 fixed work-queue splits."""
+    lengths = make_lengths("bimodal_c4", 24, seed)
+    reqs, physical = build_requests(lengths, 8, seed, 0.0)
+    st = build_steps_continuous(reqs, 8, steps)
+    return Workload("c4", "paged_attention_workqueue", 32, 8, 16, torch.float16, seed, reqs, st,
+                    physical, splits=20, fused_merge=fused_merge)
+
+
+def config_c5(hkv=1, seed=DEFAULT_SEED, steps=48, batch=64):
+    """B=64 Zipf(1.1) lengths in [128, 65536], Hq 32 with Hkv 1 (G=32) or 4 (G=8), bf16,
+    page 32, 10 % free-page holes, 48 steps, work queue with the MI355X split planner."""
+    prompts = zipf_lengths(batch, seed)
+    lengths = [(rounded_length(p, 32), steps) for p in prompts]
+    reqs, physical = build_requests(lengths, batch, seed, 0.10, page_size=32)
+    reqs = [Request(r.request_id, 0, r.prompt_len, r.decode_len, r.physical_pages) for r in reqs]
+    st = build_steps(reqs, batch)[:steps]
+    return Workload(f"c5_g{32 // hkv}", "paged_attention_workqueue", 32, hkv, 32, torch.bfloat16,
+                    seed, reqs, st, physical, splits=1, auto_splits=True,
+                    policy=pkv_native.POLICY_MI355X)
+
+
+CONFIGS = {"c1": config_c1, "c2": config_c2, "c3": config_c3, "c4": config_c4,
+           "c5_g32": lambda **kw: config_c5(hkv=1, **kw), "c5_g8": lambda **kw: config_c5(hkv=4, **kw)}
+
+
+# ---------------------------------------------------------------------------------
+# Device state and per-step metadata.
+# ---------------------------------------------------------------------------------
+def make_kv_pool(w: Workload, device, seed_offset=7):
+    """K and V pools ``[pages, Hkv, page_size, 128]`` ~ N(0, 1) (reference :1242-1251)."""
+    gen = torch.Generator(device=device)
+    gen.manual_seed(w.seed + seed_offset)
+    k = torch.randn(w.physical_pages, w.hkv, w.page_size, HEAD_DIM, generator=gen, device=device,
+                    dtype=w.dtype)
+    v = torch.randn(w.physical_pages, w.hkv, w.page_size, HEAD_DIM, generator=gen, device=device,
+                    dtype=w.dtype)
+    return k, v
+
+
+def make_q_pool(w: Workload, device):
+    """Q ``[steps, requests, Hq, 128]`` ~ N(0, 1) drawn on the CPU with ``seed + 2026``
+    (reference :301-309), then moved to ``device``."""
+    gen = torch.Generator().manual_seed(w.seed + 2026)
+    q = torch.randn(len(w.steps), len(w.requests), w.hq, HEAD_DIM, generator=gen,
+                    dtype=torch.float32)
+    return q.to(w.dtype).to(device)
+
+
+@dataclass
+class StepMeta:
+    op: str
+    bucket_length: int
+    block_table: torch.Tensor
+    seq_lens: torch.Tensor
+    q_indices: torch.Tensor
+    out_indices: torch.Tensor
+    output: torch.Tensor
+    splits: int
+    work_items: torch.Tensor | None = None
+    split_offsets: torch.Tensor | None = None
+    merge_counters: torch.Tensor | None = None
+    total_partial_slots: int = 0
+    num_tasks: int = 0
+    kv_bytes: int = 0
+
+
+def compile_step(w: Workload, step_index: int, device) -> StepMeta:
+    """Block table, lengths, indices and (work-queue op) the compact work queue of one
+    step, built on the host by libpkv.so and copied to ``device``."""
+    st = w.steps[step_index]
+    by_id = {r.request_id: r for r in w.requests}
+    page_lists = [by_id[i].physical_pages for i in st.active_ids]
+    t = lambda a: torch.as_tensor(np.ascontiguousarray(a), dtype=torch.int32).to(device)
+    n = len(st.active_ids)
+    output = torch.empty(n, w.hq, HEAD_DIM, device=device, dtype=w.dtype)
+    if w.op == "paged_attention_workqueue":
+        meta = pkv_native.build_workqueue(list(st.lengths), list(st.active_ids), page_lists,
+                                          w.page_size, w.splits, w.auto_splits, w.hkv, w.policy)
+        return StepMeta(w.op, meta["bucket_length"], t(meta["block_table"]), t(meta["seq_lens"]),
+                        t(meta["q_indices"]), t(meta["out_indices"]), output, meta["splits"],
+                        t(meta["work_items"]), t(meta["split_offsets"]),
+                        torch.zeros(n, w.hkv, device=device, dtype=torch.int32),
+                        meta["total_partial_slots"], int(meta["work_items"].shape[0]),
+                        w.kv_bytes(step_index))
+    bucket = max(st.lengths)
+    cols = math.ceil(bucket / w.page_size)
+    table = np.array([list(p[:cols]) + [p[-1]] * (cols - len(p[:cols])) for p in page_lists],
+                     dtype=np.int32)
+    return StepMeta(w.op, bucket, t(table), t(np.array(st.lengths)), t(np.array(st.active_ids)),
+                    t(np.arange(n)), output, w.splits, kv_bytes=w.kv_bytes(step_index))
+
+
+def workspace_for(w: Workload, metas, device):
+    floats = 1
+    for m in metas:
+        if m.op == "paged_attention_workqueue":
+            floats = max(floats, m.total_partial_slots * w.hq * (2 + HEAD_DIM))
+        elif m.splits > 1:
+            floats = max(floats, len(m.seq_lens) * w.hq * m.splits * (2 + HEAD_DIM))
+    return torch.empty(floats, device=device, dtype=torch.float32)
+
+
+def run_step(ext, w: Workload, meta: StepMeta, step_index: int, q_pool, k_pages, v_pages,
+             workspace):
+    """One decode step through the op the workload names; returns ``meta.output``."""
+    q_source = q_pool[step_index]
+    if meta.op == "paged_attention_workqueue":
+        ext.paged_attention_workqueue(q_source, k_pages, v_pages, meta.block_table, meta.seq_lens,
+                                      meta.work_items, meta.split_offsets, meta.merge_counters,
+                                      meta.q_indices, meta.out_indices, meta.output, workspace,
+                                      meta.bucket_length, w.page_size, meta.total_partial_slots,
+                                      w.fused_merge)
+    elif meta.op == "paged_attention_indexed":
+        ext.paged_attention_indexed(q_source, k_pages, v_pages, meta.block_table, meta.seq_lens,
+                                    meta.q_indices, meta.out_indices, meta.output, workspace,
+                                    meta.bucket_length, w.page_size, meta.splits)
+    elif meta.op == "paged_attention_masked":
+        q = q_source.index_select(0, meta.q_indices.long()).contiguous()
+        ext.paged_attention_masked(q, k_pages, v_pages, meta.block_table, meta.seq_lens,
+                                   meta.output, workspace, meta.bucket_length, w.page_size,
+                                   meta.splits)
+    elif meta.op == "paged_attention":
+        q = q_source.index_select(0, meta.q_indices.long()).contiguous()
+        ext.paged_attention(q, k_pages, v_pages, meta.block_table, meta.output, workspace,
+                            meta.bucket_length, w.page_size, meta.splits)
+    else:
+        raise ValueError(meta.op)
+    return meta.output
+
+
+def append_step_kv(w: Workload, step_index: int, k_pages, v_pages, seed_offset=11):
+    """Writes the K/V of each active row's newest token (position length - 1) into its
+    tail page, with values drawn from ``seed + seed_offset + step``."""
+    st = w.steps[step_index]
+    by_id = {r.request_id: r for r in w.requests}
+    gen = torch.Generator().manual_seed(w.seed + seed_offset + step_index)
+    for rid, length in zip(st.active_ids, st.lengths):
+        pos = length - 1
+        page = by_id[rid].physical_pages[pos // w.page_size]
+        k_new = torch.randn(w.hkv, HEAD_DIM, generator=gen).to(w.dtype)
+        v_new = torch.randn(w.hkv, HEAD_DIM, generator=gen).to(w.dtype)
+        k_pages[page, :, pos % w.page_size] = k_new.to(k_pages.device)
+        v_pages[page, :, pos % w.page_size] = v_new.to(v_pages.device)

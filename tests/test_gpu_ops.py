@@ -1,0 +1,308 @@
+"""Parity of the four ops (HIP engine) with the repack + fp32 SDPA oracle.
+
+Tolerances: max-abs 2e-3 (north star) and mean-abs 3e-4 (tests/smoke_test.cu:106) in
+fp16 and bf16.  Case shapes follow the reference's smoke cases (tests/smoke_test.cu:
+486-493) and extend them to every G in [1, 32], bf16, generic page sizes, ragged and
+empty rows, indexed Q/O rows and the compact work queue.
+"""
+import pytest
+import torch
+
+import pkv_native
+from conftest import MAX_ABS, MEAN_ABS
+from oracle import attention as oracle
+from paged_cases import errors, make_case
+
+pytestmark = pytest.mark.gpu
+
+F16, BF16 = torch.float16, torch.bfloat16
+
+
+def _dev(case, dev):
+    return (case.q.to(dev), case.k_pages.to(dev), case.v_pages.to(dev), case.block_table.to(dev),
+            case.seq_lens.to(dev))
+
+
+def _ws(batch, hq, splits, dev):
+    return torch.empty(max(1, batch * hq * splits * 130) if splits > 1 else 0,
+                       dtype=torch.float32, device=dev)
+
+
+# (B, Hq, Hkv, context, page_size, splits, dtype, table)
+PAGED = [
+    (1, 32, 8, 2048, 16, 1, F16, "random"),      # config c1 shape
+    (1, 4, 1, 257, 16, 1, F16, "contiguous"),    # smoke cases (:486-493)
+    (1, 8, 2, 257, 16, 4, F16, "reversed"),
+    (1, 32, 8, 512, 16, 4, F16, "random"),
+    (2, 32, 8, 259, 32, 3, F16, "reversed"),
+    (1, 32, 4, 511, 16, 4, F16, "random"),       # G = 8
+    (1, 8, 8, 256, 16, 2, F16, "random"),        # G = 1
+    (1, 32, 2, 700, 16, 5, F16, "random"),       # G = 16
+    (1, 32, 1, 1000, 32, 8, BF16, "random"),     # G = 32, bf16
+    (3, 12, 4, 123, 8, 2, F16, "random"),        # G = 3, page 8 (generic pager)
+    (2, 8, 2, 77, 5, 1, F16, "random"),          # page 5 (generic pager)
+    (1, 16, 16, 64, 64, 2, BF16, "random"),
+    (2, 24, 8, 100, 16, 1, BF16, "random"),
+    (1, 32, 8, 8192, 16, 1, F16, "canonical"),   # canonical fragmented table
+    (1, 32, 8, 8192, 16, 16, F16, "canonical"),
+]
+
+
+@pytest.mark.parametrize("b,hq,hkv,ctx,ps,splits,dtype,table", PAGED)
+def test_paged_attention(ext, gpu, b, hq, hkv, ctx, ps, splits, dtype, table):
+    case = make_case([ctx] * b, hq, hkv, ps, dtype, seed=ctx + splits, table=table)
+    q, k, v, bt, _ = _dev(case, gpu)
+    out = torch.full((b, hq, 128), float("nan"), dtype=dtype, device=gpu)
+    ext.paged_attention(q, k, v, bt, out, _ws(b, hq, splits, gpu), ctx, ps, splits)
+    torch.cuda.synchronize()
+    ref = oracle.paged_decode(case.q, case.k_pages, case.v_pages, case.block_table, case.seq_lens)
+    mx, mean = errors(out, ref)
+    assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
+
+
+# (lengths, Hq, Hkv, page_size, splits, dtype)
+MASKED = [
+    ([1, 31, 33, 500], 32, 8, 16, 1, F16),
+    ([1, 31, 33, 500], 32, 8, 16, 4, F16),
+    ([1, 31, 33, 500], 32, 8, 16, 16, BF16),
+    ([5, 700, 64, 129, 1024], 8, 8, 16, 8, F16),
+    ([300, 17], 32, 4, 8, 3, F16),
+    ([0, 45, 96], 32, 8, 16, 2, F16),            # empty row -> zeros
+    ([1024, 7000, 333], 32, 1, 32, 12, BF16),
+]
+
+
+@pytest.mark.parametrize("lengths,hq,hkv,ps,splits,dtype", MASKED)
+def test_paged_attention_masked(ext, gpu, lengths, hq, hkv, ps, splits, dtype):
+    case = make_case(lengths, hq, hkv, ps, dtype, seed=sum(lengths) + splits)
+    q, k, v, bt, sl = _dev(case, gpu)
+    b, bucket = len(lengths), max(max(lengths), 32 * splits)
+    if bt.shape[1] * ps < bucket:  # table must cover the bucket context
+        bt = torch.cat([bt, bt[:, -1:].expand(b, -(-bucket // ps) - bt.shape[1])], 1).contiguous()
+    out = torch.full((b, hq, 128), float("nan"), dtype=dtype, device=gpu)
+    ext.paged_attention_masked(q, k, v, bt, sl, out, _ws(b, hq, splits, gpu), bucket, ps, splits)
+    torch.cuda.synchronize()
+    ref = oracle.paged_decode(case.q, case.k_pages, case.v_pages, case.block_table, case.seq_lens)
+    mx, mean = errors(out, ref)
+    assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
+
+
+@pytest.mark.parametrize("splits,dtype", [(1, F16), (6, F16), (3, BF16)])
+def test_paged_attention_indexed(ext, gpu, splits, dtype):
+    lengths = [400, 33, 1200]
+    case = make_case(lengths, 32, 8, 16, dtype, seed=splits, q_rows=5)
+    q, k, v, bt, sl = _dev(case, gpu)
+    q_idx = torch.tensor([4, 0, 2], dtype=torch.int32)
+    o_idx = torch.tensor([3, 0, 5], dtype=torch.int32)
+    out = torch.full((6, 32, 128), 7.0, dtype=dtype, device=gpu)  # rows 1, 2, 4 untouched
+    ext.paged_attention_indexed(q, k, v, bt, sl, q_idx.to(gpu), o_idx.to(gpu), out,
+                                _ws(3, 32, splits, gpu), max(lengths), 16, splits)
+    torch.cuda.synchronize()
+    ref = oracle.paged_decode(case.q, case.k_pages, case.v_pages, case.block_table, case.seq_lens,
+                              q_idx, o_idx, 6)
+    mx, mean = errors(out, ref)
+    assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
+    assert torch.all(out[[1, 2, 4]].float().cpu() == 7.0)
+
+
+def _queue(case, requested, auto, hkv, policy=pkv_native.POLICY_REFERENCE, request_ids=None):
+    ids = request_ids or list(range(len(case.seq_lens)))
+    return pkv_native.build_workqueue(case.seq_lens.tolist(), ids, case.page_lists, case.page_size,
+                                      requested, auto, hkv, policy)
+
+
+def _run_queue(ext, gpu, case, meta, hq, hkv, fused, out_rows=None):
+    t = lambda a: torch.as_tensor(a, dtype=torch.int32, device=gpu)
+    b = len(meta["seq_lens"])
+    out = torch.full((out_rows or b, hq, 128), float("nan"), dtype=case.q.dtype, device=gpu)
+    ws = torch.empty(meta["total_partial_slots"] * hq * 130, dtype=torch.float32, device=gpu)
+    counters = torch.zeros(b, hkv, dtype=torch.int32, device=gpu)
+    ext.paged_attention_workqueue(
+        case.q.to(gpu), case.k_pages.to(gpu), case.v_pages.to(gpu), t(meta["block_table"]),
+        t(meta["seq_lens"]), t(meta["work_items"]), t(meta["split_offsets"]), counters,
+        t(meta["q_indices"]), t(meta["out_indices"]), out, ws, meta["bucket_length"],
+        case.page_size, meta["total_partial_slots"], fused)
+    torch.cuda.synchronize()
+    return out, counters
+
+
+# (lengths, Hq, Hkv, page_size, requested splits, auto, dtype)
+QUEUE = [
+    ([300, 17000, 700, 256], 32, 8, 16, 20, False, F16),   # c4-like; empty splits on short rows
+    ([300, 17000, 700, 256], 32, 8, 16, 1, True, F16),     # reference auto policy
+    ([64, 33, 1], 32, 8, 16, 20, False, F16),              # more splits than tiles everywhere
+    ([5000, 120], 32, 32, 16, 8, False, F16),              # G = 1
+    ([2000, 4000, 900], 32, 1, 32, 12, False, BF16),       # G = 32 (MQA), page 32
+    ([1500, 77], 32, 4, 32, 6, False, BF16),               # G = 8
+    ([999, 1001], 20, 4, 8, 5, False, F16),                # G = 5, page 8
+]
+
+
+@pytest.mark.parametrize("fused", [False, True])
+@pytest.mark.parametrize("lengths,hq,hkv,ps,req,auto,dtype", QUEUE)
+def test_paged_attention_workqueue(ext, gpu, lengths, hq, hkv, ps, req, auto, dtype, fused):
+    case = make_case(lengths, hq, hkv, ps, dtype, seed=len(lengths) * 7 + req, q_rows=len(lengths) + 2)
+    ids = [len(lengths) + 1 - i for i in range(len(lengths))]  # q rows in reverse order
+    meta = _queue(case, req, auto, hkv, request_ids=ids)
+    out, counters = _run_queue(ext, gpu, case, meta, hq, hkv, fused)
+    ref = oracle.paged_decode(case.q, case.k_pages, case.v_pages, meta["block_table"],
+                              meta["seq_lens"], meta["q_indices"], meta["out_indices"])
+    mx, mean = errors(out, ref)
+    assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
+    assert int(counters.abs().sum()) == 0  # the fused merge leaves the counters at zero
+
+
+def test_workqueue_mi355x_policy(ext, gpu):
+    lengths = [300, 17000, 700, 256, 31000, 900, 512, 640]
+    case = make_case(lengths, 32, 8, 16, F16, seed=99)
+    meta = _queue(case, 1, True, 8, policy=pkv_native.POLICY_MI355X)
+    out, _ = _run_queue(ext, gpu, case, meta, 32, 8, False)
+    ref = oracle.paged_decode(case.q, case.k_pages, case.v_pages, meta["block_table"],
+                              meta["seq_lens"], meta["q_indices"], meta["out_indices"])
+    mx, mean = errors(out, ref)
+    assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
+
+
+def test_workqueue_stages_equal_combined(ext, gpu):
+    lengths = [3000, 200, 9000]
+    case = make_case(lengths, 32, 8, 16, F16, seed=5)
+    meta = _queue(case, 20, False, 8)
+    combined, _ = _run_queue(ext, gpu, case, meta, 32, 8, False)
+    t = lambda a: torch.as_tensor(a, dtype=torch.int32, device=gpu)
+    staged = torch.full_like(combined, float("nan"))
+    ws = torch.empty(meta["total_partial_slots"] * 32 * 130, dtype=torch.float32, device=gpu)
+    ext.workqueue_decode(case.q.to(gpu), case.k_pages.to(gpu), case.v_pages.to(gpu),
+                         t(meta["block_table"]), t(meta["seq_lens"]), t(meta["work_items"]),
+                         t(meta["split_offsets"]), t(meta["q_indices"]), ws, meta["bucket_length"],
+                         16, meta["total_partial_slots"])
+    ext.workqueue_merge(t(meta["seq_lens"]), t(meta["split_offsets"]), t(meta["out_indices"]),
+                        staged, ws, meta["total_partial_slots"])
+    torch.cuda.synchronize()
+    assert torch.equal(staged, combined)
+
+
+def test_workqueue_matches_indexed_split_grid(ext, gpu):
+    """Fixed S splits per row give the same tile ranges in both routes, so the outputs
+    are bit-identical (empty slots are neutral in one route and skipped in the other)."""
+    lengths = [100, 2500, 40]
+    splits = 9
+    case = make_case(lengths, 32, 8, 16, F16, seed=11)
+    meta = _queue(case, splits, False, 8)
+    queue_out, _ = _run_queue(ext, gpu, case, meta, 32, 8, False)
+    q, k, v, bt, sl = _dev(case, gpu)
+    idx = torch.arange(3, dtype=torch.int32, device=gpu)
+    grid_out = torch.full_like(queue_out, float("nan"))
+    ext.paged_attention_indexed(q, k, v, bt, sl, idx, idx, grid_out, _ws(3, 32, splits, gpu),
+                                max(lengths), 16, splits)
+    torch.cuda.synchronize()
+    assert torch.equal(queue_out, grid_out)
+
+
+def test_split_partial_states_match_oracle(ext, gpu):
+    """The workspace holds the reference's partial-state format (cuh:615-632): per
+    (row, head, split) m in natural-log units of the scaled score, l, acc[128]."""
+    b, hq, hkv, ctx, splits = 2, 8, 2, 700, 5
+    case = make_case([ctx] * b, hq, hkv, 16, F16, seed=3)
+    q, k, v, bt, _ = _dev(case, gpu)
+    ws = _ws(b, hq, splits, gpu)
+    out = torch.empty(b, hq, 128, dtype=F16, device=gpu)
+    ext.paged_attention(q, k, v, bt, out, ws, ctx, 16, splits)
+    torch.cuda.synchronize()
+    n = b * hq * splits
+    w = ws.cpu()
+    m, l, acc = w[:n].view(b, hq, splits), w[n:2 * n].view(b, hq, splits), w[2 * n:].view(b, hq, splits, 128)
+    ranges = oracle.split_bounds(-(-ctx // 32), splits)
+    for row in range(b):
+        kk, vv = oracle.gather_row(case.k_pages, case.v_pages, case.block_table[row], ctx)
+        rm, rl, racc = oracle.split_partials(case.q[row], kk, vv, ranges)
+        assert torch.allclose(m[row].double(), torch.from_numpy(rm), atol=1e-4, rtol=1e-4)
+        # l and acc are relative to each split's own max; compare after normalising.
+        assert torch.allclose(l[row].double(), torch.from_numpy(rl), rtol=2e-3, atol=1e-3)
+        assert torch.allclose(acc[row].double() / l[row].double()[..., None],
+                              torch.from_numpy(racc / rl[..., None]), atol=2e-3)
+
+
+def test_deterministic_and_page_relocation_invariant(ext, gpu):
+    """Moving every page to another physical slot (and updating the table) reads the same
+    logical tokens in the same order, so the output is bit-identical."""
+    lengths = [1500, 40, 777]
+    case = make_case(lengths, 32, 8, 16, F16, seed=21, extra_pages=40)
+    meta = _queue(case, 20, False, 8)
+    a, _ = _run_queue(ext, gpu, case, meta, 32, 8, False)
+    b, _ = _run_queue(ext, gpu, case, meta, 32, 8, False)
+    assert torch.equal(a, b)
+    perm = torch.randperm(case.k_pages.shape[0], generator=torch.Generator().manual_seed(1))
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(len(perm))
+    moved = make_case(lengths, 32, 8, 16, F16, seed=21, extra_pages=40)
+    moved.k_pages = case.k_pages[inv]  # physical slot p now holds old page inv[p]
+    moved.v_pages = case.v_pages[inv]
+    moved.page_lists = [[int(perm[p]) for p in row] for row in case.page_lists]
+    moved.q = case.q
+    meta2 = _queue(moved, 20, False, 8)
+    c, _ = _run_queue(ext, gpu, moved, meta2, 32, 8, False)
+    assert torch.equal(a, c)
+
+
+def test_split_count_invariance(ext, gpu):
+    ctx = 4096
+    case = make_case([ctx], 32, 8, 16, F16, seed=8)
+    q, k, v, bt, _ = _dev(case, gpu)
+    outs = []
+    for s in (1, 2, 7, 32, 128):
+        out = torch.empty(1, 32, 128, dtype=F16, device=gpu)
+        ext.paged_attention(q, k, v, bt, out, _ws(1, 32, s, gpu), ctx, 16, s)
+        outs.append(out.float())
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert (o - outs[0]).abs().max().item() < 1e-3
+
+
+def test_hip_graph_replay(ext, gpu):
+    lengths = [2000, 300, 5000, 64]
+    case = make_case(lengths, 32, 8, 16, F16, seed=13)
+    meta = _queue(case, 20, False, 8)
+    t = lambda a: torch.as_tensor(a, dtype=torch.int32, device=gpu)
+    args = [case.q.to(gpu), case.k_pages.to(gpu), case.v_pages.to(gpu), t(meta["block_table"]),
+            t(meta["seq_lens"]), t(meta["work_items"]), t(meta["split_offsets"]),
+            torch.zeros(4, 8, dtype=torch.int32, device=gpu), t(meta["q_indices"]),
+            t(meta["out_indices"])]
+    out = torch.zeros(4, 32, 128, dtype=F16, device=gpu)
+    ws = torch.empty(meta["total_partial_slots"] * 32 * 130, dtype=torch.float32, device=gpu)
+    tail = [meta["bucket_length"], 16, meta["total_partial_slots"], False]
+    ext.paged_attention_workqueue(*args, out, ws, *tail)
+    torch.cuda.synchronize()
+    eager = out.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            ext.paged_attention_workqueue(*args, out, ws, *tail)
+    torch.cuda.synchronize()
+    for _ in range(4):
+        out.zero_()
+        ws.fill_(3.0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+
+
+def test_validation_errors(ext, gpu):
+    case = make_case([64], 32, 8, 16, F16)
+    q, k, v, bt, sl = _dev(case, gpu)
+    out = torch.empty(1, 32, 128, dtype=F16, device=gpu)
+    empty = torch.empty(0, dtype=torch.float32, device=gpu)
+    with pytest.raises(RuntimeError, match="num_splits"):
+        ext.paged_attention(q, k, v, bt, out, _ws(1, 32, 4, gpu), 64, 16, 4)  # 4 > ceil(64/32)
+    with pytest.raises(RuntimeError, match="workspace"):
+        ext.paged_attention(q, k, v, bt, out, empty, 64, 16, 2)
+    with pytest.raises(RuntimeError, match="G=Hq/Hkv"):
+        q66 = torch.zeros(1, 66, 128, dtype=F16, device=gpu)
+        ext.paged_attention(q66, k[:, :2].contiguous(), v[:, :2].contiguous(), bt,
+                            torch.empty(1, 66, 128, dtype=F16, device=gpu), empty, 64, 16, 1)
+    with pytest.raises(RuntimeError, match="wrong dtype"):
+        ext.paged_attention(q, k.to(BF16), v.to(BF16), bt, out, empty, 64, 16, 1)
+    with pytest.raises(RuntimeError, match="block_table has"):
+        ext.paged_attention(q, k, v, bt, out, empty, 4096, 16, 1)
