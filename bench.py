@@ -1,0 +1,177 @@
+"""Benchmark of the MI355X PersistentKV decode engine on its headline workload.
+
+Workload: bimodal continuous-batching trace, 24 requests,
+max-active 8, 48 decode steps, Hq 32 / Hkv 8 (G=4), D 128, fp16, page 16, 20 fixed
+work-queue splits with metadata precomputed by the host builder.  One "step" is one
+``paged_attention_workqueue`` call (decode kernel + LSE merge) over one decode step of
+the trace; timed step k replays trace step k mod 48.
+
+Cache basis: the KV pool is replicated ``--rotations`` times and consecutive timed steps
+read different replicas, so a step's pages have been evicted from the 256 MB Infinity
+Cache by the time they are read again (every figure is HBM-cold).
+
+Reported (one JSON line):
+  value        effective KV read bandwidth over the timed steps, GB/s (algorithmic
+               bytes: sum of active lengths * Hkv * 128 * 2 (K,V) * 2 bytes per step,
+               the reference's useful_kv_mb_for_state, tests/benchmark_serving_trace.py:511-513)
+  ms_per_step  mean wall time per step between the synchronised bracket points
+  roofline     decode kernel alone, timed with HIP events on its launch stream
+  cpu_baseline repack + fp32 SDPA (the reference's CPU path, restated in oracle/) on a
+               bounded sample of the same steps on the host cores
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "persistentkv-attention_amd")
+for _p in (PKG, ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "decode-step µs + effective KV HBM GB/s (% of peak), B8 bimodal G=4 fp16"
+HBM_PEAK_GBPS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "c4_decode_traffic.json")
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=96)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--rotations", type=int, default=4, help="KV pool replicas (cold-cache basis)")
+    p.add_argument("--fused-merge", action="store_true", help="single-launch fused merge variant")
+    p.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time budget")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--seed", type=int, default=20260623)
+    return p.parse_args()
+
+
+def cpu_baseline(w, q_pool_cpu, k_cpu, v_cpu, metas, budget_s):
+    """Repack + fp32 SDPA on the host for consecutive trace steps until the budget is spent."""
+    import torch
+
+    from oracle import attention as oracle
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    done_bytes, elapsed, steps = 0, 0.0, 0
+    for i, meta in enumerate(metas):
+        t0 = time.perf_counter()
+        oracle.paged_decode(q_pool_cpu[i], k_cpu, v_cpu, meta.block_table.cpu(), meta.seq_lens.cpu(),
+                            meta.q_indices.cpu(), meta.out_indices.cpu())
+        elapsed += time.perf_counter() - t0
+        done_bytes += meta.kv_bytes
+        steps += 1
+        if elapsed >= budget_s:
+            break
+    return {"value": round(done_bytes / elapsed / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"trace steps 0..{steps - 1} of {w.name} ({done_bytes / 1e6:.0f} MB of KV), "
+                      f"{elapsed / steps * 1e3:.1f} ms/step, torch CPU SDPA fp32"}
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the engine has no multi-GPU path in this build "
+              "(see DESIGN.md for how it would shard); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import persistentkv_torch_ext as ext
+    import pkv_workloads as wl
+
+    dev = torch.device("cuda:0")
+    w = wl.config_c4(seed=args.seed, fused_merge=args.fused_merge)
+    metas = [wl.compile_step(w, i, dev) for i in range(len(w.steps))]
+    ws = wl.workspace_for(w, metas, dev)
+    q_pool = wl.make_q_pool(w, dev)
+    k0, v0 = wl.make_kv_pool(w, dev)
+    pools = [(k0, v0)] + [(k0.clone(), v0.clone()) for _ in range(args.rotations - 1)]
+    torch.cuda.synchronize()
+    n_trace = len(w.steps)
+
+    def step(k):
+        i = k % n_trace
+        kp, vp = pools[k % len(pools)]
+        wl.run_step(ext, w, metas[i], i, q_pool, kp, vp, ws)
+
+    for k in range(args.warmup):
+        step(k)
+    torch.cuda.synchronize()
+
+    # Timed region: exactly args.steps steps, synchronised on both sides.
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record()
+    for k in range(args.steps):
+        step(k)
+    stop.record()
+    torch.cuda.synchronize()
+    wall_s = time.perf_counter() - t0
+    gpu_ms = start.elapsed_time(stop)
+    total_bytes = sum(metas[k % n_trace].kv_bytes for k in range(args.steps))
+
+    # Decode kernel alone (stage 1 of the op), one event pair per launch on its stream.
+    dec_ms, dec_bytes = [], []
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    for k in range(args.steps):
+        i = k % n_trace
+        m = metas[i]
+        kp, vp = pools[k % len(pools)]
+        evs[k][0].record()
+        ext.workqueue_decode(q_pool[i], kp, vp, m.block_table, m.seq_lens, m.work_items,
+                             m.split_offsets, m.q_indices, ws, m.bucket_length, w.page_size,
+                             m.total_partial_slots)
+        evs[k][1].record()
+        dec_bytes.append(m.kv_bytes)
+    torch.cuda.synchronize()
+    dec_ms = [a.elapsed_time(b) for a, b in evs]
+    achieved = sum(dec_bytes) / (sum(dec_ms) / 1e3) / 1e9
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as fh:
+            traffic = json.load(fh).get("hbm_bytes_per_launch")
+
+    value = total_bytes / (gpu_ms / 1e3) / 1e9
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_s * 1e3 / args.steps, 4),
+        "step_us_gpu": round(gpu_ms * 1e3 / args.steps, 2),
+        "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBPS, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {"workload": "c4_bimodal_workqueue", "requests": 24, "max_active": 8,
+                   "trace_steps": n_trace, "hq": 32, "hkv": 8, "head_dim": 128, "page_size": 16,
+                   "splits": 20, "fused_merge": bool(args.fused_merge),
+                   "mean_kv_mb_per_step": round(sum(m.kv_bytes for m in metas) / n_trace / 1e6, 2),
+                   "cache_basis": f"HBM-cold ({len(pools)} rotated KV pool replicas)"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": traffic, "kernel": "decode_kernel<Half,1,true,kQueue>",
+                     "mean_launch_us": round(sum(dec_ms) / len(dec_ms) * 1e3, 2)},
+    }
+    if not args.no_cpu_baseline:
+        q_cpu = q_pool.cpu()
+        result["cpu_baseline"] = cpu_baseline(w, q_cpu, k0.cpu(), v0.cpu(), metas, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

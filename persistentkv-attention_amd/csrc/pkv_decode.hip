@@ -113,6 +113,13 @@ struct DecodeArgs {
 // ---------------------------------------------------------------------------------
 __device__ inline int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
+__device__ inline void* uniform_ptr(const void* p) {
+  const uint64_t v = (uint64_t)p;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+  return (void*)(((uint64_t)hi << 32) | lo);
+}
+
 __device__ inline int row_length(const DecodeArgs& a, int row) {
   int len = a.seq_lens ? a.seq_lens[row] : a.context;
   // The reference trusts seq_lens (cuh:217-219); clamping to the table width keeps
@@ -144,26 +151,57 @@ __device__ inline void page_of(const DecodeArgs& a, int token, int& logical, int
 __device__ inline int v_slot_token(int g, int j) { return (j >> 2) * 16 + 4 * g + (j & 3); }
 
 // ---------------------------------------------------------------------------------
-// Page loaders.  FastPager handles page sizes that are multiples of 16: a 16-token
-// block then lies inside one page, so its page id is wave-uniform (scalar load) and a
-// per-block buffer descriptor bounds every lane's access.  GenericPager handles any
-// other page size with per-lane table lookups and predicated loads.
+// Cross-lane helpers.  Lanes l, l^16, l^32, l^48 hold the same head in the score
+// layout.  These run on the first tile, on the rare rescale and once per range, so the
+// LDS-routed shuffles are off the hot path.  (v_permlane{16,32}_swap would avoid LDS, but
+// the compiler folds max/sum of the two results of a swap with identical operands into a
+// single operand, which drops the exchange.)
 // ---------------------------------------------------------------------------------
+__device__ inline float head_max(float x) {
+  x = fmaxf(x, __shfl_xor(x, 16));
+  return fmaxf(x, __shfl_xor(x, 32));
+}
+__device__ inline float head_sum(float x) {
+  x += __shfl_xor(x, 16);
+  return x + __shfl_xor(x, 32);
+}
+
+// Scalar (SMEM) load of a wave-uniform int: block-table entries are read through the
+// constant address space so that waiting for them never waits for K/V vector loads.
+__device__ inline int load_scalar(const int32_t* p) {
+  return uniform(*(const __attribute__((address_space(4))) int32_t*)p);
+}
+
+// ---------------------------------------------------------------------------------
+// Page loaders.  A wave streams tiles [t0, t1) of one (row, kv head); tokens at or past
+// `lim` = min(row length, 32 * t1) are never read.  Each loader splits a tile into
+// lookup() (block-table reads, issued one tile ahead) and issue() (the 16 K/V loads).
+//
+// FastPager: page sizes that are multiples of 16, so each 16-token block lies inside one
+// page.  The page id is wave-uniform (scalar load) and each block gets a buffer
+// descriptor covering only its valid rows: rows past `lim` read as zero without a
+// memory request, and no access can leave the block.
+// GenericPager: any other page size, per-lane table lookups and predicated loads.
+// ---------------------------------------------------------------------------------
+struct TileRegs {
+  u32x4 k[2][4];  // k[b][kk]: K row (block b, token c), dims 32kk + 8g .. +8
+  u32x4 v[8];     // v[j]: V row of token slot j (v_slot_token), dims 8c .. +8
+};
+
 struct FastPager {
-  struct Tile {
-    __amdgpu_buffer_rsrc_t k[2];
-    __amdgpu_buffer_rsrc_t v[2];
+  struct Pages {
+    int page[2];  // physical page of each 16-token block (unused when the block is empty)
   };
   const DecodeArgs& a;
   const int32_t* trow;
-  int len;
+  int lim;
   long head_bytes;   // kvh * ps * 256
   long page_bytes;   // Hkv * ps * 256
   uint32_t koff[4];  // per-lane byte offsets inside a block, K (per 32-dim step)
   uint32_t voff[8];  // per-lane byte offsets inside a block, V (per token slot)
 
-  __device__ FastPager(const DecodeArgs& args, int row, int kvh, int length, int lane)
-      : a(args), len(length) {
+  __device__ FastPager(const DecodeArgs& args, int row, int kvh, int limit, int lane)
+      : a(args), lim(limit) {
     trow = a.block_table + (long)row * a.max_pages;
     head_bytes = (long)kvh * a.page_size * (kD * 2);
     page_bytes = (long)a.hkv * a.page_size * (kD * 2);
@@ -174,46 +212,59 @@ struct FastPager {
     for (int j = 0; j < 8; ++j) voff[j] = (4 * g + (j & 3)) * 256 + c * 16;
   }
 
-  __device__ inline void prepare(int tile, Tile& t) const {
+  __device__ inline Pages lookup(int tile) const {
+    Pages p;
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       const int tok0 = tile * kTile + b * 16;
-      int nvalid = len - tok0;
-      nvalid = nvalid < 0 ? 0 : (nvalid > 16 ? 16 : nvalid);
-      long off = 0;
-      if (nvalid > 0) {
+      p.page[b] = 0;
+      if (tok0 < lim) {
         int logical, in_page;
         page_of(a, tok0, logical, in_page);
-        const int page = clamp_page(a, uniform(trow[logical]));
-        off = (long)page * page_bytes + head_bytes + (long)in_page * (kD * 2);
+        p.page[b] = load_scalar(trow + logical);  // clamped in issue(), after the compute
       }
-      t.k[b] = __builtin_amdgcn_make_buffer_rsrc((void*)(a.k_pages + off), (short)0,
-                                                 nvalid * (kD * 2), kRsrcWord3);
-      t.v[b] = __builtin_amdgcn_make_buffer_rsrc((void*)(a.v_pages + off), (short)0,
-                                                 nvalid * (kD * 2), kRsrcWord3);
     }
+    return p;
   }
-  __device__ inline u32x4 load_k(const Tile& t, int b, int kk) const {
-    return __builtin_amdgcn_raw_buffer_load_b128(t.k[b], koff[kk], 0, 0);
-  }
-  __device__ inline u32x4 load_v(const Tile& t, int j) const {
-    return __builtin_amdgcn_raw_buffer_load_b128(t.v[j >> 2], voff[j], 0, 0);
+
+  __device__ inline void issue(int tile, const Pages& p, TileRegs& r) const {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int tok0 = tile * kTile + b * 16;
+      int nvalid = lim - tok0;
+      nvalid = nvalid < 0 ? 0 : (nvalid > 16 ? 16 : nvalid);
+      int logical, in_page;
+      page_of(a, tok0, logical, in_page);
+      const long off = nvalid > 0
+          ? (long)clamp_page(a, p.page[b]) * page_bytes + head_bytes + (long)in_page * (kD * 2) : 0;
+      // Descriptors must be wave-uniform (SGPRs); readfirstlane states that to the
+      // compiler, which otherwise wraps every buffer load in a waterfall loop.
+      const int nrec = uniform(nvalid * (kD * 2));
+      const __amdgpu_buffer_rsrc_t rk =
+          __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(a.k_pages + off), (short)0, nrec, kRsrcWord3);
+      const __amdgpu_buffer_rsrc_t rv =
+          __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(a.v_pages + off), (short)0, nrec, kRsrcWord3);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) r.k[b][kk] = __builtin_amdgcn_raw_buffer_load_b128(rk, koff[kk], 0, 0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) r.v[b * 4 + j] = __builtin_amdgcn_raw_buffer_load_b128(rv, voff[b * 4 + j], 0, 0);
+    }
   }
 };
 
 struct GenericPager {
-  struct Tile {
+  struct Pages {
     long k[2];  // byte offset of this lane's K chunk per block, or -1
     long v[8];  // byte offset of this lane's V chunk per slot, or -1
   };
   const DecodeArgs& a;
   const int32_t* trow;
-  int len;
+  int lim;
   long head_bytes, page_bytes;
   int c, g;
 
-  __device__ GenericPager(const DecodeArgs& args, int row, int kvh, int length, int lane)
-      : a(args), len(length) {
+  __device__ GenericPager(const DecodeArgs& args, int row, int kvh, int limit, int lane)
+      : a(args), lim(limit) {
     trow = a.block_table + (long)row * a.max_pages;
     head_bytes = (long)kvh * a.page_size * (kD * 2);
     page_bytes = (long)a.hkv * a.page_size * (kD * 2);
@@ -221,65 +272,61 @@ struct GenericPager {
     g = lane >> 4;
   }
   __device__ inline long row_offset(int token) const {
-    if (token >= len) return -1;
+    if (token >= lim) return -1;
     int logical, in_page;
     page_of(a, token, logical, in_page);
     const int page = clamp_page(a, trow[logical]);
     return (long)page * page_bytes + head_bytes + (long)in_page * (kD * 2);
   }
-  __device__ inline void prepare(int tile, Tile& t) const {
+  __device__ inline Pages lookup(int tile) const {
+    Pages p;
     const int tok0 = tile * kTile;
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       const long o = row_offset(tok0 + b * 16 + c);
-      t.k[b] = o < 0 ? -1 : o + g * 16;
+      p.k[b] = o < 0 ? -1 : o + g * 16;
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const long o = row_offset(tok0 + v_slot_token(g, j));
-      t.v[j] = o < 0 ? -1 : o + c * 16;
+      p.v[j] = o < 0 ? -1 : o + c * 16;
     }
+    return p;
   }
-  __device__ inline u32x4 load_k(const Tile& t, int b, int kk) const {
-    u32x4 z = {0u, 0u, 0u, 0u};
-    return t.k[b] < 0 ? z : *(const u32x4*)(a.k_pages + t.k[b] + kk * 64);
-  }
-  __device__ inline u32x4 load_v(const Tile& t, int j) const {
-    u32x4 z = {0u, 0u, 0u, 0u};
-    return t.v[j] < 0 ? z : *(const u32x4*)(a.v_pages + t.v[j]);
+  __device__ inline void issue(int, const Pages& p, TileRegs& r) const {
+    const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+        r.k[b][kk] = p.k[b] < 0 ? z : *(const u32x4*)(a.k_pages + p.k[b] + kk * 64);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r.v[j] = p.v[j] < 0 ? z : *(const u32x4*)(a.v_pages + p.v[j]);
   }
 };
 
 // ---------------------------------------------------------------------------------
 // Per-wave streaming state and tile step.
+//
+// Lazy rescaling: probabilities are taken relative to a per-head reference m (log2
+// units) that only moves when a score exceeds it by more than kSlack, so P <= 2^kSlack
+// and the O/l rescale (with its cross-lane broadcast) runs on the first tile and then
+// rarely.  The true running max is tracked per lane and restored in the combine, so
+// partial states keep the reference's m = max score convention.
 // ---------------------------------------------------------------------------------
+constexpr float kSlack = 8.0f;
+
 template <int HB>
 struct WaveState {
-  f32x4 o[HB][8];  // o[hb][jj][i] = O[head hb*16 + 4g + i][dim 8c + jj]
-  float m[HB];     // running max (log2 units) of head hb*16 + c
-  float l[HB];     // lane-partial running sum of exp2(x - m)
+  f32x4 o[HB][8];  // o[hb][jj][i] = O[head hb*16 + 4g + i][dim 8c + jj], relative to m
+  float m[HB];     // reference max (log2 units) of head hb*16 + c, uniform over its lanes
+  float mx[HB];    // lane-local true running max (log2 units)
+  float l[HB];     // lane-partial sum of exp2(x - m)
 };
-
-struct TileRegs {
-  u32x4 k[2][4];
-  u32x4 v[8];
-};
-
-template <class Pager>
-__device__ inline void issue_tile(const Pager& pg, int tile, TileRegs& r) {
-  typename Pager::Tile t;
-  pg.prepare(tile, t);
-#pragma unroll
-  for (int b = 0; b < 2; ++b)
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) r.k[b][kk] = pg.load_k(t, b, kk);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) r.v[j] = pg.load_v(t, j);
-}
 
 template <class Elem, int HB>
 __device__ inline void compute_tile(WaveState<HB>& st, const TileRegs& r,
-                                    const u32x4 (&qf)[HB][4], int tile, int len, int lane) {
+                                    const u32x4 (&qf)[HB][4], int tile, int lim, int lane) {
   const int g = lane >> 4;
   // V transpose: vt[jj] holds, for dim 8c + jj, the 8 tokens of this lane's slots.
   u32x4 vt[8];
@@ -293,6 +340,7 @@ __device__ inline void compute_tile(WaveState<HB>& st, const TileRegs& r,
     }
   }
   const int tok_base = tile * kTile + 4 * g;
+  const bool partial = (tile + 1) * kTile > lim;  // wave-uniform
 #pragma unroll
   for (int hb = 0; hb < HB; ++hb) {
     f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
@@ -304,31 +352,39 @@ __device__ inline void compute_tile(WaveState<HB>& st, const TileRegs& r,
     float x[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      x[i] = (tok_base + i < len) ? s0[i] * kScaleLog2 : -INFINITY;
-      x[4 + i] = (tok_base + 16 + i < len) ? s1[i] * kScaleLog2 : -INFINITY;
+      x[i] = s0[i] * kScaleLog2;
+      x[4 + i] = s1[i] * kScaleLog2;
     }
-    float mx = x[0];
+    if (partial) {
 #pragma unroll
-    for (int j = 1; j < 8; ++j) mx = fmaxf(mx, x[j]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(st.m[hb], mx);
-    const float corr = __builtin_amdgcn_exp2f(st.m[hb] - m_new);
-    st.m[hb] = m_new;
+      for (int i = 0; i < 4; ++i) {
+        if (tok_base + i >= lim) x[i] = -INFINITY;
+        if (tok_base + 16 + i >= lim) x[4 + i] = -INFINITY;
+      }
+    }
+    float lmx = x[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) lmx = fmaxf(lmx, x[j]);
+    st.mx[hb] = fmaxf(st.mx[hb], lmx);
+    if (__builtin_amdgcn_ballot_w64(lmx > st.m[hb] + kSlack) != 0) {
+      const float m_new = fmaxf(st.m[hb], head_max(lmx));
+      const float corr = __builtin_amdgcn_exp2f(st.m[hb] - m_new);
+      st.m[hb] = m_new;
+      st.l[hb] *= corr;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float ci = __shfl(corr, 4 * g + i);  // lane 4g + i holds head 4g + i
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) st.o[hb][jj][i] *= ci;
+      }
+    }
     float p[8], psum = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      p[j] = __builtin_amdgcn_exp2f(x[j] - m_new);
+      p[j] = __builtin_amdgcn_exp2f(x[j] - st.m[hb]);
       psum += p[j];
     }
-    st.l[hb] = st.l[hb] * corr + psum;
-    // Rescale O rows (heads hb*16 + 4g + i); lane 4g + i holds that head's factor.
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float ci = __shfl(corr, 4 * g + i);
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) st.o[hb][jj][i] *= ci;
-    }
+    st.l[hb] += psum;
 #pragma unroll
     for (int pass = 0; pass < Elem::kPasses; ++pass) {
       u32x4 pa;
@@ -347,21 +403,27 @@ __device__ inline void compute_tile(WaveState<HB>& st, const TileRegs& r,
   }
 }
 
-// Streams tiles [t0, t1) of one (row, kv head) into the wave state, two tiles in flight.
+// Streams tiles [t0, t1) of one (row, kv head) into the wave state.  Two tiles of K/V
+// are in flight: the next tile's loads are issued (unconditionally; past the range they
+// read nothing) before the current tile is computed, and block-table reads run one
+// further tile ahead on the scalar unit.
 template <class Elem, int HB, class Pager>
 __device__ inline void stream_range(WaveState<HB>& st, const Pager& pg, const u32x4 (&qf)[HB][4],
-                                    int t0, int t1, int len, int lane) {
+                                    int t0, int t1, int lim, int lane) {
   if (t0 >= t1) return;
   TileRegs ra, rb;
-  issue_tile(pg, t0, ra);
-  int t = t0;
-  while (true) {
-    if (t + 1 < t1) issue_tile(pg, t + 1, rb);
-    compute_tile<Elem, HB>(st, ra, qf, t, len, lane);
-    if (++t >= t1) break;
-    if (t + 1 < t1) issue_tile(pg, t + 1, ra);
-    compute_tile<Elem, HB>(st, rb, qf, t, len, lane);
-    if (++t >= t1) break;
+  typename Pager::Pages pa = pg.lookup(t0);
+  pg.issue(t0, pa, ra);
+  typename Pager::Pages pb = pg.lookup(t0 + 1);
+  for (int t = t0;; t += 2) {
+    pg.issue(t + 1, pb, rb);
+    pa = pg.lookup(t + 2);
+    compute_tile<Elem, HB>(st, ra, qf, t, lim, lane);
+    if (t + 1 >= t1) break;
+    pg.issue(t + 2, pa, ra);
+    pb = pg.lookup(t + 3);
+    compute_tile<Elem, HB>(st, rb, qf, t + 1, lim, lane);
+    if (t + 2 >= t1) break;
   }
 }
 
@@ -537,6 +599,7 @@ void decode_kernel(DecodeArgs a) {
 #pragma unroll
   for (int hb = 0; hb < HB; ++hb) {
     st.m[hb] = -FLT_MAX;
+    st.mx[hb] = -FLT_MAX;
     st.l[hb] = 0.f;
 #pragma unroll
     for (int jj = 0; jj < 8; ++jj) st.o[hb][jj] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -544,26 +607,31 @@ void decode_kernel(DecodeArgs a) {
 
   // Contiguous sub-range of the unit's tiles for this wave.
   const int n = u.te - u.tb;
-  const int w0 = u.tb + (n * wave) / kWaves;
-  const int w1 = u.tb + (n * (wave + 1)) / kWaves;
+  const int w0 = uniform(u.tb + (n * wave) / kWaves);
+  const int w1 = uniform(u.tb + (n * (wave + 1)) / kWaves);
+  const long lim_l = (long)w1 * kTile;
+  const int lim = uniform(lim_l < u.len ? (int)lim_l : u.len);
   if (FAST) {
-    FastPager pg(a, u.row, u.kvh, u.len, lane);
-    stream_range<Elem, HB>(st, pg, qf, w0, w1, u.len, lane);
+    FastPager pg(a, u.row, u.kvh, lim, lane);
+    stream_range<Elem, HB>(st, pg, qf, w0, w1, lim, lane);
   } else {
-    GenericPager pg(a, u.row, u.kvh, u.len, lane);
-    stream_range<Elem, HB>(st, pg, qf, w0, w1, u.len, lane);
+    GenericPager pg(a, u.row, u.kvh, lim, lane);
+    stream_range<Elem, HB>(st, pg, qf, w0, w1, lim, lane);
   }
 #pragma unroll
   for (int hb = 0; hb < HB; ++hb) {
-    st.l[hb] += __shfl_xor(st.l[hb], 16);
-    st.l[hb] += __shfl_xor(st.l[hb], 32);
+    st.l[hb] = head_sum(st.l[hb]);
+    st.mx[hb] = head_max(st.mx[hb]);
   }
 
   // Combine the four waves, one 16-head block at a time.
-  // LDS: m[w][32], l[w][32], o[w][16][128] (33 KB for any G).
+  // LDS: m[w][32] (reference max), l[w][32], x[w][32] (true max), o[w][gh][128] with
+  // gh = min(G, 16) (<= 34 KB).
+  const int gh = G < 16 ? G : 16;
   float* sm_m = lds;
   float* sm_l = lds + kWaves * 32;
-  float* sm_o = lds + 2 * kWaves * 32;
+  float* sm_x = lds + 2 * kWaves * 32;
+  float* sm_o = lds + 3 * kWaves * 32;
   if (g == 0) {
 #pragma unroll
     for (int hb = 0; hb < HB; ++hb) {
@@ -571,6 +639,7 @@ void decode_kernel(DecodeArgs a) {
       if (h < G) {
         sm_m[wave * 32 + h] = st.m[hb];
         sm_l[wave * 32 + h] = st.l[hb];
+        sm_x[wave * 32 + h] = st.mx[hb];
       }
     }
   }
@@ -585,7 +654,7 @@ void decode_kernel(DecodeArgs a) {
     for (int i = 0; i < 4; ++i) {
       const int hh = 4 * g + i;
       if (hh < nh) {
-        float* dst = sm_o + ((long)wave * 16 + hh) * kD + 8 * c;
+        float* dst = sm_o + ((long)wave * gh + hh) * kD + 8 * c;
         *(f32x4*)dst = f32x4{st.o[hb][0][i], st.o[hb][1][i], st.o[hb][2][i], st.o[hb][3][i]};
         *(f32x4*)(dst + 4) = f32x4{st.o[hb][4][i], st.o[hb][5][i], st.o[hb][6][i], st.o[hb][7][i]};
       }
@@ -603,7 +672,7 @@ void decode_kernel(DecodeArgs a) {
       for (int w = 0; w < kWaves; ++w) {
         const float e = __builtin_amdgcn_exp2f(sm_m[w * 32 + h] - M);
         L += e * sm_l[w * 32 + h];
-        A += e * *(const f32x4*)(sm_o + ((long)w * 16 + hh) * kD + d);
+        A += e * *(const f32x4*)(sm_o + ((long)w * gh + hh) * kD + d);
       }
       if (MODE == kDirect) {
         if (out_row >= 0 && out_row < a.out_rows) {
@@ -611,11 +680,17 @@ void decode_kernel(DecodeArgs a) {
           store_out4<Elem>(a.out, ((long)out_row * a.hq + qh0 + h) * kD + d, A * inv);
         }
       } else {
+        // Re-express (L, A) relative to the true max so the partial state is
+        // (m = max score, l = sum exp(s - m), acc = sum exp(s - m) v) as in cuh:620-632.
+        float Mx = -FLT_MAX;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) Mx = fmaxf(Mx, sm_x[w * 32 + h]);
+        const float rescale = __builtin_amdgcn_exp2f(M - Mx);
         const long s = state0 + (long)h * state_stride;
-        *(f32x4*)(a.part_acc + s * kD + d) = A;
+        *(f32x4*)(a.part_acc + s * kD + d) = A * rescale;
         if (d == 0) {
-          a.part_m[s] = M * kLn2;
-          a.part_l[s] = L;
+          a.part_m[s] = Mx * kLn2;
+          a.part_l[s] = L * rescale;
         }
       }
     }
@@ -662,46 +737,84 @@ struct MergeArgs {
   int32_t context, max_tokens;   // split mode length fallback / clamp
 };
 
+__device__ inline float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+__device__ inline float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+// One wave per (row, query head).  Lane s of each 64-slot chunk loads slot s's (m, l)
+// (all slots in parallel), the wave reduces the max and the weighted sum, then every lane
+// accumulates its two dims over the chunk with the slot weight broadcast by readlane;
+// the accumulation loop is branch-free so its loads overlap.
 template <class Elem, bool QUEUE>
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   const int wave_id = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (wave_id >= a.batch * a.hq) return;
-  const int row = wave_id / a.hq;
-  const int qh = wave_id - row * a.hq;
-  int first, count, total = 0;
+  const int row = uniform(wave_id / a.hq);
+  const int qh = uniform(wave_id - row * a.hq);
+  int first = 0, count, total = 0, nsplit, split0 = 0;
   long stride;
   if (QUEUE) {
-    int s0 = a.split_offsets[row], s1 = a.split_offsets[row + 1];
-    if (s0 < 0) s0 = 0;
-    if (s1 > a.total_slots) s1 = a.total_slots;
-    first = s0;
-    count = s1 - s0;
-    int len = a.seq_lens[row];
+    const int o0 = uniform(a.split_offsets[row]), o1 = uniform(a.split_offsets[row + 1]);
+    first = o0 < 0 ? 0 : o0;
+    const int last = o1 > a.total_slots ? a.total_slots : o1;
+    count = last - first;
+    nsplit = o1 - o0;
+    split0 = first - o0;
+    int len = uniform(a.seq_lens[row]);
     if (len > a.max_tokens) len = a.max_tokens;
     total = ceil_tiles(len < 0 ? 0 : len);
     stride = a.hq;
   } else {
-    first = 0;
     count = a.num_splits;
+    nsplit = count;
     stride = 1;
   }
   const long base = QUEUE ? (long)first * a.hq + qh : ((long)row * a.hq + qh) * a.num_splits;
-  const int nsplit = QUEUE ? (a.split_offsets[row + 1] - a.split_offsets[row]) : count;
+  // Work-queue slots of splits the builder leaves empty hold no state: skip them.
+  auto live = [&](int s) {
+    return s < count &&
+           !(QUEUE && (long)total * (split0 + s) / nsplit == (long)total * (split0 + s + 1) / nsplit);
+  };
   float M = -FLT_MAX;
-  for (int s = 0; s < count; ++s) {
-    if (QUEUE && (long)total * s / nsplit == (long)total * (s + 1) / nsplit) continue;
-    M = fmaxf(M, a.part_m[base + s * stride]);
-  }
+  for (int c0 = 0; c0 < count; c0 += 64)
+    if (live(c0 + lane)) M = fmaxf(M, a.part_m[base + (long)(c0 + lane) * stride]);
+  M = wave_max(M);
   float L = 0.f;
   f32x2 A = {0.f, 0.f};
-  for (int s = 0; s < count; ++s) {
-    if (QUEUE && (long)total * s / nsplit == (long)total * (s + 1) / nsplit) continue;
-    const long st = base + s * stride;
-    const float w = __builtin_amdgcn_exp2f((a.part_m[st] - M) * kLog2e);
-    L += w * a.part_l[st];
-    A += w * *(const f32x2*)(a.part_acc + st * kD + 2 * lane);
+  for (int c0 = 0; c0 < count; c0 += 64) {
+    float w = 0.f;
+    if (live(c0 + lane)) {
+      const long st = base + (long)(c0 + lane) * stride;
+      w = __builtin_amdgcn_exp2f((a.part_m[st] - M) * kLog2e);
+      L += w * a.part_l[st];
+    }
+    const int n = count - c0 < 64 ? count - c0 : 64;
+    for (int j0 = 0; j0 < n; j0 += 8) {  // groups of 8 slots: 8 loads in flight
+      f32x2 v[8];
+      float wj[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int j = j0 + u < n ? j0 + u : n - 1;  // tail lanes re-read a valid slot
+        wj[u] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), j));
+        if (j0 + u >= n) wj[u] = 0.f;
+        v[u] = *(const f32x2*)(a.part_acc + (base + (long)(c0 + j) * stride) * kD + 2 * lane);
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {  // select, not multiply: skipped slots may hold NaN
+        A[0] += wj[u] != 0.f ? wj[u] * v[u][0] : 0.f;
+        A[1] += wj[u] != 0.f ? wj[u] * v[u][1] : 0.f;
+      }
+    }
   }
+  L = wave_sum(L);
   const int out_row = a.out_indices ? a.out_indices[row] : row;
   if (out_row < 0 || out_row >= a.out_rows) return;
   const float inv = L > 0.f ? 1.f / L : 0.f;
@@ -735,7 +848,7 @@ int log2_exact(int x) {
 }
 
 size_t lds_bytes(int G) {
-  return (size_t)(2 * kWaves * 32 + kWaves * (G < 16 ? G : 16) * kD) * sizeof(float);
+  return (size_t)(3 * kWaves * 32 + kWaves * (G < 16 ? G : 16) * kD) * sizeof(float);
 }
 
 struct Geometry {

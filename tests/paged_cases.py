@@ -54,3 +54,30 @@ def errors(out, ref):
     mask = torch.isfinite(ref)
     diff = (out[mask] - ref[mask]).abs()
     return diff.max().item(), diff.mean().item()
+
+
+MAX_ABS = 2e-3   # north-star tolerance against the fp32 repack + SDPA oracle
+MEAN_ABS = 3e-4  # the reference's mean gate (tests/smoke_test.cu:106)
+
+
+def assert_parity(out, ref):
+    """Gate of every parity test: max-abs 2e-3 and mean-abs 3e-4 against the fp32 oracle.
+
+    bf16 outputs carry 8 significant bits, so a correctly rounded result can already sit
+    half an output ulp from the fp32 value (3.9e-3 for |ref| in [1, 2)).  For bf16 the
+    max-abs bound therefore adds half a bf16 ulp of |ref| (the kernel's own error stays
+    within 2e-3) and the mean is taken against the oracle rounded to bf16.
+    """
+    got = out.float().cpu()
+    mask = torch.isfinite(ref)
+    assert torch.isfinite(got[mask]).all(), "non-finite output"
+    diff = (got[mask] - ref[mask]).abs()
+    if out.dtype == torch.bfloat16:
+        mag = ref[mask].abs().clamp_min(2.0 ** -126)
+        half_ulp = torch.exp2(torch.floor(torch.log2(mag)) - 8)
+        excess = (diff - half_ulp).max().item()
+        mean = (got[mask] - ref[mask].to(torch.bfloat16).float()).abs().mean().item()
+        assert excess < MAX_ABS and mean < MEAN_ABS, (excess, mean, diff.max().item())
+    else:
+        mx, mean = diff.max().item(), diff.mean().item()
+        assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)

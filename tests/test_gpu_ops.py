@@ -9,9 +9,8 @@ import pytest
 import torch
 
 import pkv_native
-from conftest import MAX_ABS, MEAN_ABS
 from oracle import attention as oracle
-from paged_cases import errors, make_case
+from paged_cases import assert_parity, make_case
 
 pytestmark = pytest.mark.gpu
 
@@ -56,8 +55,7 @@ def test_paged_attention(ext, gpu, b, hq, hkv, ctx, ps, splits, dtype, table):
     ext.paged_attention(q, k, v, bt, out, _ws(b, hq, splits, gpu), ctx, ps, splits)
     torch.cuda.synchronize()
     ref = oracle.paged_decode(case.q, case.k_pages, case.v_pages, case.block_table, case.seq_lens)
-    mx, mean = errors(out, ref)
-    assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
+    assert_parity(out, ref)
 
 
 # (lengths, Hq, Hkv, page_size, splits, dtype)
@@ -83,8 +81,7 @@ def test_paged_attention_masked(ext, gpu, lengths, hq, hkv, ps, splits, dtype):
     ext.paged_attention_masked(q, k, v, bt, sl, out, _ws(b, hq, splits, gpu), bucket, ps, splits)
     torch.cuda.synchronize()
     ref = oracle.paged_decode(case.q, case.k_pages, case.v_pages, case.block_table, case.seq_lens)
-    mx, mean = errors(out, ref)
-    assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
+    assert_parity(out, ref)
 
 
 @pytest.mark.parametrize("splits,dtype", [(1, F16), (6, F16), (3, BF16)])
@@ -100,8 +97,7 @@ def test_paged_attention_indexed(ext, gpu, splits, dtype):
     torch.cuda.synchronize()
     ref = oracle.paged_decode(case.q, case.k_pages, case.v_pages, case.block_table, case.seq_lens,
                               q_idx, o_idx, 6)
-    mx, mean = errors(out, ref)
-    assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
+    assert_parity(out, ref)
     assert torch.all(out[[1, 2, 4]].float().cpu() == 7.0)
 
 
@@ -147,8 +143,7 @@ def test_paged_attention_workqueue(ext, gpu, lengths, hq, hkv, ps, req, auto, dt
     out, counters = _run_queue(ext, gpu, case, meta, hq, hkv, fused)
     ref = oracle.paged_decode(case.q, case.k_pages, case.v_pages, meta["block_table"],
                               meta["seq_lens"], meta["q_indices"], meta["out_indices"])
-    mx, mean = errors(out, ref)
-    assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
+    assert_parity(out, ref)
     assert int(counters.abs().sum()) == 0  # the fused merge leaves the counters at zero
 
 
@@ -159,8 +154,7 @@ def test_workqueue_mi355x_policy(ext, gpu):
     out, _ = _run_queue(ext, gpu, case, meta, 32, 8, False)
     ref = oracle.paged_decode(case.q, case.k_pages, case.v_pages, meta["block_table"],
                               meta["seq_lens"], meta["q_indices"], meta["out_indices"])
-    mx, mean = errors(out, ref)
-    assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
+    assert_parity(out, ref)
 
 
 def test_workqueue_stages_equal_combined(ext, gpu):

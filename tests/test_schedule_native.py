@@ -1,0 +1,87 @@
+"""The C++ host scheduling in libpkv.so against the reference (golden vectors) and the
+Python restatement, bit for bit; plus invariants of the MI355X split planner."""
+import json
+import os
+
+import numpy as np
+import pytest
+from hypothesis import given, settings
+from hypothesis import strategies as st
+
+import pkv_native as nat
+from oracle import workqueue as wq
+from test_oracle_workqueue import GOLDEN, check_builder_invariants
+
+
+@pytest.fixture(scope="module")
+def golden():
+    with open(GOLDEN) as fh:
+        return json.load(fh)
+
+
+def test_row_splits_match_reference(golden):
+    for hkv, length, active, req, auto, expected in golden["row_splits"]:
+        assert nat.choose_workqueue_row_splits(length, active, req, auto, hkv) == expected
+
+
+def test_choose_and_model_splits_match_reference(golden):
+    for hkv, lens, single, expected in golden["choose_splits"]:
+        assert nat.choose_splits(lens, 16, True, single, hkv) == expected
+    for hkv, lens, bucket, queue in golden["model_splits"]:
+        assert nat.model_bucket_splits(lens, hkv) == bucket
+        assert nat.model_workqueue_splits(lens, hkv) == queue
+
+
+def test_cost_model_and_router_match_reference(golden):
+    for hkv, lens, est, choice in golden["routes"]:
+        m = nat.cost_model(nat.POLICY_REFERENCE, num_kv_heads=hkv)
+        for route, pairs in est.items():
+            for splits, ms in pairs:
+                assert nat.estimate_route_ms(lens, route, splits, m) == ms
+        assert list(nat.choose_adaptive_route(lens, m)) == choice
+
+
+@settings(max_examples=300, deadline=None)
+@given(st.lists(st.integers(1, 40000), min_size=1, max_size=10), st.integers(1, 48),
+       st.booleans(), st.sampled_from([1, 2, 4, 8, 32]), st.sampled_from([8, 16, 32, 64]),
+       st.integers(0, 1 << 30))
+def test_builder_matches_python_restatement(lengths, requested, auto, hkv, ps, seed):
+    rng = np.random.default_rng(seed)
+    n = len(lengths)
+    page_lists = [list(rng.integers(0, 1 << 20, size=int(rng.integers(1, 3000 // ps + 2)))) for _ in range(n)]
+    ids = [int(x) for x in rng.permutation(n + 3)[:n]]
+    py = wq.build_workqueue(lengths, ids, page_lists, ps, requested, auto, hkv)
+    cc = nat.build_workqueue(lengths, ids, page_lists, ps, requested, auto, hkv)
+    assert cc["block_table"].tolist() == py["block_table"]
+    assert cc["work_items"].tolist() == py["work_items"]
+    assert cc["split_offsets"].tolist() == py["split_offsets"]
+    assert cc["seq_lens"].tolist() == py["seq_lens"]
+    assert cc["q_indices"].tolist() == py["q_indices"]
+    assert cc["out_indices"].tolist() == py["out_indices"]
+    assert cc["total_partial_slots"] == py["total_partial_slots"]
+    assert cc["bucket_length"] == py["bucket_length"] and cc["splits"] == py["splits"]
+
+
+def test_mi355x_planner_invariants():
+    rng = np.random.default_rng(3)
+    for _ in range(200):
+        n = int(rng.integers(1, 65))
+        lengths = [int(x) for x in rng.integers(1, 70000, size=n)]
+        hkv = int(rng.choice([1, 4, 8, 32]))
+        pages = [list(range(-(-x // 16) + 1)) for x in lengths]
+        meta = nat.build_workqueue(lengths, list(range(n)), pages, 16, 1, True, hkv, nat.POLICY_MI355X)
+        m = {k: (v.tolist() if hasattr(v, "tolist") else v) for k, v in meta.items()}
+        check_builder_invariants(m, lengths, hkv, pages, 16)
+        row_splits = np.diff(meta["split_offsets"])
+        tiles = np.array([(x + 31) // 32 for x in lengths])
+        assert np.all(row_splits >= 1) and np.all(row_splits <= np.maximum(tiles, 1))
+        # no empty splits: every slot has work
+        assert len(meta["work_items"]) == int(row_splits.sum()) * hkv
+
+
+def test_c4_step_uses_twenty_splits():
+    lengths = [20000, 300, 700, 256, 1024, 512, 600, 31000]
+    meta = nat.build_workqueue(lengths, list(range(8)), [list(range(-(-x // 16))) for x in lengths],
+                               16, 20, False, 8)
+    assert meta["total_partial_slots"] == 160
+    assert np.all(np.diff(meta["split_offsets"]) == 20)
