@@ -34,7 +34,11 @@ for _p in (PKG, ROOT):
         sys.path.insert(0, _p)
 
 METRIC = "decode-step µs + effective KV HBM GB/s (% of peak), B8 bimodal G=4 fp16"
+WORKLOAD_NAMES = {"c1": "c1_b1_ctx2048_direct", "c2": "c2_b8_mha_split8",
+                  "c3": "c3_b1_long_context_split32", "c4": "c4_bimodal_workqueue",
+                  "c5_g32": "c5_b64_zipf_mqa_bf16", "c5_g8": "c5_b64_zipf_g8_bf16"}
 HBM_PEAK_GBPS = 8000.0
+MALL_BYTES = 256 * 2 ** 20  # MI355X Infinity Cache
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "c4_decode_traffic.json")
 
 
@@ -43,7 +47,11 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=96)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--rotations", type=int, default=4, help="KV pool replicas (cold-cache basis)")
+    p.add_argument("--rotations", type=int, default=4,
+                   help="minimum KV pool replicas (cold-cache basis; raised for small steps)")
+    p.add_argument("--workload", default="c4", choices=["c1", "c2", "c3", "c4", "c5_g32", "c5_g8"],
+                   help="configuration (default c4, the headline; the others are reported "
+                        "for DESIGN.md and are not the metric)")
     p.add_argument("--fused-merge", action="store_true", help="single-launch fused merge variant")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time budget")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -88,12 +96,19 @@ def main():
     import pkv_workloads as wl
 
     dev = torch.device("cuda:0")
-    w = wl.config_c4(seed=args.seed, fused_merge=args.fused_merge)
+    w = wl.CONFIGS[args.workload](seed=args.seed)
+    w.fused_merge = args.fused_merge
     metas = [wl.compile_step(w, i, dev) for i in range(len(w.steps))]
     ws = wl.workspace_for(w, metas, dev)
     q_pool = wl.make_q_pool(w, dev)
     k0, v0 = wl.make_kv_pool(w, dev)
-    pools = [(k0, v0)] + [(k0.clone(), v0.clone()) for _ in range(args.rotations - 1)]
+    # Enough replicas that the bytes read between two uses of one replica exceed twice the
+    # 256 MB Infinity Cache (at most 48 GB of replicas).
+    mean_bytes = sum(m.kv_bytes for m in metas) / len(metas)
+    pool_bytes = 2 * k0.numel() * k0.element_size()
+    rotations = max(args.rotations, -(-2 * MALL_BYTES // int(mean_bytes)) + 1)
+    rotations = max(2, min(rotations, int(48e9 // pool_bytes)))
+    pools = [(k0, v0)] + [(k0.clone(), v0.clone()) for _ in range(rotations - 1)]
     torch.cuda.synchronize()
     n_trace = len(w.steps)
 
@@ -119,18 +134,23 @@ def main():
     gpu_ms = start.elapsed_time(stop)
     total_bytes = sum(metas[k % n_trace].kv_bytes for k in range(args.steps))
 
-    # Decode kernel alone (stage 1 of the op), one event pair per launch on its stream.
+    # Decode kernel alone (stage 1 of the work-queue op), one event pair per launch on its
+    # stream.  The grid ops have no separate stage entry point: their whole op is timed.
     dec_ms, dec_bytes = [], []
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(args.steps)]
+    queue = w.op == "paged_attention_workqueue"
     for k in range(args.steps):
         i = k % n_trace
         m = metas[i]
         kp, vp = pools[k % len(pools)]
         evs[k][0].record()
-        ext.workqueue_decode(q_pool[i], kp, vp, m.block_table, m.seq_lens, m.work_items,
-                             m.split_offsets, m.q_indices, ws, m.bucket_length, w.page_size,
-                             m.total_partial_slots)
+        if queue:
+            ext.workqueue_decode(q_pool[i], kp, vp, m.block_table, m.seq_lens, m.work_items,
+                                 m.split_offsets, m.q_indices, ws, m.bucket_length, w.page_size,
+                                 m.total_partial_slots)
+        else:
+            step(k)
         evs[k][1].record()
         dec_bytes.append(m.kv_bytes)
     torch.cuda.synchronize()
@@ -142,6 +162,12 @@ def main():
             traffic = json.load(fh).get("hbm_bytes_per_launch")
 
     value = total_bytes / (gpu_ms / 1e3) / 1e9
+    kernel = {"paged_attention_workqueue": "decode_kernel<*,kQueue> (stage 1 only)",
+              "paged_attention_indexed": "decode_kernel<*,kSplit> + merge_kernel (whole op)",
+              "paged_attention_masked": "decode_kernel<*,kSplit> + merge_kernel (whole op)",
+              "paged_attention": "decode_kernel<*,kDirect> (whole op)"}[w.op]
+    if w.op == "paged_attention" and w.splits > 1:
+        kernel = "decode_kernel<*,kSplit> + merge_kernel (whole op)"
     result = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -155,16 +181,19 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp16",
+        "dtype": "fp16" if w.dtype == torch.float16 else "bf16",
         "data": "synthetic",
-        "config": {"workload": "c4_bimodal_workqueue", "requests": 24, "max_active": 8,
-                   "trace_steps": n_trace, "hq": 32, "hkv": 8, "head_dim": 128, "page_size": 16,
-                   "splits": 20, "fused_merge": bool(args.fused_merge),
+        "config": {"workload": WORKLOAD_NAMES[args.workload], "requests": len(w.requests),
+                   "max_active": max(len(s.active_ids) for s in w.steps),
+                   "trace_steps": n_trace, "hq": w.hq, "hkv": w.hkv, "head_dim": 128,
+                   "page_size": w.page_size,
+                   "splits": "auto (mi355x planner)" if w.auto_splits else w.splits,
+                   "fused_merge": bool(args.fused_merge),
                    "mean_kv_mb_per_step": round(sum(m.kv_bytes for m in metas) / n_trace / 1e6, 2),
                    "cache_basis": f"HBM-cold ({len(pools)} rotated KV pool replicas)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": traffic, "kernel": "decode_kernel<Half,1,true,kQueue>",
+                     "traffic": traffic if args.workload == "c4" else None, "kernel": kernel,
                      "mean_launch_us": round(sum(dec_ms) / len(dec_ms) * 1e3, 2)},
     }
     if not args.no_cpu_baseline:

@@ -236,6 +236,20 @@ int pkv_build_workqueue(
     int32_t* work_items, int32_t work_capacity, int32_t* out_num_tasks,
     int32_t* split_offsets, int32_t* out_total_partial_slots);
 
+/* ---------------------------------------------------------------------------------
+ * HBM calibration probes (counterparts of the reference's
+ * micro_benchmarks/01_hbm_bandwidth.cu:20-51 read/copy kernels).
+ * ------------------------------------------------------------------------------- */
+
+/* Reads `bytes` (a multiple of 4096, < 8 TiB) of `src` once, visiting its 4 KB chunks in
+ * a permuted order with access pattern 0 (contiguous 1 KB per load instruction),
+ * 1 (the decode kernel's K-operand loads: 16 rows x 64 B) or 2 (its V-operand loads:
+ * 4 rows x 256 B).  `sink` receives at most one word per workgroup (2048 words). */
+int pkv_probe_read(const void* src, size_t bytes, int32_t pattern, void* sink, void* stream);
+
+/* Copies `bytes` (a multiple of 16) from src to dst with a plain grid-stride kernel. */
+int pkv_probe_copy(const void* src, void* dst, size_t bytes, void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

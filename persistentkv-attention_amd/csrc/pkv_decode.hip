@@ -27,6 +27,7 @@
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 
 #include "pkv.h"
 
@@ -34,8 +35,7 @@ namespace pkv {
 
 constexpr int kD = 128;              // head dim (cuh:26)
 constexpr int kTile = 32;            // work-item tile in tokens (cuh:28)
-constexpr int kWaves = 4;            // waves per workgroup
-constexpr int kThreads = 64 * kWaves;
+constexpr int kMaxWaves = 8;         // waves per workgroup: 4 or 8 (template NW)
 constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit data format (gfx9 family)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -487,8 +487,8 @@ __device__ inline Unit resolve_unit(const DecodeArgs& a) {
 
 // Neutral partial state of an empty split (cuh:340-363): m = -FLT_MAX, l = 0, acc = 0.
 __device__ inline void write_neutral(const DecodeArgs& a, long state0, long state_stride,
-                                     int G, int tid) {
-  for (int idx = tid; idx < G * (kD / 4); idx += kThreads) {
+                                     int G, int tid, int nthreads) {
+  for (int idx = tid; idx < G * (kD / 4); idx += nthreads) {
     const int h = idx / (kD / 4), d = (idx % (kD / 4)) * 4;
     const long s = state0 + (long)h * state_stride;
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
@@ -512,7 +512,8 @@ __device__ inline void store_out4(uint8_t* out, long elem, f32x4 v) {
 // cuh:648-716).  Slots of empty splits are skipped by recomputing the builder's split
 // bounds, so rows with more splits than tiles are merged correctly.
 template <class Elem>
-__device__ void fused_merge_group(const DecodeArgs& a, const Unit& u, int qh0, int G, int tid) {
+__device__ void fused_merge_group(const DecodeArgs& a, const Unit& u, int qh0, int G, int tid,
+                                  int nthreads) {
   const int s_begin = a.split_offsets[u.row];
   const int s_end = a.split_offsets[u.row + 1];
   const int nsplit = s_end - s_begin;
@@ -520,7 +521,7 @@ __device__ void fused_merge_group(const DecodeArgs& a, const Unit& u, int qh0, i
   const int out_row = a.out_indices ? a.out_indices[u.row] : u.row;
   if (out_row < 0 || out_row >= a.out_rows) return;
   if (s_begin < 0 || s_end > a.total_slots || nsplit <= 0) return;  // malformed offsets
-  for (int idx = tid; idx < G * (kD / 4); idx += kThreads) {
+  for (int idx = tid; idx < G * (kD / 4); idx += nthreads) {
     const int h = idx / (kD / 4), d = (idx % (kD / 4)) * 4;
     const int qh = qh0 + h;
     float M = -FLT_MAX;
@@ -551,9 +552,11 @@ __device__ void fused_merge_group(const DecodeArgs& a, const Unit& u, int qh0, i
 // ---------------------------------------------------------------------------------
 // G <= 16 (one head block) keeps two waves per SIMD (<= 256 registers each); G <= 32
 // doubles the accumulators and runs one wave per SIMD with the AGPR file available.
-template <class Elem, int HB, bool FAST, int MODE>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(HB == 1 ? 2 : 1)))
+template <class Elem, int HB, bool FAST, int MODE, int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(HB == 1 ? 2 : 1)))
 void decode_kernel(DecodeArgs a) {
+  constexpr int kWaves = NW;
+  constexpr int kThreads = NW * 64;
   extern __shared__ float lds[];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -576,7 +579,7 @@ void decode_kernel(DecodeArgs a) {
   }
 
   if (MODE != kDirect && u.tb >= u.te) {
-    write_neutral(a, state0, state_stride, G, tid);
+    write_neutral(a, state0, state_stride, G, tid, kThreads);
     return;
   }
 
@@ -624,10 +627,11 @@ void decode_kernel(DecodeArgs a) {
     st.mx[hb] = head_max(st.mx[hb]);
   }
 
-  // Combine the four waves, one 16-head block at a time.
-  // LDS: m[w][32] (reference max), l[w][32], x[w][32] (true max), o[w][gh][128] with
-  // gh = min(G, 16) (<= 34 KB).
-  const int gh = G < 16 ? G : 16;
+  // Combine the waves one chunk of heads at a time (16 heads with 4 waves, 8 with 8, so
+  // the O staging stays at 32 KB).  LDS: m[w][32] (reference max), l[w][32],
+  // x[w][32] (true max), o[w][gh][128] with gh = min(G, chunk).
+  constexpr int kChunk = NW == 8 ? 8 : 16;
+  const int gh = G < kChunk ? G : kChunk;
   float* sm_m = lds;
   float* sm_l = lds + kWaves * 32;
   float* sm_x = lds + 2 * kWaves * 32;
@@ -647,50 +651,54 @@ void decode_kernel(DecodeArgs a) {
   if (MODE == kDirect) out_row = a.out_indices ? a.out_indices[u.row] : u.row;
 #pragma unroll
   for (int hb = 0; hb < HB; ++hb) {
-    const int h0 = hb * 16;
-    const int nh = G - h0 < 16 ? G - h0 : 16;
-    if (hb > 0) __syncthreads();  // the previous block's readers are done with sm_o
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int hh = 4 * g + i;
-      if (hh < nh) {
-        float* dst = sm_o + ((long)wave * gh + hh) * kD + 8 * c;
-        *(f32x4*)dst = f32x4{st.o[hb][0][i], st.o[hb][1][i], st.o[hb][2][i], st.o[hb][3][i]};
-        *(f32x4*)(dst + 4) = f32x4{st.o[hb][4][i], st.o[hb][5][i], st.o[hb][6][i], st.o[hb][7][i]};
-      }
-    }
-    __syncthreads();
-    for (int idx = tid; idx < nh * (kD / 4); idx += kThreads) {
-      const int hh = idx / (kD / 4), d = (idx % (kD / 4)) * 4;
-      const int h = h0 + hh;
-      float M = -FLT_MAX;
+    for (int sub = 0; sub < 16 / kChunk; ++sub) {
+      const int h0 = hb * 16 + sub * kChunk;
+      const int nh = G - h0 < kChunk ? G - h0 : kChunk;
+      if (nh <= 0) break;
+      if (hb > 0 || sub > 0) __syncthreads();  // previous chunk's readers are done with sm_o
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w * 32 + h]);
-      float L = 0.f;
-      f32x4 A = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        const float e = __builtin_amdgcn_exp2f(sm_m[w * 32 + h] - M);
-        L += e * sm_l[w * 32 + h];
-        A += e * *(const f32x4*)(sm_o + ((long)w * gh + hh) * kD + d);
-      }
-      if (MODE == kDirect) {
-        if (out_row >= 0 && out_row < a.out_rows) {
-          const float inv = L > 0.f ? 1.f / L : 0.f;
-          store_out4<Elem>(a.out, ((long)out_row * a.hq + qh0 + h) * kD + d, A * inv);
+      for (int i = 0; i < 4; ++i) {
+        const int hh = 4 * g + i - sub * kChunk;
+        if (hh >= 0 && hh < nh) {
+          float* dst = sm_o + ((long)wave * gh + hh) * kD + 8 * c;
+          *(f32x4*)dst = f32x4{st.o[hb][0][i], st.o[hb][1][i], st.o[hb][2][i], st.o[hb][3][i]};
+          *(f32x4*)(dst + 4) = f32x4{st.o[hb][4][i], st.o[hb][5][i], st.o[hb][6][i], st.o[hb][7][i]};
         }
-      } else {
-        // Re-express (L, A) relative to the true max so the partial state is
-        // (m = max score, l = sum exp(s - m), acc = sum exp(s - m) v) as in cuh:620-632.
-        float Mx = -FLT_MAX;
+      }
+      __syncthreads();
+      for (int idx = tid; idx < nh * (kD / 4); idx += kThreads) {
+        const int hh = idx / (kD / 4), d = (idx % (kD / 4)) * 4;
+        const int h = h0 + hh;
+        float M = -FLT_MAX;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) Mx = fmaxf(Mx, sm_x[w * 32 + h]);
-        const float rescale = __builtin_amdgcn_exp2f(M - Mx);
-        const long s = state0 + (long)h * state_stride;
-        *(f32x4*)(a.part_acc + s * kD + d) = A * rescale;
-        if (d == 0) {
-          a.part_m[s] = Mx * kLn2;
-          a.part_l[s] = L * rescale;
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w * 32 + h]);
+        float L = 0.f;
+        f32x4 A = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+          const float e = __builtin_amdgcn_exp2f(sm_m[w * 32 + h] - M);
+          L += e * sm_l[w * 32 + h];
+          A += e * *(const f32x4*)(sm_o + ((long)w * gh + hh) * kD + d);
+        }
+        if (MODE == kDirect) {
+          if (out_row >= 0 && out_row < a.out_rows) {
+            const float inv = L > 0.f ? 1.f / L : 0.f;
+            store_out4<Elem>(a.out, ((long)out_row * a.hq + qh0 + h) * kD + d, A * inv);
+          }
+        } else {
+          // Re-express (L, A) relative to the true max so the partial state is
+          // (m = max score, l = sum exp(s - m), acc = sum exp(s - m) v) as in cuh:620-632.
+          float Mx = -FLT_MAX;
+#pragma unroll
+          for (int w = 0; w < kWaves; ++w) Mx = fmaxf(Mx, sm_x[w * 32 + h]);
+          const float rescale = __builtin_amdgcn_exp2f(M - Mx);
+          const long s = state0 + (long)h * state_stride;
+          *(f32x4*)(a.part_acc + s * kD + d) = A * rescale;
+          if (d == 0) {
+            a.part_m[s] = Mx * kLn2;
+            a.part_l[s] = L * rescale;
+          }
         }
       }
     }
@@ -710,7 +718,7 @@ void decode_kernel(DecodeArgs a) {
     __syncthreads();
     if (last) {
       __threadfence();
-      fused_merge_group<Elem>(a, u, qh0, G, tid);
+      fused_merge_group<Elem>(a, u, qh0, G, tid, kThreads);
       __syncthreads();
       if (tid == 0) a.merge_counters[(long)u.row * a.hkv + u.kvh] = 0;
     }
@@ -748,10 +756,12 @@ __device__ inline float wave_sum(float x) {
   return x;
 }
 
-// One wave per (row, query head).  Lane s of each 64-slot chunk loads slot s's (m, l)
-// (all slots in parallel), the wave reduces the max and the weighted sum, then every lane
-// accumulates its two dims over the chunk with the slot weight broadcast by readlane;
-// the accumulation loop is branch-free so its loads overlap.
+// One wave per (row, query head).  After the row's slot range is known, every load of a
+// chunk of up to 32 slots is issued at once: lane s loads slot s's (m, l) and each lane
+// loads its two dims of every slot's acc.  The merge then costs two memory round trips
+// (row metadata, slot data) instead of one per slot.
+constexpr int kMergeChunk = 32;
+
 template <class Elem, bool QUEUE>
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   const int wave_id = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -783,38 +793,36 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     return s < count &&
            !(QUEUE && (long)total * (split0 + s) / nsplit == (long)total * (split0 + s + 1) / nsplit);
   };
-  float M = -FLT_MAX;
-  for (int c0 = 0; c0 < count; c0 += 64)
-    if (live(c0 + lane)) M = fmaxf(M, a.part_m[base + (long)(c0 + lane) * stride]);
-  M = wave_max(M);
-  float L = 0.f;
+  float M = -FLT_MAX, L = 0.f;
   f32x2 A = {0.f, 0.f};
-  for (int c0 = 0; c0 < count; c0 += 64) {
-    float w = 0.f;
-    if (live(c0 + lane)) {
-      const long st = base + (long)(c0 + lane) * stride;
-      w = __builtin_amdgcn_exp2f((a.part_m[st] - M) * kLog2e);
-      L += w * a.part_l[st];
+  for (int c0 = 0; c0 < count; c0 += kMergeChunk) {
+    const int n = count - c0 < kMergeChunk ? count - c0 : kMergeChunk;
+    // Issue the chunk's loads together (tail slots re-read the last live index).
+    const int s_lane = c0 + (lane < n ? lane : n - 1);
+    const float ms = a.part_m[base + (long)s_lane * stride];
+    const float ls = a.part_l[base + (long)s_lane * stride];
+    f32x2 v[kMergeChunk];
+#pragma unroll
+    for (int j = 0; j < kMergeChunk; ++j) {
+      const int s = c0 + (j < n ? j : n - 1);
+      v[j] = *(const f32x2*)(a.part_acc + (base + (long)s * stride) * kD + 2 * lane);
     }
-    const int n = count - c0 < 64 ? count - c0 : 64;
-    for (int j0 = 0; j0 < n; j0 += 8) {  // groups of 8 slots: 8 loads in flight
-      f32x2 v[8];
-      float wj[8];
+    const bool ok = lane < n && live(c0 + lane);
+    // Online rescale across chunks: fold this chunk's max into M.
+    const float cm = wave_max(ok ? ms : -FLT_MAX);
+    const float m_new = fmaxf(M, cm);
+    const float corr = __builtin_amdgcn_exp2f((M - m_new) * kLog2e);
+    M = m_new;
+    const float w = ok ? __builtin_amdgcn_exp2f((ms - M) * kLog2e) : 0.f;
+    L = L * corr + wave_sum(w * ls);
+    A *= corr;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int j = j0 + u < n ? j0 + u : n - 1;  // tail lanes re-read a valid slot
-        wj[u] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), j));
-        if (j0 + u >= n) wj[u] = 0.f;
-        v[u] = *(const f32x2*)(a.part_acc + (base + (long)(c0 + j) * stride) * kD + 2 * lane);
-      }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {  // select, not multiply: skipped slots may hold NaN
-        A[0] += wj[u] != 0.f ? wj[u] * v[u][0] : 0.f;
-        A[1] += wj[u] != 0.f ? wj[u] * v[u][1] : 0.f;
-      }
+    for (int j = 0; j < kMergeChunk; ++j) {
+      const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), j));
+      A[0] += wj != 0.f ? wj * v[j][0] : 0.f;  // select, not multiply: skipped slots may hold NaN
+      A[1] += wj != 0.f ? wj * v[j][1] : 0.f;
     }
   }
-  L = wave_sum(L);
   const int out_row = a.out_indices ? a.out_indices[row] : row;
   if (out_row < 0 || out_row >= a.out_rows) return;
   const float inv = L > 0.f ? 1.f / L : 0.f;
@@ -847,8 +855,9 @@ int log2_exact(int x) {
   return s;
 }
 
-size_t lds_bytes(int G) {
-  return (size_t)(3 * kWaves * 32 + kWaves * (G < 16 ? G : 16) * kD) * sizeof(float);
+size_t lds_bytes(int G, int nw) {
+  const int chunk = nw == 8 ? 8 : 16;
+  return (size_t)(3 * nw * 32 + nw * (G < chunk ? G : chunk) * kD) * sizeof(float);
 }
 
 struct Geometry {
@@ -878,9 +887,26 @@ int check_geometry(const Geometry& g, const void* q, const void* k, const void* 
   return PKV_OK;
 }
 
+// Waves per decode workgroup.  Eight spread each unit over more waves (shorter critical
+// path, full occupancy with fewer units); G > 16 runs one wave per SIMD and stays at four.
+// PKV_DECODE_WAVES=4|8 overrides the choice (tuning).
+int decode_waves(int hb) {
+  static const int forced = [] {
+    const char* e = getenv("PKV_DECODE_WAVES");
+    return e ? atoi(e) : 0;
+  }();
+  if (hb > 1) return 4;
+  if (forced == 4 || forced == 8) return forced;
+  return 8;
+}
+
 template <class Elem, int HB, bool FAST, int MODE>
 hipError_t launch_decode(const DecodeArgs& a, int grid, hipStream_t stream) {
-  decode_kernel<Elem, HB, FAST, MODE><<<dim3(grid), dim3(kThreads), lds_bytes(a.group), stream>>>(a);
+  if (HB == 1 && decode_waves(HB) == 8)
+    decode_kernel<Elem, HB, FAST, MODE, (HB == 1 ? 8 : 4)>
+        <<<dim3(grid), dim3(8 * 64), lds_bytes(a.group, 8), stream>>>(a);
+  else
+    decode_kernel<Elem, HB, FAST, MODE, 4><<<dim3(grid), dim3(4 * 64), lds_bytes(a.group, 4), stream>>>(a);
   return hipGetLastError();
 }
 
