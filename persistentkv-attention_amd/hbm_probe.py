@@ -1,0 +1,102 @@
+"""Achievable-HBM-bandwidth probes and rocprof byte-counter calibration.
+
+The MI355X counterpart of the reference's micro_benchmarks/01_hbm_bandwidth.cu:20-51
+(hbm_read / hbm_copy), driving ``pkv_probe_read`` / ``pkv_probe_copy`` of libpkv.so:
+
+  python hbm_probe.py read            # read bandwidth for the decode kernel's access patterns
+  python hbm_probe.py copy --mib 1024 # one known-size copy per launch, for rocprofv3 --pmc
+
+``read`` reports GB/s per pattern (contiguous, K-operand 16 rows x 64 B, V-operand 4 rows
+x 256 B) and size; sizes above the 256 MB Infinity Cache measure HBM.  ``copy`` launches
+``pkv_probe_copy`` ``--iters`` times over ``--mib`` MiB: the FETCH_SIZE and WRITE_SIZE that
+rocprofv3 reports per dispatch divided by the known byte count is the counter scale factor.
+"""
+from __future__ import annotations
+
+import argparse
+import os
+import sys
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+if _HERE not in sys.path:
+    sys.path.insert(0, _HERE)
+
+PATTERNS = {0: "contiguous", 1: "K operand (16 rows x 64 B)", 2: "V operand (4 rows x 256 B)"}
+
+
+def _time_ms(torch, fn, iters):
+    fn()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(iters):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / iters
+
+
+def _check(lib, status):
+    if status != 0:
+        raise RuntimeError(f"probe launch failed: {lib.pkv_status_string(status).decode()}")
+
+
+def run_read(sizes_mib, iters):
+    import torch
+
+    import pkv_native
+
+    lib = pkv_native.lib()
+    dev = torch.device("cuda:0")
+    buf = torch.empty(max(sizes_mib) << 20, dtype=torch.uint8, device=dev).random_(0, 256)
+    sink = torch.zeros(4096, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    rows = []
+    for pattern, name in PATTERNS.items():
+        for mib in sizes_mib:
+            nbytes = mib << 20
+            ms = _time_ms(torch, lambda: _check(lib, lib.pkv_probe_read(
+                buf.data_ptr(), nbytes, pattern, sink.data_ptr(), stream)), iters)
+            rows.append((name, mib, nbytes / ms / 1e6, ms * 1e3))
+            print(f"read {name:28s} {mib:6d} MiB: {nbytes / ms / 1e6:8.0f} GB/s "
+                  f"({ms * 1e3:8.1f} us)", flush=True)
+    return rows
+
+
+def run_copy(mib, iters):
+    import torch
+
+    import pkv_native
+
+    lib = pkv_native.lib()
+    dev = torch.device("cuda:0")
+    nbytes = mib << 20
+    src = torch.empty(nbytes, dtype=torch.uint8, device=dev).random_(0, 256)
+    dst = torch.empty_like(src)
+    stream = torch.cuda.current_stream().cuda_stream
+    ms = _time_ms(torch, lambda: _check(lib, lib.pkv_probe_copy(
+        src.data_ptr(), dst.data_ptr(), nbytes, stream)), iters)
+    if not torch.equal(src, dst):
+        raise RuntimeError("probe copy produced wrong bytes")
+    print(f"copy {mib} MiB per launch x {iters + 1} launches: read {nbytes} B + write {nbytes} B "
+          f"per launch, {2 * nbytes / ms / 1e6:.0f} GB/s read+write ({ms * 1e3:.1f} us)", flush=True)
+
+
+def main(argv=None):
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    sub = p.add_subparsers(dest="cmd", required=True)
+    r = sub.add_parser("read")
+    r.add_argument("--mib", type=int, nargs="+", default=[4096, 256, 64])
+    r.add_argument("--iters", type=int, default=10)
+    c = sub.add_parser("copy")
+    c.add_argument("--mib", type=int, default=1024)
+    c.add_argument("--iters", type=int, default=4)
+    a = p.parse_args(argv)
+    if a.cmd == "read":
+        run_read(a.mib, a.iters)
+    else:
+        run_copy(a.mib, a.iters)
+
+
+if __name__ == "__main__":
+    main()

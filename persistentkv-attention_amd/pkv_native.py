@@ -87,6 +87,12 @@ def lib():
         _PI32, _PI32, _I32, _PI32, _PI32, _I32, _I32, _I32, _I32, _I32,
         _PI32, _I32, _PI32, _PI32, _PI32, _PI32, _PI32, _I32, _PI32, _PI32, _PI32]
     so.pkv_build_workqueue.restype = ctypes.c_int
+    so.pkv_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, _I32, ctypes.c_void_p,
+                                  ctypes.c_void_p]
+    so.pkv_probe_read.restype = ctypes.c_int
+    so.pkv_probe_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                  ctypes.c_void_p]
+    so.pkv_probe_copy.restype = ctypes.c_int
     _lib = so
     return so
 
