@@ -1,8 +1,9 @@
 // pkv_decode.hip — paged GQA decode attention for MI355X (gfx950, CDNA4).
 //
-// One workgroup (4 wave64s) owns one unit of work: a (row, kv head) pair and a range
-// of 32-token tiles.  The unit is a whole row (direct op), one sequence split of a row
-// (grid-split ops) or one compact work item (work-queue op).  The four waves stream
+// One workgroup (8 wave64s when G <= 16, 4 when G > 16) owns one unit of work: a
+// (row, kv head) pair and a range of 32-token tiles.  The unit is a whole row (direct
+// op), one sequence split of a row (grid-split ops) or one compact work item (work-queue
+// op).  The waves stream
 // disjoint sub-ranges of the unit's tiles, so one K/V fetch from HBM serves all G query
 // heads of the KV group, then combine their online-softmax states through LDS.
 //
