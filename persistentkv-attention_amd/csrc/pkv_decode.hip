@@ -176,7 +176,7 @@ __device__ inline int load_scalar(const int32_t* p) {
 // ---------------------------------------------------------------------------------
 // Page loaders.  A wave streams tiles [t0, t1) of one (row, kv head); tokens at or past
 // `lim` = min(row length, 32 * t1) are never read.  Each loader splits a tile into
-// lookup() (block-table reads, issued one tile ahead) and issue() (the 16 K/V loads).
+// lookup() (block-table reads, issued two tiles ahead) and issue() (the 16 K/V loads).
 //
 // FastPager: page sizes that are multiples of 16, so each 16-token block lies inside one
 // page.  The page id is wave-uniform (scalar load) and each block gets a buffer
@@ -213,17 +213,17 @@ struct FastPager {
     for (int j = 0; j < 8; ++j) voff[j] = (4 * g + (j & 3)) * 256 + c * 16;
   }
 
+  // Table reads do not depend on the row length (columns are clamped to the table), so
+  // the first ones can be issued as soon as the work item is known.
   __device__ inline Pages lookup(int tile) const {
     Pages p;
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      const int tok0 = tile * kTile + b * 16;
-      p.page[b] = 0;
-      if (tok0 < lim) {
-        int logical, in_page;
-        page_of(a, tok0, logical, in_page);
-        p.page[b] = load_scalar(trow + logical);  // clamped in issue(), after the compute
-      }
+      const int tok0 = (tile < 0 ? 0 : tile) * kTile + b * 16;
+      int logical, in_page;
+      page_of(a, tok0, logical, in_page);
+      logical = logical < a.max_pages ? logical : a.max_pages - 1;
+      p.page[b] = load_scalar(trow + logical);  // clamped in issue(), after the compute
     }
     return p;
   }
@@ -404,46 +404,50 @@ __device__ inline void compute_tile(WaveState<HB>& st, const TileRegs& r,
   }
 }
 
-// Streams tiles [t0, t1) of one (row, kv head) into the wave state.  Two tiles of K/V
-// are in flight: the next tile's loads are issued (unconditionally; past the range they
-// read nothing) before the current tile is computed, and block-table reads run one
-// further tile ahead on the scalar unit.
+// Streams tiles [t0, t1) of one (row, kv head) into the wave state, given the block-table
+// reads of tiles t0 and t0 + 1.  One tile of K/V per wave is in flight while block-table
+// reads run two tiles ahead on the scalar unit.  Latency is hidden by the other waves of
+// the CU: 8 waves x 16 KB per CU already saturate HBM, and a deeper per-wave pipeline only
+// lengthens the memory queues (measured: two tiles in flight per wave made the work-queue
+// step about 7 % slower and doubled the registers held by tile buffers).
+template <class Elem, int HB, class Pager>
+__device__ inline void stream_range_from(WaveState<HB>& st, const Pager& pg,
+                                         const u32x4 (&qf)[HB][4], int t0, int t1, int lim,
+                                         int lane, typename Pager::Pages pa,
+                                         typename Pager::Pages pb) {
+  TileRegs r;
+  for (int t = t0; t < t1; ++t) {
+    pg.issue(t, pa, r);
+    pa = pb;
+    pb = pg.lookup(t + 2);
+    compute_tile<Elem, HB>(st, r, qf, t, lim, lane);
+  }
+}
+
 template <class Elem, int HB, class Pager>
 __device__ inline void stream_range(WaveState<HB>& st, const Pager& pg, const u32x4 (&qf)[HB][4],
                                     int t0, int t1, int lim, int lane) {
   if (t0 >= t1) return;
-  TileRegs ra, rb;
-  typename Pager::Pages pa = pg.lookup(t0);
-  pg.issue(t0, pa, ra);
-  typename Pager::Pages pb = pg.lookup(t0 + 1);
-  for (int t = t0;; t += 2) {
-    pg.issue(t + 1, pb, rb);
-    pa = pg.lookup(t + 2);
-    compute_tile<Elem, HB>(st, ra, qf, t, lim, lane);
-    if (t + 1 >= t1) break;
-    pg.issue(t + 2, pa, ra);
-    pb = pg.lookup(t + 3);
-    compute_tile<Elem, HB>(st, rb, qf, t + 1, lim, lane);
-    if (t + 2 >= t1) break;
-  }
+  stream_range_from<Elem, HB>(st, pg, qf, t0, t1, lim, lane, pg.lookup(t0), pg.lookup(t0 + 1));
 }
 
 // ---------------------------------------------------------------------------------
 // Work-unit resolution.
 // ---------------------------------------------------------------------------------
 struct Unit {
-  int row, kvh, split, tb, te, len, slot_base;  // slot_base: queue-mode slot of split 0
+  int row, kvh, split, tb, te, len;
+  int slot_base, row_splits;  // queue mode: slot of split 0 and the row's split count
   bool valid;
 };
 
 __device__ inline int ceil_tiles(int len) { return (len + kTile - 1) / kTile; }
 
 template <int MODE>
-__device__ inline Unit resolve_unit(const DecodeArgs& a) {
+__device__ inline Unit resolve_unit(const DecodeArgs& a, int idx) {
   Unit u;
   u.valid = true;
   u.slot_base = 0;
-  const int idx = blockIdx.x;
+  u.row_splits = 1;
   if (MODE == kDirect) {
     u.row = idx / a.hkv;
     u.kvh = idx - u.row * a.hkv;
@@ -464,11 +468,11 @@ __device__ inline Unit resolve_unit(const DecodeArgs& a) {
     u.te = (int)(((long)total * (u.split + 1)) / a.num_splits);
   } else {
     const int32_t* w = a.work_items + (long)idx * 5;
-    u.row = uniform(w[0]);
-    u.kvh = uniform(w[1]);
-    u.split = uniform(w[2]);
-    u.tb = uniform(w[3]);
-    u.te = uniform(w[4]);
+    u.row = load_scalar(w + 0);
+    u.kvh = load_scalar(w + 1);
+    u.split = load_scalar(w + 2);
+    u.tb = load_scalar(w + 3);
+    u.te = load_scalar(w + 4);
     // Malformed items are skipped instead of addressing outside the buffers.
     if (u.row < 0 || u.row >= a.batch || u.kvh < 0 || u.kvh >= a.hkv || u.split < 0) {
       u.valid = false;
@@ -476,9 +480,9 @@ __device__ inline Unit resolve_unit(const DecodeArgs& a) {
     }
     u.len = row_length(a, u.row);
     u.slot_base = uniform(a.split_offsets[u.row]);
-    const int row_splits = uniform(a.split_offsets[u.row + 1]) - u.slot_base;
+    u.row_splits = uniform(a.split_offsets[u.row + 1]) - u.slot_base;
     const int total = ceil_tiles(u.len);
-    if (u.split >= row_splits) u.valid = false;
+    if (u.split >= u.row_splits) u.valid = false;
     if (u.tb < 0) u.tb = 0;
     if (u.te > total) u.te = total;
     if (u.slot_base < 0 || u.slot_base + u.split >= a.total_slots) u.valid = false;
@@ -486,17 +490,53 @@ __device__ inline Unit resolve_unit(const DecodeArgs& a) {
   return u;
 }
 
+// ---------------------------------------------------------------------------------
+// Partial-state stores and loads.  With the fused merge another workgroup (possibly on
+// another XCD, behind another L2) reads the states in the same launch.  They are then
+// written with agent-scope atomic stores (write-through to the coherence point) and
+// read with agent-scope atomic loads; the writer waits for its stores to complete
+// before it counts its arrival.  That replaces an agent-scope release fence, which
+// would write back the whole L2 on every arrival.
+// ---------------------------------------------------------------------------------
+__device__ inline void put_f32(float* p, float v, bool coherent) {
+  if (coherent) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else *p = v;
+}
+__device__ inline void put_f32x4(float* p, f32x4 v, bool coherent) {
+  if (coherent) {
+    __hip_atomic_store((uint64_t*)p, __builtin_bit_cast(uint64_t, f32x2{v[0], v[1]}),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store((uint64_t*)p + 1, __builtin_bit_cast(uint64_t, f32x2{v[2], v[3]}),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    *(f32x4*)p = v;
+  }
+}
+template <bool COHERENT>
+__device__ inline float get_f32(const float* p) {
+  if (COHERENT) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return *p;
+}
+template <bool COHERENT>
+__device__ inline f32x2 get_f32x2(const float* p) {
+  if (COHERENT)
+    return __builtin_bit_cast(f32x2, __hip_atomic_load((const uint64_t*)p, __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT));
+  return *(const f32x2*)p;
+}
+// Waits until every memory access this wave issued has completed.
+__device__ inline void wait_memory() { __builtin_amdgcn_s_waitcnt(0); }
+
 // Neutral partial state of an empty split (cuh:340-363): m = -FLT_MAX, l = 0, acc = 0.
 __device__ inline void write_neutral(const DecodeArgs& a, long state0, long state_stride,
-                                     int G, int tid, int nthreads) {
+                                     int G, int tid, int nthreads, bool coherent) {
   for (int idx = tid; idx < G * (kD / 4); idx += nthreads) {
     const int h = idx / (kD / 4), d = (idx % (kD / 4)) * 4;
     const long s = state0 + (long)h * state_stride;
-    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-    *(f32x4*)(a.part_acc + s * kD + d) = z;
+    put_f32x4(a.part_acc + s * kD + d, f32x4{0.f, 0.f, 0.f, 0.f}, coherent);
     if (d == 0) {
-      a.part_m[s] = -FLT_MAX;
-      a.part_l[s] = 0.f;
+      put_f32(a.part_m + s, -FLT_MAX, coherent);
+      put_f32(a.part_l + s, 0.f, coherent);
     }
   }
 }
@@ -509,50 +549,163 @@ __device__ inline void store_out4(uint8_t* out, long elem, f32x4 v) {
   *(u32x2*)(out + elem * 2) = w;
 }
 
-// Last-arriver merge of one (row, kv head) group's partial states (fused merge,
-// cuh:648-716).  Slots of empty splits are skipped by recomputing the builder's split
-// bounds, so rows with more splits than tiles are merged correctly.
+__device__ inline float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+__device__ inline float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+// ---------------------------------------------------------------------------------
+// LSE merge of one query head's partial states by one wave (cuh:719-784): M = max m,
+// L = sum e^(m - M) l, A = sum e^(m - M) acc, O = A / L (0 when L == 0).  Slot s's state
+// index is base + s * stride.  In queue mode, slots of splits the builder leaves empty
+// (split0 + s of nsplit splits over `total` tiles) hold no state and are skipped; the
+// reference reads them uninitialised.  All loads of a chunk of up to 32 slots are
+// issued together: lane s loads slot s's (m, l) and each lane its two dims of every
+// slot's acc.  Lane owns output dims 2*lane, 2*lane + 1 of `out` (128 elements).
+// ---------------------------------------------------------------------------------
+constexpr int kMergeChunk = 32;
+
+template <class Elem, bool QUEUE, bool COHERENT>
+__device__ inline void merge_head(const float* pm, const float* pl, const float* pacc, long base,
+                                  long stride, int count, int total, int nsplit, int split0,
+                                  uint8_t* out, int lane) {
+  auto live = [&](int s) {
+    return s < count &&
+           !(QUEUE && (long)total * (split0 + s) / nsplit == (long)total * (split0 + s + 1) / nsplit);
+  };
+  float M = -FLT_MAX, L = 0.f;
+  f32x2 A = {0.f, 0.f};
+  for (int c0 = 0; c0 < count; c0 += kMergeChunk) {
+    const int n = count - c0 < kMergeChunk ? count - c0 : kMergeChunk;
+    // Issue the chunk's loads together (tail slots re-read the last index).
+    const int s_lane = c0 + (lane < n ? lane : n - 1);
+    const float ms = get_f32<COHERENT>(pm + base + (long)s_lane * stride);
+    const float ls = get_f32<COHERENT>(pl + base + (long)s_lane * stride);
+    f32x2 v[kMergeChunk];
+#pragma unroll
+    for (int j = 0; j < kMergeChunk; ++j) {
+      const int s = c0 + (j < n ? j : n - 1);
+      v[j] = get_f32x2<COHERENT>(pacc + (base + (long)s * stride) * kD + 2 * lane);
+    }
+    const bool ok = lane < n && live(c0 + lane);
+    // Online rescale across chunks: fold this chunk's max into M.
+    const float cm = wave_max(ok ? ms : -FLT_MAX);
+    const float m_new = fmaxf(M, cm);
+    const float corr = __builtin_amdgcn_exp2f((M - m_new) * kLog2e);
+    M = m_new;
+    const float w = ok ? __builtin_amdgcn_exp2f((ms - M) * kLog2e) : 0.f;
+    L = L * corr + wave_sum(w * ls);
+    A *= corr;
+#pragma unroll
+    for (int j = 0; j < kMergeChunk; ++j) {
+      const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), j));
+      A[0] += wj != 0.f ? wj * v[j][0] : 0.f;  // select, not multiply: skipped slots may hold NaN
+      A[1] += wj != 0.f ? wj * v[j][1] : 0.f;
+    }
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  *(uint32_t*)(out + 4 * lane) = Elem::bits(A[0] * inv) | (Elem::bits(A[1] * inv) << 16);
+}
+
+// Fused merge of query head qh of a work-queue row by one wave (last arriver of the
+// row's (row, kv head) group; cuh:648-716).
 template <class Elem>
-__device__ void fused_merge_group(const DecodeArgs& a, const Unit& u, int qh0, int G, int tid,
-                                  int nthreads) {
-  const int s_begin = a.split_offsets[u.row];
-  const int s_end = a.split_offsets[u.row + 1];
-  const int nsplit = s_end - s_begin;
-  const int total = ceil_tiles(u.len);
+__device__ inline void fused_merge_head(const DecodeArgs& a, const Unit& u, int qh, int lane) {
   const int out_row = a.out_indices ? a.out_indices[u.row] : u.row;
   if (out_row < 0 || out_row >= a.out_rows) return;
-  if (s_begin < 0 || s_end > a.total_slots || nsplit <= 0) return;  // malformed offsets
-  for (int idx = tid; idx < G * (kD / 4); idx += nthreads) {
-    const int h = idx / (kD / 4), d = (idx % (kD / 4)) * 4;
-    const int qh = qh0 + h;
-    float M = -FLT_MAX;
-    for (int s = 0; s < nsplit; ++s) {
-      if ((long)total * s / nsplit == (long)total * (s + 1) / nsplit) continue;
-      const long st = (long)(s_begin + s) * a.hq + qh;
-      M = fmaxf(M, __hip_atomic_load(a.part_m + st, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  const int count = u.slot_base + u.row_splits > a.total_slots ? a.total_slots - u.slot_base
+                                                                : u.row_splits;
+  merge_head<Elem, true, true>(a.part_m, a.part_l, a.part_acc, (long)u.slot_base * a.hq + qh, a.hq,
+                               count, ceil_tiles(u.len), u.row_splits, 0,
+                               a.out + ((long)out_row * a.hq + qh) * kD * 2, lane);
+}
+
+// Number of work items of the unit's (row, kv head): one per non-empty split.
+__device__ inline int expected_arrivals(const Unit& u) {
+  const int total = ceil_tiles(u.len);
+  return u.row_splits < total ? u.row_splits : total;
+}
+
+// ---------------------------------------------------------------------------------
+// Pieces shared by the two decode paths.
+// ---------------------------------------------------------------------------------
+// Partial-state addressing: state index of head h is state0 + h * stride.
+template <int MODE>
+__device__ inline void unit_states(const DecodeArgs& a, const Unit& u, int qh0, long& state0,
+                                   long& stride) {
+  state0 = 0;
+  stride = 1;
+  if (MODE == kSplit) {
+    state0 = ((long)u.row * a.hq + qh0) * a.num_splits + u.split;
+    stride = a.num_splits;
+  } else if (MODE == kQueue) {
+    state0 = (long)(u.slot_base + u.split) * a.hq + qh0;
+  }
+}
+
+// Q^T operand: lane (g, c) holds head hb*16 + c, dims 32kk + 8g .. +8.
+template <int HB>
+__device__ inline void load_q(const DecodeArgs& a, int row, int qh0, int lane, u32x4 (&qf)[HB][4]) {
+  const int c = lane & 15, g = lane >> 4;
+  int q_row = a.q_indices ? a.q_indices[row] : row;
+  q_row = q_row < 0 ? 0 : (q_row >= a.q_rows ? a.q_rows - 1 : q_row);
+#pragma unroll
+  for (int hb = 0; hb < HB; ++hb) {
+    const int h = hb * 16 + c;
+    const uint8_t* qp = a.q + (((long)q_row * a.hq + qh0 + h) * kD + 8 * g) * 2;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      qf[hb][kk] = h < a.group ? *(const u32x4*)(qp + kk * 64) : z;
     }
-    float L = 0.f;
-    f32x4 A = {0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < nsplit; ++s) {
-      if ((long)total * s / nsplit == (long)total * (s + 1) / nsplit) continue;
-      const long st = (long)(s_begin + s) * a.hq + qh;
-      const float ms = __hip_atomic_load(a.part_m + st, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const float ls = __hip_atomic_load(a.part_l + st, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const float w = __builtin_amdgcn_exp2f((ms - M) * kLog2e);
-      L += w * ls;
-      const f32x4 acc = *(const f32x4*)(a.part_acc + st * kD + d);
-      A += w * acc;
-    }
-    const float inv = L > 0.f ? 1.f / L : 0.f;
-    store_out4<Elem>(a.out, ((long)out_row * a.hq + qh) * kD + d, A * inv);
+  }
+}
+
+template <int HB>
+__device__ inline void init_state(WaveState<HB>& st) {
+#pragma unroll
+  for (int hb = 0; hb < HB; ++hb) {
+    st.m[hb] = -FLT_MAX;
+    st.mx[hb] = -FLT_MAX;
+    st.l[hb] = 0.f;
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) st.o[hb][jj] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+}
+
+template <class Elem, int HB, bool FAST>
+__device__ inline void stream_unit(const DecodeArgs& a, WaveState<HB>& st, const u32x4 (&qf)[HB][4],
+                                   int row, int kvh, int t0, int t1, int len, int lane,
+                                   bool have_first = false, FastPager::Pages f0 = {},
+                                   FastPager::Pages f1 = {}) {
+  const long lim_l = (long)t1 * kTile;
+  const int lim = uniform(lim_l < len ? (int)lim_l : len);
+  if (FAST) {
+    FastPager pg(a, row, kvh, lim, lane);
+    if (have_first) stream_range_from<Elem, HB>(st, pg, qf, t0, t1, lim, lane, f0, f1);
+    else stream_range<Elem, HB>(st, pg, qf, t0, t1, lim, lane);
+  } else {
+    GenericPager pg(a, row, kvh, lim, lane);
+    stream_range<Elem, HB>(st, pg, qf, t0, t1, lim, lane);
+  }
+#pragma unroll
+  for (int hb = 0; hb < HB; ++hb) {
+    st.l[hb] = head_sum(st.l[hb]);
+    st.mx[hb] = head_max(st.mx[hb]);
   }
 }
 
 // ---------------------------------------------------------------------------------
 // The decode kernel.
 // ---------------------------------------------------------------------------------
-// G <= 16 (one head block) keeps two waves per SIMD (<= 256 registers each); G <= 32
-// doubles the accumulators and runs one wave per SIMD with the AGPR file available.
+// Register budget: G <= 16 (one head block) must fit two waves per SIMD (<= 256 registers
+// each); G <= 32 doubles the accumulators and may use the whole register file.
 template <class Elem, int HB, bool FAST, int MODE, int NW>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(HB == 1 ? 2 : 1)))
 void decode_kernel(DecodeArgs a) {
@@ -565,68 +718,47 @@ void decode_kernel(DecodeArgs a) {
   const int c = lane & 15, g = lane >> 4;
   const int G = a.group;
 
-  const Unit u = resolve_unit<MODE>(a);
-  if (!u.valid) return;
-  const int qh0 = u.kvh * G;
-
-  // Partial-state addressing: state index of head h is state0 + h * state_stride.
-  long state0 = 0, state_stride = 1;
-  if (MODE == kSplit) {
-    state0 = ((long)u.row * a.hq + qh0) * a.num_splits + u.split;
-    state_stride = a.num_splits;
-  } else if (MODE == kQueue) {
-    state0 = (long)(u.slot_base + u.split) * a.hq + qh0;
-    state_stride = 1;
+  // Work-queue units: issue this wave's first two block-table reads together with the
+  // row metadata loads (they need only the work item), shortening the dependent chain
+  // work item -> row metadata -> table -> K/V by one memory round trip.
+  FastPager::Pages first0 = {}, first1 = {};
+  int first_tile = -1;
+  if (MODE == kQueue && FAST) {
+    const int32_t* w = a.work_items + (long)blockIdx.x * 5;
+    int row = load_scalar(w + 0), kvh = load_scalar(w + 1);
+    const int tb = load_scalar(w + 3), te = load_scalar(w + 4);
+    row = row < 0 ? 0 : (row >= a.batch ? a.batch - 1 : row);
+    kvh = kvh < 0 ? 0 : (kvh >= a.hkv ? a.hkv - 1 : kvh);
+    const int n = te > tb ? te - tb : 0;
+    first_tile = uniform(tb + (n * wave) / kWaves);
+    const FastPager pg(a, row, kvh, 0, lane);
+    first0 = pg.lookup(first_tile);
+    first1 = pg.lookup(first_tile + 1);
   }
 
+  const Unit u = resolve_unit<MODE>(a, blockIdx.x);
+  if (!u.valid) return;
+  const int qh0 = u.kvh * G;
+  long state0, state_stride;
+  unit_states<MODE>(a, u, qh0, state0, state_stride);
+  const bool fused = MODE == kQueue && a.merge_counters != nullptr;
+
   if (MODE != kDirect && u.tb >= u.te) {
-    write_neutral(a, state0, state_stride, G, tid, kThreads);
+    write_neutral(a, state0, state_stride, G, tid, kThreads, fused);
     return;
   }
 
-  // Q^T operand: lane (g, c) holds head hb*16 + c, dims 32kk + 8g .. +8.
-  int q_row = a.q_indices ? a.q_indices[u.row] : u.row;
-  q_row = q_row < 0 ? 0 : (q_row >= a.q_rows ? a.q_rows - 1 : q_row);
   u32x4 qf[HB][4];
-#pragma unroll
-  for (int hb = 0; hb < HB; ++hb) {
-    const int h = hb * 16 + c;
-    const uint8_t* qp = a.q + (((long)q_row * a.hq + qh0 + h) * kD + 8 * g) * 2;
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const u32x4 z = {0u, 0u, 0u, 0u};
-      qf[hb][kk] = h < G ? *(const u32x4*)(qp + kk * 64) : z;
-    }
-  }
-
+  load_q<HB>(a, u.row, qh0, lane, qf);
   WaveState<HB> st;
-#pragma unroll
-  for (int hb = 0; hb < HB; ++hb) {
-    st.m[hb] = -FLT_MAX;
-    st.mx[hb] = -FLT_MAX;
-    st.l[hb] = 0.f;
-#pragma unroll
-    for (int jj = 0; jj < 8; ++jj) st.o[hb][jj] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
+  init_state<HB>(st);
 
   // Contiguous sub-range of the unit's tiles for this wave.
   const int n = u.te - u.tb;
   const int w0 = uniform(u.tb + (n * wave) / kWaves);
   const int w1 = uniform(u.tb + (n * (wave + 1)) / kWaves);
-  const long lim_l = (long)w1 * kTile;
-  const int lim = uniform(lim_l < u.len ? (int)lim_l : u.len);
-  if (FAST) {
-    FastPager pg(a, u.row, u.kvh, lim, lane);
-    stream_range<Elem, HB>(st, pg, qf, w0, w1, lim, lane);
-  } else {
-    GenericPager pg(a, u.row, u.kvh, lim, lane);
-    stream_range<Elem, HB>(st, pg, qf, w0, w1, lim, lane);
-  }
-#pragma unroll
-  for (int hb = 0; hb < HB; ++hb) {
-    st.l[hb] = head_sum(st.l[hb]);
-    st.mx[hb] = head_max(st.mx[hb]);
-  }
+  stream_unit<Elem, HB, FAST>(a, st, qf, u.row, u.kvh, w0, w1, u.len, lane, w0 == first_tile,
+                              first0, first1);
 
   // Combine the waves one chunk of heads at a time (16 heads with 4 waves, 8 with 8, so
   // the O staging stays at 32 KB).  LDS: m[w][32] (reference max), l[w][32],
@@ -695,42 +827,39 @@ void decode_kernel(DecodeArgs a) {
           for (int w = 0; w < kWaves; ++w) Mx = fmaxf(Mx, sm_x[w * 32 + h]);
           const float rescale = __builtin_amdgcn_exp2f(M - Mx);
           const long s = state0 + (long)h * state_stride;
-          *(f32x4*)(a.part_acc + s * kD + d) = A * rescale;
+          put_f32x4(a.part_acc + s * kD + d, A * rescale, fused);
           if (d == 0) {
-            a.part_m[s] = Mx * kLn2;
-            a.part_l[s] = L * rescale;
+            put_f32(a.part_m + s, Mx * kLn2, fused);
+            put_f32(a.part_l + s, L * rescale, fused);
           }
         }
       }
     }
   }
 
-  if (MODE == kQueue && a.merge_counters != nullptr) {
+  if (fused) {
     __shared__ int last;
+    wait_memory();  // this thread's partial-state stores have completed
     __syncthreads();
     if (tid == 0) {
-      const int nsplit = a.split_offsets[u.row + 1] - a.split_offsets[u.row];
-      const int total = ceil_tiles(u.len);
-      const int expected = nsplit < total ? nsplit : total;  // non-empty splits
-      __threadfence();
-      const int old = atomicAdd(a.merge_counters + (long)u.row * a.hkv + u.kvh, 1);
-      last = (old == expected - 1);
+      const int old = __hip_atomic_fetch_add(a.merge_counters + (long)u.row * a.hkv + u.kvh, 1,
+                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = old == expected_arrivals(u) - 1;
     }
     __syncthreads();
     if (last) {
-      __threadfence();
-      fused_merge_group<Elem>(a, u, qh0, G, tid, kThreads);
-      __syncthreads();
-      if (tid == 0) a.merge_counters[(long)u.row * a.hkv + u.kvh] = 0;
+      for (int h = wave; h < G; h += kWaves) fused_merge_head<Elem>(a, u, qh0 + h, lane);
+      if (tid == 0)
+        __hip_atomic_store(a.merge_counters + (long)u.row * a.hkv + u.kvh, 0, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
 
 // ---------------------------------------------------------------------------------
-// Segmented LSE merge: one wave per (row, query head); lane owns dims 2*lane, 2*lane+1.
-// Grid-split slots are ((row*Hq + qh)*S + s) (cuh:719-751); work-queue slots are
-// (split_offsets[row] + s)*Hq + qh (cuh:753-784), skipping splits the builder leaves
-// empty (the reference reads those slots uninitialised).
+// Segmented LSE merge kernel: one wave per (row, query head).  Grid-split slots are
+// ((row*Hq + qh)*S + s) (cuh:719-751); work-queue slots are (split_offsets[row] + s)*Hq
+// + qh (cuh:753-784).
 // ---------------------------------------------------------------------------------
 struct MergeArgs {
   const float* part_m;
@@ -746,23 +875,6 @@ struct MergeArgs {
   int32_t context, max_tokens;   // split mode length fallback / clamp
 };
 
-__device__ inline float wave_max(float x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-  return x;
-}
-__device__ inline float wave_sum(float x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
-  return x;
-}
-
-// One wave per (row, query head).  After the row's slot range is known, every load of a
-// chunk of up to 32 slots is issued at once: lane s loads slot s's (m, l) and each lane
-// loads its two dims of every slot's acc.  The merge then costs two memory round trips
-// (row metadata, slot data) instead of one per slot.
-constexpr int kMergeChunk = 32;
-
 template <class Elem, bool QUEUE>
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   const int wave_id = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -770,11 +882,11 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   if (wave_id >= a.batch * a.hq) return;
   const int row = uniform(wave_id / a.hq);
   const int qh = uniform(wave_id - row * a.hq);
-  int first = 0, count, total = 0, nsplit, split0 = 0;
-  long stride;
+  int count, total = 0, nsplit = 1, split0 = 0;
+  long base, stride;
   if (QUEUE) {
     const int o0 = uniform(a.split_offsets[row]), o1 = uniform(a.split_offsets[row + 1]);
-    first = o0 < 0 ? 0 : o0;
+    const int first = o0 < 0 ? 0 : o0;
     const int last = o1 > a.total_slots ? a.total_slots : o1;
     count = last - first;
     nsplit = o1 - o0;
@@ -782,53 +894,17 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     int len = uniform(a.seq_lens[row]);
     if (len > a.max_tokens) len = a.max_tokens;
     total = ceil_tiles(len < 0 ? 0 : len);
+    base = (long)first * a.hq + qh;
     stride = a.hq;
   } else {
     count = a.num_splits;
-    nsplit = count;
+    base = ((long)row * a.hq + qh) * a.num_splits;
     stride = 1;
-  }
-  const long base = QUEUE ? (long)first * a.hq + qh : ((long)row * a.hq + qh) * a.num_splits;
-  // Work-queue slots of splits the builder leaves empty hold no state: skip them.
-  auto live = [&](int s) {
-    return s < count &&
-           !(QUEUE && (long)total * (split0 + s) / nsplit == (long)total * (split0 + s + 1) / nsplit);
-  };
-  float M = -FLT_MAX, L = 0.f;
-  f32x2 A = {0.f, 0.f};
-  for (int c0 = 0; c0 < count; c0 += kMergeChunk) {
-    const int n = count - c0 < kMergeChunk ? count - c0 : kMergeChunk;
-    // Issue the chunk's loads together (tail slots re-read the last live index).
-    const int s_lane = c0 + (lane < n ? lane : n - 1);
-    const float ms = a.part_m[base + (long)s_lane * stride];
-    const float ls = a.part_l[base + (long)s_lane * stride];
-    f32x2 v[kMergeChunk];
-#pragma unroll
-    for (int j = 0; j < kMergeChunk; ++j) {
-      const int s = c0 + (j < n ? j : n - 1);
-      v[j] = *(const f32x2*)(a.part_acc + (base + (long)s * stride) * kD + 2 * lane);
-    }
-    const bool ok = lane < n && live(c0 + lane);
-    // Online rescale across chunks: fold this chunk's max into M.
-    const float cm = wave_max(ok ? ms : -FLT_MAX);
-    const float m_new = fmaxf(M, cm);
-    const float corr = __builtin_amdgcn_exp2f((M - m_new) * kLog2e);
-    M = m_new;
-    const float w = ok ? __builtin_amdgcn_exp2f((ms - M) * kLog2e) : 0.f;
-    L = L * corr + wave_sum(w * ls);
-    A *= corr;
-#pragma unroll
-    for (int j = 0; j < kMergeChunk; ++j) {
-      const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), j));
-      A[0] += wj != 0.f ? wj * v[j][0] : 0.f;  // select, not multiply: skipped slots may hold NaN
-      A[1] += wj != 0.f ? wj * v[j][1] : 0.f;
-    }
   }
   const int out_row = a.out_indices ? a.out_indices[row] : row;
   if (out_row < 0 || out_row >= a.out_rows) return;
-  const float inv = L > 0.f ? 1.f / L : 0.f;
-  const uint32_t word = Elem::bits(A[0] * inv) | (Elem::bits(A[1] * inv) << 16);
-  *(uint32_t*)(a.out + (((long)out_row * a.hq + qh) * kD + 2 * lane) * 2) = word;
+  merge_head<Elem, QUEUE, false>(a.part_m, a.part_l, a.part_acc, base, stride, count, total, nsplit,
+                                 split0, a.out + ((long)out_row * a.hq + qh) * kD * 2, lane);
 }
 
 // ---------------------------------------------------------------------------------

@@ -176,8 +176,10 @@ def test_workqueue_stages_equal_combined(ext, gpu):
 
 
 def test_workqueue_matches_indexed_split_grid(ext, gpu):
-    """Fixed S splits per row give the same tile ranges in both routes, so the outputs
-    are bit-identical (empty slots are neutral in one route and skipped in the other)."""
+    """Fixed S splits per row give the same tile ranges in both routes (empty slots are
+    neutral in one route and skipped in the other).  A unit may be streamed by one wave
+    in one route and by a whole workgroup in the other (short-unit packing depends on its
+    neighbours), so the outputs agree to fp32 rounding rather than bit for bit."""
     lengths = [100, 2500, 40]
     splits = 9
     case = make_case(lengths, 32, 8, 16, F16, seed=11)
@@ -189,7 +191,9 @@ def test_workqueue_matches_indexed_split_grid(ext, gpu):
     ext.paged_attention_indexed(q, k, v, bt, sl, idx, idx, grid_out, _ws(3, 32, splits, gpu),
                                 max(lengths), 16, splits)
     torch.cuda.synchronize()
-    assert torch.equal(queue_out, grid_out)
+    assert (queue_out.float() - grid_out.float()).abs().max().item() < 1e-3
+    ref = oracle.paged_decode(case.q, case.k_pages, case.v_pages, case.block_table, case.seq_lens)
+    assert_parity(grid_out, ref)
 
 
 def test_split_partial_states_match_oracle(ext, gpu):
