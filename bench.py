@@ -53,6 +53,9 @@ def parse_args():
                    help="configuration (default c4, the headline; the others are reported "
                         "for DESIGN.md and are not the metric)")
     p.add_argument("--fused-merge", action="store_true", help="single-launch fused merge variant")
+    p.add_argument("--graph", action="store_true",
+                   help="capture the timed steps into one HIP graph and replay it (as the "
+                        "reference harness replays captured steps, benchmark_serving_trace.py:1439-1452)")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time budget")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--seed", type=int, default=20260623)
@@ -101,6 +104,7 @@ def main():
     metas = [wl.compile_step(w, i, dev) for i in range(len(w.steps))]
     ws = wl.workspace_for(w, metas, dev)
     q_pool = wl.make_q_pool(w, dev)
+    wl.bind_queries(metas, q_pool)
     k0, v0 = wl.make_kv_pool(w, dev)
     # Enough replicas that the bytes read between two uses of one replica exceed twice the
     # 256 MB Infinity Cache (at most 48 GB of replicas).
@@ -117,8 +121,26 @@ def main():
         kp, vp = pools[k % len(pools)]
         wl.run_step(ext, w, metas[i], i, q_pool, kp, vp, ws)
 
-    for k in range(args.warmup):
-        step(k)
+    graph = None
+    if args.graph:
+        # Warm up on the capture stream (per-stream scratch is allocated outside capture),
+        # then capture exactly args.steps steps into one graph.
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for k in range(args.warmup):
+                step(k)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(graph, stream=side):
+                for k in range(args.steps):
+                    step(k)
+        torch.cuda.synchronize()
+        graph.replay()
+    else:
+        for k in range(args.warmup):
+            step(k)
     torch.cuda.synchronize()
 
     # Timed region: exactly args.steps steps, synchronised on both sides.
@@ -126,8 +148,11 @@ def main():
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     start.record()
-    for k in range(args.steps):
-        step(k)
+    if graph is not None:
+        graph.replay()
+    else:
+        for k in range(args.steps):
+            step(k)
     stop.record()
     torch.cuda.synchronize()
     wall_s = time.perf_counter() - t0
@@ -208,6 +233,7 @@ def main():
                    "page_size": w.page_size,
                    "splits": "auto (mi355x planner)" if w.auto_splits else w.splits,
                    "fused_merge": bool(args.fused_merge),
+                   "launch": "hip graph replay" if args.graph else "eager",
                    "mean_kv_mb_per_step": round(sum(m.kv_bytes for m in metas) / n_trace / 1e6, 2),
                    "cache_basis": f"HBM-cold ({len(pools)} rotated KV pool replicas)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS,

@@ -30,6 +30,10 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <mutex>
+#include <tuple>
+#include <vector>
+
 #include "pkv.h"
 
 namespace pkv {
@@ -613,8 +617,9 @@ __device__ inline void merge_head(const float* pm, const float* pl, const float*
   *(uint32_t*)(out + 4 * lane) = Elem::bits(A[0] * inv) | (Elem::bits(A[1] * inv) << 16);
 }
 
-// Fused merge of query head qh of a work-queue row by one wave (last arriver of the
-// row's (row, kv head) group; cuh:648-716).
+// Fused merge of query head qh of a work-queue row by one wave, run by the last work item
+// of the row's (row, kv head) group to finish (cuh:648-716).  Slots are
+// (split_offsets[row] + s)*Hq + qh.
 template <class Elem>
 __device__ inline void fused_merge_head(const DecodeArgs& a, const Unit& u, int qh, int lane) {
   const int out_row = a.out_indices ? a.out_indices[u.row] : u.row;
@@ -626,10 +631,40 @@ __device__ inline void fused_merge_head(const DecodeArgs& a, const Unit& u, int 
                                a.out + ((long)out_row * a.hq + qh) * kD * 2, lane);
 }
 
-// Number of work items of the unit's (row, kv head): one per non-empty split.
+// Work items of one (row, kv head): one per non-empty split (the builder emits no empty
+// ones), so the last arrival is the min(S_row, T)-th.
 __device__ inline int expected_arrivals(const Unit& u) {
   const int total = ceil_tiles(u.len);
   return u.row_splits < total ? u.row_splits : total;
+}
+
+// Arrival of a unit whose partial states are written (with agent-scope stores): the last
+// unit of its (row, kv head) merges the group's G heads and clears the counter.  With
+// `nwaves` > 1 the whole workgroup calls this (it synchronises); with 1, a single wave.
+template <class Elem>
+__device__ inline void arrive(const DecodeArgs& a, const Unit& u, int qh0, int lane, int wave,
+                              int nwaves) {
+  __shared__ int last_flag;
+  int32_t* counter = a.merge_counters + (long)u.row * a.hkv + u.kvh;
+  wait_memory();  // this wave's partial-state stores have completed
+  if (nwaves > 1) __syncthreads();
+  int last = 0;
+  if (wave == 0 && lane == 0) {
+    const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = old == expected_arrivals(u) - 1;
+    if (nwaves > 1) last_flag = last;
+  }
+  if (nwaves > 1) {
+    __syncthreads();
+    last = last_flag;
+  } else {
+    last = uniform(last);
+  }
+  if (last) {
+    for (int h = wave; h < a.group; h += nwaves) fused_merge_head<Elem>(a, u, qh0 + h, lane);
+    if (wave == 0 && lane == 0)
+      __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 // ---------------------------------------------------------------------------------
@@ -702,6 +737,62 @@ __device__ inline void stream_unit(const DecodeArgs& a, WaveState<HB>& st, const
 }
 
 // ---------------------------------------------------------------------------------
+// Small units (at most kSoloTiles tiles) are streamed by wave 0 alone: its state is final,
+// so it goes straight from registers to the workspace without the LDS combine, and the
+// other waves return at once, which frees their slots for the next workgroup on the CU.
+// No barrier is reached on this path.  Lanes (*, c) hold the softmax state of head
+// hb*16 + c; lane (g, c) holds O of heads hb*16 + 4g + i, dims 8c .. 8c + 7.
+// ---------------------------------------------------------------------------------
+constexpr int kSoloTiles = 2;
+
+template <class Elem, int HB, bool FAST, int MODE>
+__device__ void solo_unit(const DecodeArgs& a, const Unit& u, long state0, long stride, int lane,
+                          bool have_first, FastPager::Pages f0, FastPager::Pages f1) {
+  const int G = a.group, c = lane & 15, g = lane >> 4;
+  const int qh0 = u.kvh * G;
+  const bool fused = MODE == kQueue && a.merge_counters != nullptr;
+  u32x4 qf[HB][4];
+  load_q<HB>(a, u.row, qh0, lane, qf);
+  WaveState<HB> st;
+  init_state<HB>(st);
+  stream_unit<Elem, HB, FAST>(a, st, qf, u.row, u.kvh, u.tb, u.te, u.len, lane, have_first, f0, f1);
+  int out_row = 0;
+  if (MODE == kDirect) out_row = a.out_indices ? a.out_indices[u.row] : u.row;
+#pragma unroll
+  for (int hb = 0; hb < HB; ++hb) {
+    // Partial states relative to the true max (m = max score, l = sum exp(s - m),
+    // acc = sum exp(s - m) v; cuh:620-632); the direct op normalises instead.
+    const float rescale = __builtin_amdgcn_exp2f(st.m[hb] - st.mx[hb]);
+    const float inv_l = st.l[hb] > 0.f ? 1.f / st.l[hb] : 0.f;
+    if (MODE != kDirect && g == 0 && hb * 16 + c < G) {
+      const long s = state0 + (long)(hb * 16 + c) * stride;
+      put_f32(a.part_m + s, st.mx[hb] * kLn2, fused);
+      put_f32(a.part_l + s, st.l[hb] * rescale, fused);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int h = hb * 16 + 4 * g + i;  // lane 4g + i holds the state of head h
+      const float r = __shfl(MODE == kDirect ? inv_l : rescale, 4 * g + i);
+      const f32x4 lo = f32x4{st.o[hb][0][i], st.o[hb][1][i], st.o[hb][2][i], st.o[hb][3][i]} * r;
+      const f32x4 hi = f32x4{st.o[hb][4][i], st.o[hb][5][i], st.o[hb][6][i], st.o[hb][7][i]} * r;
+      if (h >= G) continue;
+      if (MODE == kDirect) {
+        if (out_row >= 0 && out_row < a.out_rows) {
+          const long e = ((long)out_row * a.hq + qh0 + h) * kD + 8 * c;
+          store_out4<Elem>(a.out, e, lo);
+          store_out4<Elem>(a.out, e + 4, hi);
+        }
+      } else {
+        float* dst = a.part_acc + (state0 + (long)h * stride) * kD + 8 * c;
+        put_f32x4(dst, lo, fused);
+        put_f32x4(dst + 4, hi, fused);
+      }
+    }
+  }
+  if (fused) arrive<Elem>(a, u, qh0, lane, 0, 1);
+}
+
+// ---------------------------------------------------------------------------------
 // The decode kernel.
 // ---------------------------------------------------------------------------------
 // Register budget: G <= 16 (one head block) must fit two waves per SIMD (<= 256 registers
@@ -748,13 +839,20 @@ void decode_kernel(DecodeArgs a) {
     return;
   }
 
+  const int n = u.te - u.tb;
+  if (n <= kSoloTiles) {
+    if (wave == 0)
+      solo_unit<Elem, HB, FAST, MODE>(a, u, state0, state_stride, lane, u.tb == first_tile, first0,
+                                      first1);
+    return;
+  }
+
   u32x4 qf[HB][4];
   load_q<HB>(a, u.row, qh0, lane, qf);
   WaveState<HB> st;
   init_state<HB>(st);
 
   // Contiguous sub-range of the unit's tiles for this wave.
-  const int n = u.te - u.tb;
   const int w0 = uniform(u.tb + (n * wave) / kWaves);
   const int w1 = uniform(u.tb + (n * (wave + 1)) / kWaves);
   stream_unit<Elem, HB, FAST>(a, st, qf, u.row, u.kvh, w0, w1, u.len, lane, w0 == first_tile,
@@ -837,23 +935,7 @@ void decode_kernel(DecodeArgs a) {
     }
   }
 
-  if (fused) {
-    __shared__ int last;
-    wait_memory();  // this thread's partial-state stores have completed
-    __syncthreads();
-    if (tid == 0) {
-      const int old = __hip_atomic_fetch_add(a.merge_counters + (long)u.row * a.hkv + u.kvh, 1,
-                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      last = old == expected_arrivals(u) - 1;
-    }
-    __syncthreads();
-    if (last) {
-      for (int h = wave; h < G; h += kWaves) fused_merge_head<Elem>(a, u, qh0 + h, lane);
-      if (tid == 0)
-        __hip_atomic_store(a.merge_counters + (long)u.row * a.hkv + u.kvh, 0, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
+  if (fused) arrive<Elem>(a, u, qh0, lane, wave, kWaves);
 }
 
 // ---------------------------------------------------------------------------------
@@ -1023,6 +1105,55 @@ int dispatch_merge(const MergeArgs& m, bool queue, int dtype, hipStream_t stream
   return PKV_OK;
 }
 
+// Scratch partial states for the direct op's internal split, one buffer per (device,
+// stream): launches on one stream run in order, so each buffer is only ever used by one
+// op at a time.  Allocated on the first launch on a stream that needs it (never while
+// the stream is being captured into a graph) and kept until the process ends.  Launches
+// that get no buffer (more than kMaxScratchStreams streams, capture before the first
+// launch, allocation failure) run the single-launch direct kernel instead.
+constexpr size_t kScratchBytes = 4u << 20;
+constexpr int kMaxScratchStreams = 64;
+
+float* stream_scratch(hipStream_t stream) {
+  static std::mutex mu;
+  static std::vector<std::tuple<int, hipStream_t, float*>> table;
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  for (const auto& e : table)
+    if (std::get<0>(e) == device && std::get<1>(e) == stream) return std::get<2>(e);
+  if ((int)table.size() >= kMaxScratchStreams) return nullptr;
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &capture) != hipSuccess || capture != hipStreamCaptureStatusNone)
+    return nullptr;
+  float* p = nullptr;
+  if (hipMalloc(&p, kScratchBytes) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  table.emplace_back(device, stream, p);
+  return p;
+}
+
+// Internal split count for a direct (num_splits == 1) launch.  One workgroup per
+// (row, kv head) streams at most ~37 GB/s (the per-CU load bandwidth of MI355X), so with
+// few rows the op is split into about 256 units of at least 4 tiles, merged by the merge
+// kernel from scratch partial states.  PKV_DIRECT_SPLIT=0 keeps the single launch.
+int direct_splits(const Geometry& g, int context) {
+  static const bool on = [] {
+    const char* e = getenv("PKV_DIRECT_SPLIT");
+    return !(e && e[0] == '0');
+  }();
+  const long units = (long)g.batch * g.hkv;
+  if (!on || units >= 128) return 1;
+  const int tiles = (context + kTile - 1) / kTile;
+  long s = (256 + units - 1) / units;
+  if (s > tiles / 4) s = tiles / 4;
+  const long per_split = (long)g.batch * g.hq * (kD + 2) * (long)sizeof(float);
+  if (s * per_split > (long)kScratchBytes) s = (long)kScratchBytes / per_split;
+  return s >= 2 ? (int)s : 1;
+}
+
 DecodeArgs base_args(const Geometry& g, const void* q, int q_rows, const void* k, const void* v,
                      const int32_t* table, void* out, int out_rows) {
   DecodeArgs a = {};
@@ -1070,8 +1201,16 @@ int run_grid(const Geometry& g, const void* q, int q_rows, const void* k, const 
   a.context = context;
   a.num_splits = num_splits;
   if (num_splits == 1) {
-    st = dispatch_decode<kDirect>(a, g.dtype, g.batch * g.hkv, stream);
-    return st == PKV_OK ? ok() : st;
+    const int internal = direct_splits(g, context);
+    float* scratch = internal > 1 ? stream_scratch(stream) : nullptr;
+    if (!scratch) {
+      st = dispatch_decode<kDirect>(a, g.dtype, g.batch * g.hkv, stream);
+      return st == PKV_OK ? ok() : st;
+    }
+    num_splits = internal;
+    ws = scratch;
+    ws_bytes = kScratchBytes;
+    a.num_splits = num_splits;
   }
   const size_t need = pkv_workspace_bytes(g.batch, g.hq, num_splits);
   if (!ws || ws_bytes < need)
