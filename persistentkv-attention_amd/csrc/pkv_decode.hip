@@ -575,30 +575,14 @@ __device__ inline float wave_sum(float x) {
 // ---------------------------------------------------------------------------------
 constexpr int kMergeChunk = 32;
 
-template <class Elem, bool QUEUE, bool COHERENT>
-__device__ inline void merge_head(const float* pm, const float* pl, const float* pacc, long base,
-                                  long stride, int count, int total, int nsplit, int split0,
-                                  uint8_t* out, int lane) {
-  auto live = [&](int s) {
-    return s < count &&
-           !(QUEUE && (long)total * (split0 + s) / nsplit == (long)total * (split0 + s + 1) / nsplit);
-  };
+// Running LSE merge held by one wave; lane owns output dims 2*lane, 2*lane + 1.
+struct LseAcc {
   float M = -FLT_MAX, L = 0.f;
   f32x2 A = {0.f, 0.f};
-  for (int c0 = 0; c0 < count; c0 += kMergeChunk) {
-    const int n = count - c0 < kMergeChunk ? count - c0 : kMergeChunk;
-    // Issue the chunk's loads together (tail slots re-read the last index).
-    const int s_lane = c0 + (lane < n ? lane : n - 1);
-    const float ms = get_f32<COHERENT>(pm + base + (long)s_lane * stride);
-    const float ls = get_f32<COHERENT>(pl + base + (long)s_lane * stride);
-    f32x2 v[kMergeChunk];
-#pragma unroll
-    for (int j = 0; j < kMergeChunk; ++j) {
-      const int s = c0 + (j < n ? j : n - 1);
-      v[j] = get_f32x2<COHERENT>(pacc + (base + (long)s * stride) * kD + 2 * lane);
-    }
-    const bool ok = lane < n && live(c0 + lane);
-    // Online rescale across chunks: fold this chunk's max into M.
+
+  // Folds in up to 32 states: lane j holds (ms, ls) of state j (valid when ok); v[j] holds
+  // this lane's two dims of state j's acc.
+  __device__ inline void fold(bool ok, float ms, float ls, const f32x2 (&v)[kMergeChunk]) {
     const float cm = wave_max(ok ? ms : -FLT_MAX);
     const float m_new = fmaxf(M, cm);
     const float corr = __builtin_amdgcn_exp2f((M - m_new) * kLog2e);
@@ -613,8 +597,36 @@ __device__ inline void merge_head(const float* pm, const float* pl, const float*
       A[1] += wj != 0.f ? wj * v[j][1] : 0.f;
     }
   }
-  const float inv = L > 0.f ? 1.f / L : 0.f;
-  *(uint32_t*)(out + 4 * lane) = Elem::bits(A[0] * inv) | (Elem::bits(A[1] * inv) << 16);
+
+  template <class Elem>
+  __device__ inline void store(uint8_t* out, int lane) const {
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    *(uint32_t*)(out + 4 * lane) = Elem::bits(A[0] * inv) | (Elem::bits(A[1] * inv) << 16);
+  }
+};
+
+template <bool QUEUE, bool COHERENT>
+__device__ inline void fold_slots(LseAcc& acc, const float* pm, const float* pl, const float* pacc,
+                                  long base, long stride, int count, int total, int nsplit,
+                                  int split0, int lane) {
+  auto live = [&](int s) {
+    return s < count &&
+           !(QUEUE && (long)total * (split0 + s) / nsplit == (long)total * (split0 + s + 1) / nsplit);
+  };
+  for (int c0 = 0; c0 < count; c0 += kMergeChunk) {
+    const int n = count - c0 < kMergeChunk ? count - c0 : kMergeChunk;
+    // Issue the chunk's loads together (tail slots re-read the last index).
+    const int s_lane = c0 + (lane < n ? lane : n - 1);
+    const float ms = get_f32<COHERENT>(pm + base + (long)s_lane * stride);
+    const float ls = get_f32<COHERENT>(pl + base + (long)s_lane * stride);
+    f32x2 v[kMergeChunk];
+#pragma unroll
+    for (int j = 0; j < kMergeChunk; ++j) {
+      const int s = c0 + (j < n ? j : n - 1);
+      v[j] = get_f32x2<COHERENT>(pacc + (base + (long)s * stride) * kD + 2 * lane);
+    }
+    acc.fold(lane < n && live(c0 + lane), ms, ls, v);
+  }
 }
 
 // Fused merge of query head qh of a work-queue row by one wave, run by the last work item
@@ -626,9 +638,10 @@ __device__ inline void fused_merge_head(const DecodeArgs& a, const Unit& u, int 
   if (out_row < 0 || out_row >= a.out_rows) return;
   const int count = u.slot_base + u.row_splits > a.total_slots ? a.total_slots - u.slot_base
                                                                 : u.row_splits;
-  merge_head<Elem, true, true>(a.part_m, a.part_l, a.part_acc, (long)u.slot_base * a.hq + qh, a.hq,
-                               count, ceil_tiles(u.len), u.row_splits, 0,
-                               a.out + ((long)out_row * a.hq + qh) * kD * 2, lane);
+  LseAcc acc;
+  fold_slots<true, true>(acc, a.part_m, a.part_l, a.part_acc, (long)u.slot_base * a.hq + qh, a.hq,
+                         count, ceil_tiles(u.len), u.row_splits, 0, lane);
+  acc.store<Elem>(a.out + ((long)out_row * a.hq + qh) * kD * 2, lane);
 }
 
 // Work items of one (row, kv head): one per non-empty split (the builder emits no empty
@@ -737,63 +750,165 @@ __device__ inline void stream_unit(const DecodeArgs& a, WaveState<HB>& st, const
 }
 
 // ---------------------------------------------------------------------------------
-// Small units (at most kSoloTiles tiles) are streamed by wave 0 alone: its state is final,
-// so it goes straight from registers to the workspace without the LDS combine, and the
-// other waves return at once, which frees their slots for the next workgroup on the CU.
-// No barrier is reached on this path.  Lanes (*, c) hold the softmax state of head
-// hb*16 + c; lane (g, c) holds O of heads hb*16 + 4g + i, dims 8c .. 8c + 7.
+// Writers of a unit's final state.  `Dest` addresses partial states: head h of the unit
+// goes to state index state0 + h * stride of (m, l, acc); `coherent` selects agent-scope
+// stores (fused merge).  Direct launches write the normalised output instead.
 // ---------------------------------------------------------------------------------
-constexpr int kSoloTiles = 2;
+struct Dest {
+  float* m;
+  float* l;
+  float* acc;
+  long state0, stride;
+  bool coherent;
+};
 
-template <class Elem, int HB, bool FAST, int MODE>
-__device__ void solo_unit(const DecodeArgs& a, const Unit& u, long state0, long stride, int lane,
-                          bool have_first, FastPager::Pages f0, FastPager::Pages f1) {
+// One wave's state is the unit's whole state: write it from registers.  Lanes (*, c) hold
+// the softmax state of head hb*16 + c; lane (g, c) holds O of heads hb*16 + 4g + i, dims
+// 8c .. 8c + 7.
+template <class Elem, int HB, bool DIRECT>
+__device__ inline void write_wave_state(const DecodeArgs& a, const WaveState<HB>& st, int qh0,
+                                        int out_row, const Dest& d, int lane) {
   const int G = a.group, c = lane & 15, g = lane >> 4;
-  const int qh0 = u.kvh * G;
-  const bool fused = MODE == kQueue && a.merge_counters != nullptr;
-  u32x4 qf[HB][4];
-  load_q<HB>(a, u.row, qh0, lane, qf);
-  WaveState<HB> st;
-  init_state<HB>(st);
-  stream_unit<Elem, HB, FAST>(a, st, qf, u.row, u.kvh, u.tb, u.te, u.len, lane, have_first, f0, f1);
-  int out_row = 0;
-  if (MODE == kDirect) out_row = a.out_indices ? a.out_indices[u.row] : u.row;
 #pragma unroll
   for (int hb = 0; hb < HB; ++hb) {
     // Partial states relative to the true max (m = max score, l = sum exp(s - m),
     // acc = sum exp(s - m) v; cuh:620-632); the direct op normalises instead.
     const float rescale = __builtin_amdgcn_exp2f(st.m[hb] - st.mx[hb]);
     const float inv_l = st.l[hb] > 0.f ? 1.f / st.l[hb] : 0.f;
-    if (MODE != kDirect && g == 0 && hb * 16 + c < G) {
-      const long s = state0 + (long)(hb * 16 + c) * stride;
-      put_f32(a.part_m + s, st.mx[hb] * kLn2, fused);
-      put_f32(a.part_l + s, st.l[hb] * rescale, fused);
+    if (!DIRECT && g == 0 && hb * 16 + c < G) {
+      const long s = d.state0 + (long)(hb * 16 + c) * d.stride;
+      put_f32(d.m + s, st.mx[hb] * kLn2, d.coherent);
+      put_f32(d.l + s, st.l[hb] * rescale, d.coherent);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int h = hb * 16 + 4 * g + i;  // lane 4g + i holds the state of head h
-      const float r = __shfl(MODE == kDirect ? inv_l : rescale, 4 * g + i);
+      const float r = __shfl(DIRECT ? inv_l : rescale, 4 * g + i);
       const f32x4 lo = f32x4{st.o[hb][0][i], st.o[hb][1][i], st.o[hb][2][i], st.o[hb][3][i]} * r;
       const f32x4 hi = f32x4{st.o[hb][4][i], st.o[hb][5][i], st.o[hb][6][i], st.o[hb][7][i]} * r;
       if (h >= G) continue;
-      if (MODE == kDirect) {
+      if (DIRECT) {
         if (out_row >= 0 && out_row < a.out_rows) {
           const long e = ((long)out_row * a.hq + qh0 + h) * kD + 8 * c;
           store_out4<Elem>(a.out, e, lo);
           store_out4<Elem>(a.out, e + 4, hi);
         }
       } else {
-        float* dst = a.part_acc + (state0 + (long)h * stride) * kD + 8 * c;
-        put_f32x4(dst, lo, fused);
-        put_f32x4(dst + 4, hi, fused);
+        float* dst = d.acc + (d.state0 + (long)h * d.stride) * kD + 8 * c;
+        put_f32x4(dst, lo, d.coherent);
+        put_f32x4(dst + 4, hi, d.coherent);
       }
     }
   }
-  if (fused) arrive<Elem>(a, u, qh0, lane, 0, 1);
+}
+
+// Combines the NW waves' states of one unit through LDS, one chunk of heads at a time
+// (16 heads with 4 waves, 8 with 8, so the O staging stays at 32 KB), and writes the
+// result.  LDS: m[w][32] (reference max), l[w][32], x[w][32] (true max),
+// o[w][gh][128] with gh = min(G, chunk).  Starts with a barrier, so LDS can be reused by
+// consecutive units of one workgroup.
+template <class Elem, int HB, int NW, bool DIRECT>
+__device__ inline void combine_waves(const DecodeArgs& a, const WaveState<HB>& st, float* lds,
+                                     int qh0, int out_row, const Dest& d, int tid, int lane,
+                                     int wave) {
+  constexpr int kThreads = NW * 64;
+  constexpr int kChunk = NW == 8 ? 8 : 16;
+  const int G = a.group, c = lane & 15, g = lane >> 4;
+  const int gh = G < kChunk ? G : kChunk;
+  float* sm_m = lds;
+  float* sm_l = lds + NW * 32;
+  float* sm_x = lds + 2 * NW * 32;
+  float* sm_o = lds + 3 * NW * 32;
+  __syncthreads();
+  if (g == 0) {
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) {
+      const int h = hb * 16 + c;
+      if (h < G) {
+        sm_m[wave * 32 + h] = st.m[hb];
+        sm_l[wave * 32 + h] = st.l[hb];
+        sm_x[wave * 32 + h] = st.mx[hb];
+      }
+    }
+  }
+#pragma unroll
+  for (int hb = 0; hb < HB; ++hb) {
+#pragma unroll
+    for (int sub = 0; sub < 16 / kChunk; ++sub) {
+      const int h0 = hb * 16 + sub * kChunk;
+      const int nh = G - h0 < kChunk ? G - h0 : kChunk;
+      if (nh <= 0) break;
+      if (hb > 0 || sub > 0) __syncthreads();  // previous chunk's readers are done with sm_o
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int hh = 4 * g + i - sub * kChunk;
+        if (hh >= 0 && hh < nh) {
+          float* dst = sm_o + ((long)wave * gh + hh) * kD + 8 * c;
+          *(f32x4*)dst = f32x4{st.o[hb][0][i], st.o[hb][1][i], st.o[hb][2][i], st.o[hb][3][i]};
+          *(f32x4*)(dst + 4) = f32x4{st.o[hb][4][i], st.o[hb][5][i], st.o[hb][6][i], st.o[hb][7][i]};
+        }
+      }
+      __syncthreads();
+      for (int idx = tid; idx < nh * (kD / 4); idx += kThreads) {
+        const int hh = idx / (kD / 4), dd = (idx % (kD / 4)) * 4;
+        const int h = h0 + hh;
+        float M = -FLT_MAX;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, sm_m[w * 32 + h]);
+        float L = 0.f;
+        f32x4 A = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          const float e = __builtin_amdgcn_exp2f(sm_m[w * 32 + h] - M);
+          L += e * sm_l[w * 32 + h];
+          A += e * *(const f32x4*)(sm_o + ((long)w * gh + hh) * kD + dd);
+        }
+        if (DIRECT) {
+          if (out_row >= 0 && out_row < a.out_rows) {
+            const float inv = L > 0.f ? 1.f / L : 0.f;
+            store_out4<Elem>(a.out, ((long)out_row * a.hq + qh0 + h) * kD + dd, A * inv);
+          }
+        } else {
+          // Re-express (L, A) relative to the true max so the partial state is
+          // (m = max score, l = sum exp(s - m), acc = sum exp(s - m) v) as in cuh:620-632.
+          float Mx = -FLT_MAX;
+#pragma unroll
+          for (int w = 0; w < NW; ++w) Mx = fmaxf(Mx, sm_x[w * 32 + h]);
+          const float rescale = __builtin_amdgcn_exp2f(M - Mx);
+          const long s = d.state0 + (long)h * d.stride;
+          put_f32x4(d.acc + s * kD + dd, A * rescale, d.coherent);
+          if (dd == 0) {
+            put_f32(d.m + s, Mx * kLn2, d.coherent);
+            put_f32(d.l + s, L * rescale, d.coherent);
+          }
+        }
+      }
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------------
-// The decode kernel.
+// Small units (at most kSoloTiles tiles) are streamed by one wave alone: its state is
+// final, so it goes straight from registers to its destination without the LDS combine.
+// ---------------------------------------------------------------------------------
+constexpr int kSoloTiles = 2;
+
+template <class Elem, int HB, bool FAST, int MODE>
+__device__ void solo_unit(const DecodeArgs& a, const Unit& u, int t0, int t1, const Dest& d,
+                          int lane, bool have_first, FastPager::Pages f0, FastPager::Pages f1) {
+  const int qh0 = u.kvh * a.group;
+  u32x4 qf[HB][4];
+  load_q<HB>(a, u.row, qh0, lane, qf);
+  WaveState<HB> st;
+  init_state<HB>(st);
+  stream_unit<Elem, HB, FAST>(a, st, qf, u.row, u.kvh, t0, t1, u.len, lane, have_first, f0, f1);
+  const int out_row = MODE == kDirect ? (a.out_indices ? a.out_indices[u.row] : u.row) : 0;
+  write_wave_state<Elem, HB, MODE == kDirect>(a, st, qh0, out_row, d, lane);
+  if (MODE == kQueue && a.merge_counters != nullptr) arrive<Elem>(a, u, qh0, lane, 0, 1);
+}
+
+// ---------------------------------------------------------------------------------
+// The decode kernel: one workgroup per unit.
 // ---------------------------------------------------------------------------------
 // Register budget: G <= 16 (one head block) must fit two waves per SIMD (<= 256 registers
 // each); G <= 32 doubles the accumulators and may use the whole register file.
@@ -806,7 +921,6 @@ void decode_kernel(DecodeArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = uniform(tid >> 6);
-  const int c = lane & 15, g = lane >> 4;
   const int G = a.group;
 
   // Work-queue units: issue this wave's first two block-table reads together with the
@@ -833,17 +947,19 @@ void decode_kernel(DecodeArgs a) {
   long state0, state_stride;
   unit_states<MODE>(a, u, qh0, state0, state_stride);
   const bool fused = MODE == kQueue && a.merge_counters != nullptr;
+  const Dest d{a.part_m, a.part_l, a.part_acc, state0, state_stride, fused};
 
   if (MODE != kDirect && u.tb >= u.te) {
     write_neutral(a, state0, state_stride, G, tid, kThreads, fused);
     return;
   }
 
+  // Small units: wave 0 alone; the other waves return at once and free their slots for
+  // the next workgroup on the CU.  No barrier is reached on this path.
   const int n = u.te - u.tb;
   if (n <= kSoloTiles) {
     if (wave == 0)
-      solo_unit<Elem, HB, FAST, MODE>(a, u, state0, state_stride, lane, u.tb == first_tile, first0,
-                                      first1);
+      solo_unit<Elem, HB, FAST, MODE>(a, u, u.tb, u.te, d, lane, u.tb == first_tile, first0, first1);
     return;
   }
 
@@ -857,84 +973,8 @@ void decode_kernel(DecodeArgs a) {
   const int w1 = uniform(u.tb + (n * (wave + 1)) / kWaves);
   stream_unit<Elem, HB, FAST>(a, st, qf, u.row, u.kvh, w0, w1, u.len, lane, w0 == first_tile,
                               first0, first1);
-
-  // Combine the waves one chunk of heads at a time (16 heads with 4 waves, 8 with 8, so
-  // the O staging stays at 32 KB).  LDS: m[w][32] (reference max), l[w][32],
-  // x[w][32] (true max), o[w][gh][128] with gh = min(G, chunk).
-  constexpr int kChunk = NW == 8 ? 8 : 16;
-  const int gh = G < kChunk ? G : kChunk;
-  float* sm_m = lds;
-  float* sm_l = lds + kWaves * 32;
-  float* sm_x = lds + 2 * kWaves * 32;
-  float* sm_o = lds + 3 * kWaves * 32;
-  if (g == 0) {
-#pragma unroll
-    for (int hb = 0; hb < HB; ++hb) {
-      const int h = hb * 16 + c;
-      if (h < G) {
-        sm_m[wave * 32 + h] = st.m[hb];
-        sm_l[wave * 32 + h] = st.l[hb];
-        sm_x[wave * 32 + h] = st.mx[hb];
-      }
-    }
-  }
-  int out_row = 0;
-  if (MODE == kDirect) out_row = a.out_indices ? a.out_indices[u.row] : u.row;
-#pragma unroll
-  for (int hb = 0; hb < HB; ++hb) {
-#pragma unroll
-    for (int sub = 0; sub < 16 / kChunk; ++sub) {
-      const int h0 = hb * 16 + sub * kChunk;
-      const int nh = G - h0 < kChunk ? G - h0 : kChunk;
-      if (nh <= 0) break;
-      if (hb > 0 || sub > 0) __syncthreads();  // previous chunk's readers are done with sm_o
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int hh = 4 * g + i - sub * kChunk;
-        if (hh >= 0 && hh < nh) {
-          float* dst = sm_o + ((long)wave * gh + hh) * kD + 8 * c;
-          *(f32x4*)dst = f32x4{st.o[hb][0][i], st.o[hb][1][i], st.o[hb][2][i], st.o[hb][3][i]};
-          *(f32x4*)(dst + 4) = f32x4{st.o[hb][4][i], st.o[hb][5][i], st.o[hb][6][i], st.o[hb][7][i]};
-        }
-      }
-      __syncthreads();
-      for (int idx = tid; idx < nh * (kD / 4); idx += kThreads) {
-        const int hh = idx / (kD / 4), d = (idx % (kD / 4)) * 4;
-        const int h = h0 + hh;
-        float M = -FLT_MAX;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w * 32 + h]);
-        float L = 0.f;
-        f32x4 A = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-          const float e = __builtin_amdgcn_exp2f(sm_m[w * 32 + h] - M);
-          L += e * sm_l[w * 32 + h];
-          A += e * *(const f32x4*)(sm_o + ((long)w * gh + hh) * kD + d);
-        }
-        if (MODE == kDirect) {
-          if (out_row >= 0 && out_row < a.out_rows) {
-            const float inv = L > 0.f ? 1.f / L : 0.f;
-            store_out4<Elem>(a.out, ((long)out_row * a.hq + qh0 + h) * kD + d, A * inv);
-          }
-        } else {
-          // Re-express (L, A) relative to the true max so the partial state is
-          // (m = max score, l = sum exp(s - m), acc = sum exp(s - m) v) as in cuh:620-632.
-          float Mx = -FLT_MAX;
-#pragma unroll
-          for (int w = 0; w < kWaves; ++w) Mx = fmaxf(Mx, sm_x[w * 32 + h]);
-          const float rescale = __builtin_amdgcn_exp2f(M - Mx);
-          const long s = state0 + (long)h * state_stride;
-          put_f32x4(a.part_acc + s * kD + d, A * rescale, fused);
-          if (d == 0) {
-            put_f32(a.part_m + s, Mx * kLn2, fused);
-            put_f32(a.part_l + s, L * rescale, fused);
-          }
-        }
-      }
-    }
-  }
-
+  const int out_row = MODE == kDirect ? (a.out_indices ? a.out_indices[u.row] : u.row) : 0;
+  combine_waves<Elem, HB, NW, MODE == kDirect>(a, st, lds, qh0, out_row, d, tid, lane, wave);
   if (fused) arrive<Elem>(a, u, qh0, lane, wave, kWaves);
 }
 
@@ -985,8 +1025,10 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   }
   const int out_row = a.out_indices ? a.out_indices[row] : row;
   if (out_row < 0 || out_row >= a.out_rows) return;
-  merge_head<Elem, QUEUE, false>(a.part_m, a.part_l, a.part_acc, base, stride, count, total, nsplit,
-                                 split0, a.out + ((long)out_row * a.hq + qh) * kD * 2, lane);
+  LseAcc acc;
+  fold_slots<QUEUE, false>(acc, a.part_m, a.part_l, a.part_acc, base, stride, count, total, nsplit,
+                           split0, lane);
+  acc.store<Elem>(a.out + ((long)out_row * a.hq + qh) * kD * 2, lane);
 }
 
 // ---------------------------------------------------------------------------------
@@ -1105,34 +1147,54 @@ int dispatch_merge(const MergeArgs& m, bool queue, int dtype, hipStream_t stream
   return PKV_OK;
 }
 
-// Scratch partial states for the direct op's internal split, one buffer per (device,
-// stream): launches on one stream run in order, so each buffer is only ever used by one
-// op at a time.  Allocated on the first launch on a stream that needs it (never while
-// the stream is being captured into a graph) and kept until the process ends.  Launches
-// that get no buffer (more than kMaxScratchStreams streams, capture before the first
-// launch, allocation failure) run the single-launch direct kernel instead.
-constexpr size_t kScratchBytes = 4u << 20;
+// Per-stream scratch for the partial states of the direct op's internal split: one device
+// buffer per (device, stream).  Launches on one stream run in order, so a buffer is only
+// ever used by one op at a time.  It is allocated, or grown, on a launch that needs it,
+// never while the stream is being captured into a graph, and kept until the process ends.
+// A launch that gets no buffer (more than kMaxScratchStreams streams, capture before the
+// first launch, allocation failure) runs the single-launch direct kernel instead.
+struct StreamScratch {
+  int device;
+  hipStream_t stream;
+  void* ptr;
+  size_t bytes;
+};
+constexpr size_t kMinScratchBytes = 4u << 20;
 constexpr int kMaxScratchStreams = 64;
 
-float* stream_scratch(hipStream_t stream) {
+StreamScratch* stream_scratch(hipStream_t stream, size_t need) {
   static std::mutex mu;
-  static std::vector<std::tuple<int, hipStream_t, float*>> table;
+  static StreamScratch table[kMaxScratchStreams];
+  static int used = 0;
   int device = 0;
   if (hipGetDevice(&device) != hipSuccess) return nullptr;
   std::lock_guard<std::mutex> lock(mu);
-  for (const auto& e : table)
-    if (std::get<0>(e) == device && std::get<1>(e) == stream) return std::get<2>(e);
-  if ((int)table.size() >= kMaxScratchStreams) return nullptr;
+  StreamScratch* e = nullptr;
+  for (int i = 0; i < used; ++i)
+    if (table[i].device == device && table[i].stream == stream) e = &table[i];
+  if (e && e->bytes >= need) return e;
+  if (!e && used >= kMaxScratchStreams) return nullptr;
   hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(stream, &capture) != hipSuccess || capture != hipStreamCaptureStatusNone)
     return nullptr;
-  float* p = nullptr;
-  if (hipMalloc(&p, kScratchBytes) != hipSuccess) {
+  const size_t bytes = need > kMinScratchBytes ? need : kMinScratchBytes;
+  void* p = nullptr;
+  if (hipMalloc(&p, bytes) != hipSuccess) {
     (void)hipGetLastError();
     return nullptr;
   }
-  table.emplace_back(device, stream, p);
-  return p;
+  if (e) {  // grow: the old buffer may still be read by work queued on this stream
+    if (hipStreamSynchronize(stream) != hipSuccess || hipFree(e->ptr) != hipSuccess) {
+      (void)hipFree(p);
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    e->ptr = p;
+    e->bytes = bytes;
+    return e;
+  }
+  table[used] = StreamScratch{device, stream, p, bytes};
+  return &table[used++];
 }
 
 // Internal split count for a direct (num_splits == 1) launch.  One workgroup per
@@ -1150,7 +1212,7 @@ int direct_splits(const Geometry& g, int context) {
   long s = (256 + units - 1) / units;
   if (s > tiles / 4) s = tiles / 4;
   const long per_split = (long)g.batch * g.hq * (kD + 2) * (long)sizeof(float);
-  if (s * per_split > (long)kScratchBytes) s = (long)kScratchBytes / per_split;
+  if (s * per_split > (long)kMinScratchBytes) s = (long)kMinScratchBytes / per_split;
   return s >= 2 ? (int)s : 1;
 }
 
@@ -1202,14 +1264,15 @@ int run_grid(const Geometry& g, const void* q, int q_rows, const void* k, const 
   a.num_splits = num_splits;
   if (num_splits == 1) {
     const int internal = direct_splits(g, context);
-    float* scratch = internal > 1 ? stream_scratch(stream) : nullptr;
+    StreamScratch* scratch =
+        internal > 1 ? stream_scratch(stream, pkv_workspace_bytes(g.batch, g.hq, internal)) : nullptr;
     if (!scratch) {
       st = dispatch_decode<kDirect>(a, g.dtype, g.batch * g.hkv, stream);
       return st == PKV_OK ? ok() : st;
     }
     num_splits = internal;
-    ws = scratch;
-    ws_bytes = kScratchBytes;
+    ws = scratch->ptr;
+    ws_bytes = scratch->bytes;
     a.num_splits = num_splits;
   }
   const size_t need = pkv_workspace_bytes(g.batch, g.hq, num_splits);

@@ -268,11 +268,12 @@ def test_hip_graph_replay(ext, gpu):
     out = torch.zeros(4, 32, 128, dtype=F16, device=gpu)
     ws = torch.empty(meta["total_partial_slots"] * 32 * 130, dtype=torch.float32, device=gpu)
     tail = [meta["bucket_length"], 16, meta["total_partial_slots"], False]
-    ext.paged_attention_workqueue(*args, out, ws, *tail)
-    torch.cuda.synchronize()
-    eager = out.clone()
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):  # eager run on the capture stream (allocates its scratch)
+        ext.paged_attention_workqueue(*args, out, ws, *tail)
+    torch.cuda.synchronize()
+    eager = out.clone()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.stream(s):
         with torch.cuda.graph(graph, stream=s):
