@@ -250,6 +250,12 @@ int pkv_probe_read(const void* src, size_t bytes, int32_t pattern, void* sink, v
 /* Copies `bytes` (a multiple of 16) from src to dst with a plain grid-stride kernel. */
 int pkv_probe_copy(const void* src, void* dst, size_t bytes, void* stream);
 
+/* pkv_probe_read over `workgroups` workgroups of 8 waves, at most one per CU (each holds
+ * 96 KB of LDS): with fewer workgroups than CUs it measures the read bandwidth of that
+ * many CUs (sink holds `workgroups` words).  No counterpart in the reference. */
+int pkv_probe_read_cus(const void* src, size_t bytes, int32_t pattern, int32_t workgroups,
+                       void* sink, void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

@@ -29,12 +29,13 @@ __device__ inline uint32_t lane_offset(int pattern, int lane, int k) {
 }
 
 // One wave reads whole 4 KB chunks (4 loads of 1 KB); 4 chunks in flight per iteration.
-__global__ __launch_bounds__(256) void probe_read_kernel(const uint8_t* src, uint64_t chunks,
+__global__ __launch_bounds__(512) void probe_read_kernel(const uint8_t* src, uint64_t chunks,
                                                          uint64_t stride, int pattern,
                                                          uint32_t* sink) {
   const int lane = threadIdx.x & 63;
-  const uint64_t wave = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const uint64_t nwaves = (uint64_t)gridDim.x * 4;
+  const int waves_per_group = blockDim.x >> 6;
+  const uint64_t wave = (uint64_t)blockIdx.x * waves_per_group + (threadIdx.x >> 6);
+  const uint64_t nwaves = (uint64_t)gridDim.x * waves_per_group;
   u32x4 acc = {0u, 0u, 0u, 0u};
   for (uint64_t base = wave; base < chunks; base += 4 * nwaves) {
     u32x4 v[4][4];
@@ -79,6 +80,21 @@ int pkv_probe_read(const void* src, size_t bytes, int32_t pattern, void* sink, v
   // order idx * stride mod chunks is a permutation.
   const uint64_t stride = chunks > 1 ? 2147483647ull % chunks : 1;
   hipLaunchKernelGGL(probe_read_kernel, dim3(2048), dim3(256), 0, (hipStream_t)stream,
+                     (const uint8_t*)src, chunks, stride ? stride : 1, pattern, (uint32_t*)sink);
+  return hipGetLastError() == hipSuccess ? PKV_OK : PKV_ERR_LAUNCH;
+}
+
+// pkv_probe_read with `workgroups` workgroups of 8 waves, each holding 96 KB of LDS so
+// that no two share a CU: with fewer workgroups than CUs it measures what a given number
+// of CUs can stream (sink must hold `workgroups` words).
+int pkv_probe_read_cus(const void* src, size_t bytes, int32_t pattern, int32_t workgroups,
+                       void* sink, void* stream) {
+  if (!src || !sink || bytes < 4096 || bytes % 4096 || bytes / 4096 >= 2147483647ull ||
+      pattern < 0 || pattern > 2 || workgroups <= 0 || workgroups > 65536)
+    return PKV_ERR_INVALID_ARGUMENT;
+  const uint64_t chunks = bytes / 4096;
+  const uint64_t stride = chunks > 1 ? 2147483647ull % chunks : 1;
+  hipLaunchKernelGGL(probe_read_kernel, dim3(workgroups), dim3(512), 96 * 1024, (hipStream_t)stream,
                      (const uint8_t*)src, chunks, stride ? stride : 1, pattern, (uint32_t*)sink);
   return hipGetLastError() == hipSuccess ? PKV_OK : PKV_ERR_LAUNCH;
 }

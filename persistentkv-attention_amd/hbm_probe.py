@@ -5,6 +5,7 @@ The MI355X counterpart of the reference's micro_benchmarks/01_hbm_bandwidth.cu:2
 
   python hbm_probe.py read            # read bandwidth for the decode kernel's access patterns
   python hbm_probe.py copy --mib 1024 # one known-size copy per launch, for rocprofv3 --pmc
+  python hbm_probe.py cus             # read bandwidth of 8 .. 256 CUs, one workgroup each
 
 ``read`` reports GB/s per pattern (contiguous, K-operand 16 rows x 64 B, V-operand 4 rows
 x 256 B) and size; sizes above the 256 MB Infinity Cache measure HBM.  ``copy`` launches
@@ -63,6 +64,27 @@ def run_read(sizes_mib, iters):
     return rows
 
 
+def run_cus(counts, mib, iters):
+    """Read bandwidth of 1 GiB-class streams with `n` workgroups of 8 waves, at most one
+    per CU: the per-CU ceiling when n is below the CU count."""
+    import torch
+
+    import pkv_native
+
+    lib = pkv_native.lib()
+    dev = torch.device("cuda:0")
+    nbytes = mib << 20
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=dev).random_(0, 256)
+    sink = torch.zeros(65536, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    for n in counts:
+        ms = _time_ms(torch, lambda: _check(lib, lib.pkv_probe_read_cus(
+            buf.data_ptr(), nbytes, 1, n, sink.data_ptr(), stream)), iters)
+        gbps = nbytes / ms / 1e6
+        print(f"cus {n:4d} workgroups x 8 waves (K operand): {gbps:8.0f} GB/s, {gbps / n:6.1f} GB/s "
+              f"per workgroup ({ms * 1e3:8.1f} us)", flush=True)
+
+
 def run_copy(mib, iters):
     import torch
 
@@ -88,12 +110,18 @@ def main(argv=None):
     r = sub.add_parser("read")
     r.add_argument("--mib", type=int, nargs="+", default=[4096, 256, 64])
     r.add_argument("--iters", type=int, default=10)
+    u = sub.add_parser("cus")
+    u.add_argument("--workgroups", type=int, nargs="+", default=[8, 32, 64, 128, 160, 192, 256])
+    u.add_argument("--mib", type=int, default=1024)
+    u.add_argument("--iters", type=int, default=3)
     c = sub.add_parser("copy")
     c.add_argument("--mib", type=int, default=1024)
     c.add_argument("--iters", type=int, default=4)
     a = p.parse_args(argv)
     if a.cmd == "read":
         run_read(a.mib, a.iters)
+    elif a.cmd == "cus":
+        run_cus(a.workgroups, a.mib, a.iters)
     else:
         run_copy(a.mib, a.iters)
 
