@@ -38,11 +38,14 @@ inline int32_t round_up4(int64_t v) { return (int32_t)(floordiv(v + 3, 4) * 4); 
 
 inline int64_t tiles_of(int64_t length) { return floordiv(length + 31, 32); }
 
-// MI355X targets: 256 CUs, two resident 4-wave workgroups per CU, and at least this
-// many 32-token tiles per work item so the per-item Q load, LDS combine and partial
-// write stay small next to the K/V stream.
+// MI355X targets: 256 CUs with one decode workgroup each, about 1.5 work items per CU,
+// and at least this many 32-token tiles per work item so the per-item Q load, LDS
+// combine and partial write stay small next to the K/V stream.  Measured on equal-sized
+// items over the C4 and C5 traces: 384 items was the fastest or tied (C5 G=32: 88.7 us
+// per step against 106 us at 1024 items; C5 G=8 and C4 within 1 % or better), since
+// every item pays a fixed chain of dependent loads and one CU streams at most ~35 GB/s.
 constexpr int kMiComputeUnits = 256;
-constexpr int kMiItemsPerCu = 4;
+constexpr int kMiTargetItems = kMiComputeUnits * 3 / 2;
 constexpr int kMiMinTilesPerItem = 8;
 constexpr int kMiMaxSplits = 128;
 
@@ -82,7 +85,7 @@ int32_t pkv_choose_workqueue_row_splits(int32_t length, int32_t active_count,
   const int64_t active = std::max<int32_t>(1, active_count);
   if (policy == PKV_POLICY_MI355X) {
     // Per-row view of the joint planner: assume the other rows are as long as this one.
-    const int64_t target = (int64_t)kMiComputeUnits * kMiItemsPerCu;
+    const int64_t target = kMiTargetItems;
     const int64_t per_item = std::max<int64_t>(kMiMinTilesPerItem,
                                                ceil_div_pos(tiles * active * hkv, target));
     const int64_t s = ceil_div_pos(tiles, per_item);
@@ -116,7 +119,7 @@ int32_t pkv_choose_splits(const int32_t* lengths, int32_t count, int32_t request
   if (policy == PKV_POLICY_MI355X) {
     // One split count for the whole bucket: enough items for every CU, at least
     // kMiMinTilesPerItem tiles per item on the shortest row.
-    const int64_t target = (int64_t)kMiComputeUnits * kMiItemsPerCu;
+    const int64_t target = kMiTargetItems;
     int64_t s = ceil_div_pos(target, hkv * batch);
     s = std::min<int64_t>(s, std::max<int64_t>(1, t_min / kMiMinTilesPerItem));
     return (int32_t)std::max<int64_t>(1, std::min<int64_t>(s, std::min<int64_t>(kMiMaxSplits, t_min)));
@@ -243,7 +246,7 @@ static void plan_row_splits(const int32_t* lengths, int32_t count, int32_t reque
     int64_t total = 0;
     for (int i = 0; i < count; ++i) total += std::max<int64_t>(1, tiles_of(lengths[i]));
     const int64_t hkv = num_kv_heads > 0 ? num_kv_heads : 1;
-    const int64_t target = (int64_t)kMiComputeUnits * kMiItemsPerCu;
+    const int64_t target = kMiTargetItems;
     const int64_t per_item = std::max<int64_t>(kMiMinTilesPerItem, ceil_div_pos(total * hkv, target));
     for (int i = 0; i < count; ++i) {
       const int64_t tiles = std::max<int64_t>(1, tiles_of(lengths[i]));
