@@ -2,11 +2,16 @@
  * pkv.h — C ABI of the MI355X (gfx950) PersistentKV paged decode-attention engine.
  *
  * Every entry point takes plain device pointers, sizes and a HIP stream passed as
- * `void*` (a hipStream_t; NULL selects the null stream).  Nothing here allocates device
- * memory: outputs, the split workspace and the merge counters are owned by the caller,
- * exactly as in the reference op surface.  Calls enqueue work asynchronously and never
- * synchronise the host.  Errors are reported as a pkv_status code; a one-line message
- * describing the last failure on the calling thread is available from pkv_last_error().
+ * `void*` (a hipStream_t; NULL selects the null stream).  Outputs, the split workspace
+ * and the merge counters are owned by the caller, exactly as in the reference op surface.
+ * One exception to "the library allocates nothing": a direct launch (num_splits == 1) of
+ * fewer than 128 (row, kv head) pairs is split internally, and its partial states go to a
+ * scratch buffer that the library allocates on the first such launch on a stream (4 MiB
+ * or more, never during graph capture, kept until the process ends; PKV_DIRECT_SPLIT=0 in
+ * the environment turns this off).  Calls enqueue work asynchronously and never
+ * synchronise the host (a scratch buffer that must grow waits for its stream once).
+ * Errors are reported as a pkv_status code; a one-line message describing the last
+ * failure on the calling thread is available from pkv_last_error().
  *
  * Layouts (all row-major, contiguous):
  *   q / q_source   [rows, num_q_heads, 128]                   fp16 or bf16
