@@ -35,7 +35,8 @@ for _p in (PKG, ROOT):
 
 METRIC = "decode-step µs + effective KV HBM GB/s (% of peak), B8 bimodal G=4 fp16"
 WORKLOAD_NAMES = {"c1": "c1_b1_ctx2048_direct", "c2": "c2_b8_mha_split8",
-                  "c3": "c3_b1_long_context_split32", "c4": "c4_bimodal_workqueue",
+                  "c3": "c3_b1_long_context_split32", "c3_32k": "c3_b1_32k_context_split32",
+                  "c4": "c4_bimodal_workqueue",
                   "c5_g32": "c5_b64_zipf_mqa_bf16", "c5_g8": "c5_b64_zipf_g8_bf16"}
 HBM_PEAK_GBPS = 8000.0
 MALL_BYTES = 256 * 2 ** 20  # MI355X Infinity Cache
@@ -49,7 +50,7 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--rotations", type=int, default=4,
                    help="minimum KV pool replicas (cold-cache basis; raised for small steps)")
-    p.add_argument("--workload", default="c4", choices=["c1", "c2", "c3", "c4", "c5_g32", "c5_g8"],
+    p.add_argument("--workload", default="c4", choices=sorted(WORKLOAD_NAMES),
                    help="configuration (default c4, the headline; the others are reported "
                         "for DESIGN.md and are not the metric)")
     p.add_argument("--fused-merge", action="store_true", help="single-launch fused merge variant")

@@ -242,13 +242,18 @@ def config_c2(seed=DEFAULT_SEED):
                     [StepState(0, tuple(range(8)), tuple(lengths))], physical, splits=8)
 
 
-def config_c3(seed=DEFAULT_SEED, steps=64):
+def config_c3(seed=DEFAULT_SEED, steps=64, first_bucket=16384):
     """B=1 long-context trace: 16 requests with prompts alternating 16384 / 32768 served one
-    at a time, 64 steps, split 32, each step appending one token's K/V."""
+    at a time, 64 steps, split 32, each step appending one token's K/V.  With
+    ``first_bucket=32768`` the alternation starts at the 32k bucket (the B1 32k-context
+    case; the 16k-first trace spends its 64 steps in the first request)."""
     lengths = make_lengths("bucketed_c3", 16, seed)
+    if first_bucket == 32768:
+        lengths = [(lengths[i ^ 1][0], lengths[i][1]) for i in range(len(lengths))]
     reqs, physical = build_requests(lengths, 1, seed, 0.0)
     st = build_steps_continuous(reqs, 1, steps)
-    return Workload("c3", "paged_attention_indexed", 32, 8, 16, torch.float16, seed, reqs, st,
+    name = "c3" if first_bucket == 16384 else "c3_32k"
+    return Workload(name, "paged_attention_indexed", 32, 8, 16, torch.float16, seed, reqs, st,
                     physical, splits=32, append_kv=True)
 
 
@@ -275,7 +280,8 @@ def config_c5(hkv=1, seed=DEFAULT_SEED, steps=48, batch=64):
                     policy=pkv_native.POLICY_MI355X)
 
 
-CONFIGS = {"c1": config_c1, "c2": config_c2, "c3": config_c3, "c4": config_c4,
+CONFIGS = {"c1": config_c1, "c2": config_c2, "c3": config_c3,
+           "c3_32k": lambda **kw: config_c3(first_bucket=32768, **kw), "c4": config_c4,
            "c5_g32": lambda **kw: config_c5(hkv=1, **kw), "c5_g8": lambda **kw: config_c5(hkv=4, **kw)}
 
 
