@@ -44,6 +44,10 @@ PAGED = [
     (2, 24, 8, 100, 16, 1, BF16, "random"),
     (1, 32, 8, 8192, 16, 1, F16, "canonical"),   # canonical fragmented table
     (1, 32, 8, 8192, 16, 16, F16, "canonical"),
+    (1, 32, 1, 3000, 16, 1, F16, "random"),      # G = 32 direct, split inside
+    (2, 48, 2, 600, 16, 3, BF16, "reversed"),    # G = 24
+    (2, 40, 2, 333, 8, 1, F16, "random"),        # G = 20, page 8 (generic pager)
+    (1, 27, 1, 300, 16, 2, F16, "random"),       # G = 27
 ]
 
 
@@ -131,6 +135,8 @@ QUEUE = [
     ([2000, 4000, 900], 32, 1, 32, 12, False, BF16),       # G = 32 (MQA), page 32
     ([1500, 77], 32, 4, 32, 6, False, BF16),               # G = 8
     ([999, 1001], 20, 4, 8, 5, False, F16),                # G = 5, page 8
+    ([3000, 40, 1200], 48, 2, 16, 7, False, F16),          # G = 24
+    ([700, 2100], 27, 1, 16, 4, False, BF16),              # G = 27
 ]
 
 
