@@ -37,7 +37,12 @@ METRIC = "decode-step µs + effective KV HBM GB/s (% of peak), B8 bimodal G=4 fp
 WORKLOAD_NAMES = {"c1": "c1_b1_ctx2048_direct", "c2": "c2_b8_mha_split8",
                   "c3": "c3_b1_long_context_split32", "c3_32k": "c3_b1_32k_context_split32",
                   "c4": "c4_bimodal_workqueue",
-                  "c5_g32": "c5_b64_zipf_mqa_bf16", "c5_g8": "c5_b64_zipf_g8_bf16"}
+                  "c5_g32": "c5_b64_zipf_mqa_bf16", "c5_g8": "c5_b64_zipf_g8_bf16",
+                  "smoke_g4_8k": "smoke_b1_g4_n8192_contiguous_split16",
+                  "smoke_g4_32k": "smoke_b1_g4_n32768_contiguous_split16"}
+# Published figures of the reference for the same metric and configuration (RTX 3060,
+# 360 GB/s peak): results/smoke_test.txt:25 and :27.
+PUBLISHED_GBPS = {"smoke_g4_8k": 237.1, "smoke_g4_32k": 238.6}
 HBM_PEAK_GBPS = 8000.0
 MALL_BYTES = 256 * 2 ** 20  # MI355X Infinity Cache
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "c4_decode_traffic.json")
@@ -74,8 +79,12 @@ def cpu_baseline(w, q_pool_cpu, k_cpu, v_cpu, metas, budget_s):
     done_bytes, elapsed, steps = 0, 0.0, 0
     for i, meta in enumerate(metas):
         t0 = time.perf_counter()
-        oracle.paged_decode(q_pool_cpu[i], k_cpu, v_cpu, meta.block_table.cpu(), meta.seq_lens.cpu(),
-                            meta.q_indices.cpu(), meta.out_indices.cpu())
+        if w.op == "attention_contiguous":
+            for b in range(len(meta.seq_lens)):
+                oracle.sdpa_row(q_pool_cpu[i][b], k_cpu[b], v_cpu[b])
+        else:
+            oracle.paged_decode(q_pool_cpu[i], k_cpu, v_cpu, meta.block_table.cpu(),
+                                meta.seq_lens.cpu(), meta.q_indices.cpu(), meta.out_indices.cpu())
         elapsed += time.perf_counter() - t0
         done_bytes += meta.kv_bytes
         steps += 1
@@ -210,8 +219,9 @@ def main():
     kernel = {"paged_attention_workqueue": "decode_kernel<*,kQueue> (stage 1 only)",
               "paged_attention_indexed": "decode_kernel<*,kSplit> + merge_kernel (whole op)",
               "paged_attention_masked": "decode_kernel<*,kSplit> + merge_kernel (whole op)",
-              "paged_attention": "decode_kernel<*,kDirect> (whole op)"}[w.op]
-    if w.op == "paged_attention" and w.splits > 1:
+              "paged_attention": "decode_kernel<*,kDirect> (whole op)",
+              "attention_contiguous": "decode_kernel<*,kDirect> (whole op)"}[w.op]
+    if w.op in ("paged_attention", "attention_contiguous") and w.splits > 1:
         kernel = "decode_kernel<*,kSplit> + merge_kernel (whole op)"
     result = {
         "metric": METRIC,
@@ -225,7 +235,8 @@ def main():
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBPS, 2),
         "higher_is_better": True,
         "scaling": "weak",
-        "vs_baseline": None,
+        "vs_baseline": (round(value / PUBLISHED_GBPS[args.workload], 3)
+                        if args.workload in PUBLISHED_GBPS else None),
         "dtype": "fp16" if w.dtype == torch.float16 else "bf16",
         "data": "synthetic",
         "config": {"workload": WORKLOAD_NAMES[args.workload], "requests": len(w.requests),
@@ -244,6 +255,20 @@ def main():
                      "mean_launch_us_event_bracketed": round(sum(dec_ms) / len(dec_ms) * 1e3, 2),
                      "algorithmic_bytes_per_launch": int(sum(dec_bytes) / len(dec_bytes))},
     }
+    if w.op == "attention_contiguous":
+        # The reference's query-head baseline on the same inputs (smoke_test.cu:342-374
+        # reports the grouped op's speedup over it).
+        n_base = max(2, min(args.steps, 16))
+        c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        c0.record()
+        for k in range(n_base):
+            kp, vp = pools[k % len(pools)]
+            ext.attention_query_head_baseline(metas[0].q, kp, vp, metas[0].output)
+        c1.record()
+        torch.cuda.synchronize()
+        base_us = c0.elapsed_time(c1) * 1e3 / n_base
+        result["query_head_baseline"] = {"step_us": round(base_us, 2),
+                                         "speedup": round(base_us / (gpu_ms * 1e3 / args.steps), 2)}
     if not args.no_cpu_baseline:
         q_cpu = q_pool.cpu()
         result["cpu_baseline"] = cpu_baseline(w, q_cpu, k0.cpu(), v0.cpu(), metas, args.cpu_seconds)

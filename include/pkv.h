@@ -157,6 +157,30 @@ int pkv_workqueue_merge(
     int32_t dtype, void* stream);
 
 /* ---------------------------------------------------------------------------------
+ * Contiguous-layout decode: K and V are [batch, num_kv_heads, context, 128] (every row
+ * holds `context` tokens) and q / output are [batch, num_q_heads, 128].
+ * ------------------------------------------------------------------------------- */
+
+/* GQA decode over contiguous K/V, unsplit (num_splits == 1, no workspace) or split
+ * (workspace of pkv_workspace_bytes(batch, num_q_heads, num_splits) bytes).
+ * Replaces persistentkv_dispatch (cuh:1077-1090) and persistentkv_split_dispatch
+ * (cuh:1092-1108) over PkvContiguousAccessor (cuh:128-178). */
+int pkv_attention_contiguous(
+    const void* q, const void* k, const void* v, void* output,
+    void* workspace, size_t workspace_bytes,
+    int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t context,
+    int32_t head_dim, int32_t num_splits, int32_t dtype, void* stream);
+
+/* Query-head baseline: each query head streams its KV head on its own, so every K/V
+ * byte is read G times (the redundant GQA traffic the grouped path removes).  Same
+ * output as pkv_attention_contiguous.  Replaces persistentkv_baseline_dispatch
+ * (cuh:1263-1282) and pkv_query_head_baseline_kernel (cuh:786-889). */
+int pkv_attention_query_head_baseline(
+    const void* q, const void* k, const void* v, void* output,
+    int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t context,
+    int32_t head_dim, int32_t dtype, void* stream);
+
+/* ---------------------------------------------------------------------------------
  * Host scheduling: split policy, cost model and compact work-queue builder.
  * Pure host code (no GPU needed).  "Reference" mode reproduces
  * tests/benchmark_serving_trace.py bit for bit; "mi355x" mode is re-tuned for 256 CUs.

@@ -111,6 +111,9 @@ struct DecodeArgs {
   int32_t max_pages, num_pages;
   int32_t num_splits;         // split mode
   int32_t num_tasks, total_slots;  // queue mode
+  // Contiguous layout only: unit kv head v reads the K/V of head v / kv_div (1, or G for
+  // the query-head baseline, whose units are single query heads).
+  int32_t kv_div;
 };
 
 // ---------------------------------------------------------------------------------
@@ -244,6 +247,50 @@ struct FastPager {
           ? (long)clamp_page(a, p.page[b]) * page_bytes + head_bytes + (long)in_page * (kD * 2) : 0;
       // Descriptors must be wave-uniform (SGPRs); readfirstlane states that to the
       // compiler, which otherwise wraps every buffer load in a waterfall loop.
+      const int nrec = uniform(nvalid * (kD * 2));
+      const __amdgpu_buffer_rsrc_t rk =
+          __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(a.k_pages + off), (short)0, nrec, kRsrcWord3);
+      const __amdgpu_buffer_rsrc_t rv =
+          __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(a.v_pages + off), (short)0, nrec, kRsrcWord3);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) r.k[b][kk] = __builtin_amdgcn_raw_buffer_load_b128(rk, koff[kk], 0, 0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) r.v[b * 4 + j] = __builtin_amdgcn_raw_buffer_load_b128(rv, voff[b * 4 + j], 0, 0);
+    }
+  }
+};
+
+// Contiguous K/V [B, Hkv, N, 128] (cuh:128-178): token t of (row, kv head) at
+// ((row*Hkv + kvh)*N + t)*256 bytes, N = context.  Same per-lane operand layout as the
+// page-16 pager, with no block table to read.
+struct ContigPager {
+  struct Pages {};
+  const DecodeArgs& a;
+  long base;         // byte offset of token 0 of (row, kv head)
+  int lim;
+  uint32_t koff[4];
+  uint32_t voff[8];
+
+  __device__ ContigPager(const DecodeArgs& args, int row, int kvh, int limit, int lane)
+      : a(args), lim(limit) {
+    const int hkv = a.hkv / a.kv_div;
+    base = ((long)row * hkv + kvh / a.kv_div) * a.context * (kD * 2);
+    const int c = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) koff[kk] = c * 256 + kk * 64 + g * 16;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) voff[j] = (4 * g + (j & 3)) * 256 + c * 16;
+  }
+
+  __device__ inline Pages lookup(int) const { return {}; }
+
+  __device__ inline void issue(int tile, const Pages&, TileRegs& r) const {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int tok0 = tile * kTile + b * 16;
+      int nvalid = lim - tok0;
+      nvalid = nvalid < 0 ? 0 : (nvalid > 16 ? 16 : nvalid);
+      const long off = nvalid > 0 ? base + (long)tok0 * (kD * 2) : 0;
       const int nrec = uniform(nvalid * (kD * 2));
       const __amdgpu_buffer_rsrc_t rk =
           __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(a.k_pages + off), (short)0, nrec, kRsrcWord3);
@@ -727,17 +774,24 @@ __device__ inline void init_state(WaveState<HB>& st) {
   }
 }
 
-template <class Elem, int HB, bool FAST>
+// K/V addressing of a launch: paged with 16-token-aligned pages, paged with any page
+// size, or contiguous.
+enum : int { kPgGeneric = 0, kPgFast = 1, kPgContig = 2 };
+
+template <class Elem, int HB, int PG>
 __device__ inline void stream_unit(const DecodeArgs& a, WaveState<HB>& st, const u32x4 (&qf)[HB][4],
                                    int row, int kvh, int t0, int t1, int len, int lane,
                                    bool have_first = false, FastPager::Pages f0 = {},
                                    FastPager::Pages f1 = {}) {
   const long lim_l = (long)t1 * kTile;
   const int lim = uniform(lim_l < len ? (int)lim_l : len);
-  if (FAST) {
+  if constexpr (PG == kPgFast) {
     FastPager pg(a, row, kvh, lim, lane);
     if (have_first) stream_range_from<Elem, HB>(st, pg, qf, t0, t1, lim, lane, f0, f1);
     else stream_range<Elem, HB>(st, pg, qf, t0, t1, lim, lane);
+  } else if constexpr (PG == kPgContig) {
+    ContigPager pg(a, row, kvh, lim, lane);
+    stream_range<Elem, HB>(st, pg, qf, t0, t1, lim, lane);
   } else {
     GenericPager pg(a, row, kvh, lim, lane);
     stream_range<Elem, HB>(st, pg, qf, t0, t1, lim, lane);
@@ -893,7 +947,7 @@ __device__ inline void combine_waves(const DecodeArgs& a, const WaveState<HB>& s
 // ---------------------------------------------------------------------------------
 constexpr int kSoloTiles = 2;
 
-template <class Elem, int HB, bool FAST, int MODE>
+template <class Elem, int HB, int PG, int MODE>
 __device__ void solo_unit(const DecodeArgs& a, const Unit& u, int t0, int t1, const Dest& d,
                           int lane, bool have_first, FastPager::Pages f0, FastPager::Pages f1) {
   const int qh0 = u.kvh * a.group;
@@ -901,7 +955,7 @@ __device__ void solo_unit(const DecodeArgs& a, const Unit& u, int t0, int t1, co
   load_q<HB>(a, u.row, qh0, lane, qf);
   WaveState<HB> st;
   init_state<HB>(st);
-  stream_unit<Elem, HB, FAST>(a, st, qf, u.row, u.kvh, t0, t1, u.len, lane, have_first, f0, f1);
+  stream_unit<Elem, HB, PG>(a, st, qf, u.row, u.kvh, t0, t1, u.len, lane, have_first, f0, f1);
   const int out_row = MODE == kDirect ? (a.out_indices ? a.out_indices[u.row] : u.row) : 0;
   write_wave_state<Elem, HB, MODE == kDirect>(a, st, qh0, out_row, d, lane);
   if (MODE == kQueue && a.merge_counters != nullptr) arrive<Elem>(a, u, qh0, lane, 0, 1);
@@ -912,7 +966,7 @@ __device__ void solo_unit(const DecodeArgs& a, const Unit& u, int t0, int t1, co
 // ---------------------------------------------------------------------------------
 // Register budget: G <= 16 (one head block) must fit two waves per SIMD (<= 256 registers
 // each); G <= 32 doubles the accumulators and may use the whole register file.
-template <class Elem, int HB, bool FAST, int MODE, int NW>
+template <class Elem, int HB, int PG, int MODE, int NW>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(HB == 1 ? 2 : 1)))
 void decode_kernel(DecodeArgs a) {
   constexpr int kWaves = NW;
@@ -928,7 +982,7 @@ void decode_kernel(DecodeArgs a) {
   // work item -> row metadata -> table -> K/V by one memory round trip.
   FastPager::Pages first0 = {}, first1 = {};
   int first_tile = -1;
-  if (MODE == kQueue && FAST) {
+  if (MODE == kQueue && PG == kPgFast) {
     const int32_t* w = a.work_items + (long)blockIdx.x * 5;
     int row = load_scalar(w + 0), kvh = load_scalar(w + 1);
     const int tb = load_scalar(w + 3), te = load_scalar(w + 4);
@@ -959,7 +1013,7 @@ void decode_kernel(DecodeArgs a) {
   const int n = u.te - u.tb;
   if (n <= kSoloTiles) {
     if (wave == 0)
-      solo_unit<Elem, HB, FAST, MODE>(a, u, u.tb, u.te, d, lane, u.tb == first_tile, first0, first1);
+      solo_unit<Elem, HB, PG, MODE>(a, u, u.tb, u.te, d, lane, u.tb == first_tile, first0, first1);
     return;
   }
 
@@ -971,7 +1025,7 @@ void decode_kernel(DecodeArgs a) {
   // Contiguous sub-range of the unit's tiles for this wave.
   const int w0 = uniform(u.tb + (n * wave) / kWaves);
   const int w1 = uniform(u.tb + (n * (wave + 1)) / kWaves);
-  stream_unit<Elem, HB, FAST>(a, st, qf, u.row, u.kvh, w0, w1, u.len, lane, w0 == first_tile,
+  stream_unit<Elem, HB, PG>(a, st, qf, u.row, u.kvh, w0, w1, u.len, lane, w0 == first_tile,
                               first0, first1);
   const int out_row = MODE == kDirect ? (a.out_indices ? a.out_indices[u.row] : u.row) : 0;
   combine_waves<Elem, HB, NW, MODE == kDirect>(a, st, lds, qh0, out_row, d, tid, lane, wave);
@@ -1101,32 +1155,35 @@ int decode_waves(int hb) {
   return 8;
 }
 
-template <class Elem, int HB, bool FAST, int MODE>
+template <class Elem, int HB, int PG, int MODE>
 hipError_t launch_decode(const DecodeArgs& a, int grid, hipStream_t stream) {
   if (HB == 1 && decode_waves(HB) == 8)
-    decode_kernel<Elem, HB, FAST, MODE, (HB == 1 ? 8 : 4)>
+    decode_kernel<Elem, HB, PG, MODE, (HB == 1 ? 8 : 4)>
         <<<dim3(grid), dim3(8 * 64), lds_bytes(a.group, 8), stream>>>(a);
   else
-    decode_kernel<Elem, HB, FAST, MODE, 4><<<dim3(grid), dim3(4 * 64), lds_bytes(a.group, 4), stream>>>(a);
+    decode_kernel<Elem, HB, PG, MODE, 4><<<dim3(grid), dim3(4 * 64), lds_bytes(a.group, 4), stream>>>(a);
   return hipGetLastError();
+}
+
+// Contiguous K/V (no block table) runs only the direct and split modes.
+template <class Elem, int HB, int MODE>
+hipError_t launch_layout(const DecodeArgs& a, int grid, hipStream_t stream) {
+  if constexpr (MODE != kQueue) {
+    if (!a.block_table) return launch_decode<Elem, HB, kPgContig, MODE>(a, grid, stream);
+  }
+  return (a.page_size % 16) == 0 ? launch_decode<Elem, HB, kPgFast, MODE>(a, grid, stream)
+                                 : launch_decode<Elem, HB, kPgGeneric, MODE>(a, grid, stream);
 }
 
 template <int MODE>
 int dispatch_decode(const DecodeArgs& a, int dtype, int grid, hipStream_t stream) {
-  const bool fast = (a.page_size % 16) == 0;
-  const int hb = a.group <= 16 ? 1 : 2;
+  const bool one_block = a.group <= 16;
   hipError_t e;
-  if (dtype == PKV_DTYPE_F16) {
-    if (hb == 1) e = fast ? launch_decode<Half, 1, true, MODE>(a, grid, stream)
-                          : launch_decode<Half, 1, false, MODE>(a, grid, stream);
-    else e = fast ? launch_decode<Half, 2, true, MODE>(a, grid, stream)
-                  : launch_decode<Half, 2, false, MODE>(a, grid, stream);
-  } else {
-    if (hb == 1) e = fast ? launch_decode<BFloat, 1, true, MODE>(a, grid, stream)
-                          : launch_decode<BFloat, 1, false, MODE>(a, grid, stream);
-    else e = fast ? launch_decode<BFloat, 2, true, MODE>(a, grid, stream)
-                  : launch_decode<BFloat, 2, false, MODE>(a, grid, stream);
-  }
+  if (dtype == PKV_DTYPE_F16)
+    e = one_block ? launch_layout<Half, 1, MODE>(a, grid, stream) : launch_layout<Half, 2, MODE>(a, grid, stream);
+  else
+    e = one_block ? launch_layout<BFloat, 1, MODE>(a, grid, stream)
+                  : launch_layout<BFloat, 2, MODE>(a, grid, stream);
   if (e != hipSuccess) return fail(PKV_ERR_LAUNCH, "decode launch failed: %s", hipGetErrorString(e));
   return PKV_OK;
 }
@@ -1234,10 +1291,56 @@ DecodeArgs base_args(const Geometry& g, const void* q, int q_rows, const void* k
   a.page_shift = log2_exact(g.page_size);
   a.max_pages = g.max_pages;
   a.num_pages = g.num_pages;
+  a.kv_div = 1;
   return a;
 }
 
-// Shared body of the three grid ops (cuh:929-974 persistentkv_launch).
+// Launches of the grid ops once arguments are checked: one direct launch, or split decode
+// plus merge (cuh:929-974 persistentkv_launch).  `internal_split` lets a direct launch of
+// few units split itself into the per-stream scratch.
+int launch_grid(const Geometry& g, DecodeArgs a, void* ws, size_t ws_bytes, int num_splits,
+                bool internal_split, hipStream_t stream) {
+  int st;
+  const int units = (int)((long)a.batch * a.hkv);
+  a.num_splits = num_splits;
+  if (num_splits == 1) {
+    const int internal = internal_split ? direct_splits(g, a.context) : 1;
+    StreamScratch* scratch =
+        internal > 1 ? stream_scratch(stream, pkv_workspace_bytes(g.batch, g.hq, internal)) : nullptr;
+    if (!scratch) {
+      st = dispatch_decode<kDirect>(a, g.dtype, units, stream);
+      return st == PKV_OK ? ok() : st;
+    }
+    num_splits = internal;
+    ws = scratch->ptr;
+    ws_bytes = scratch->bytes;
+    a.num_splits = num_splits;
+  }
+  const size_t need = pkv_workspace_bytes(g.batch, g.hq, num_splits);
+  if (!ws || ws_bytes < need)
+    return fail(PKV_ERR_WORKSPACE_TOO_SMALL, "split dispatch requires a workspace of %zu bytes (got %zu)",
+                need, ws ? ws_bytes : (size_t)0);
+  const long states = (long)g.batch * g.hq * num_splits;
+  a.part_m = (float*)ws;
+  a.part_l = a.part_m + states;
+  a.part_acc = a.part_l + states;
+  st = dispatch_decode<kSplit>(a, g.dtype, units * num_splits, stream);
+  if (st != PKV_OK) return st;
+  MergeArgs m = {};
+  m.part_m = a.part_m;
+  m.part_l = a.part_l;
+  m.part_acc = a.part_acc;
+  m.out_indices = a.out_indices;
+  m.out = a.out;
+  m.batch = g.batch;
+  m.hq = g.hq;
+  m.out_rows = a.out_rows;
+  m.num_splits = num_splits;
+  st = dispatch_merge(m, false, g.dtype, stream);
+  return st == PKV_OK ? ok() : st;
+}
+
+// Shared body of the three paged grid ops.
 int run_grid(const Geometry& g, const void* q, int q_rows, const void* k, const void* v,
              const int32_t* table, const int32_t* seq_lens, const int32_t* q_idx,
              const int32_t* out_idx, void* out, int out_rows, void* ws, size_t ws_bytes,
@@ -1255,48 +1358,42 @@ int run_grid(const Geometry& g, const void* q, int q_rows, const void* k, const 
                 g.max_pages, g.page_size, context);
   if (q_rows <= 0 && g.batch > 0) return fail(PKV_ERR_INVALID_ARGUMENT, "q has no rows");
   if (g.batch == 0) return ok();
-  hipStream_t stream = (hipStream_t)stream_ptr;
   DecodeArgs a = base_args(g, q, q_rows, k, v, table, out, out_rows);
   a.seq_lens = seq_lens;
   a.q_indices = q_idx;
   a.out_indices = out_idx;
   a.context = context;
-  a.num_splits = num_splits;
-  if (num_splits == 1) {
-    const int internal = direct_splits(g, context);
-    StreamScratch* scratch =
-        internal > 1 ? stream_scratch(stream, pkv_workspace_bytes(g.batch, g.hq, internal)) : nullptr;
-    if (!scratch) {
-      st = dispatch_decode<kDirect>(a, g.dtype, g.batch * g.hkv, stream);
-      return st == PKV_OK ? ok() : st;
-    }
-    num_splits = internal;
-    ws = scratch->ptr;
-    ws_bytes = scratch->bytes;
-    a.num_splits = num_splits;
-  }
-  const size_t need = pkv_workspace_bytes(g.batch, g.hq, num_splits);
-  if (!ws || ws_bytes < need)
-    return fail(PKV_ERR_WORKSPACE_TOO_SMALL, "split dispatch requires a workspace of %zu bytes (got %zu)",
-                need, ws ? ws_bytes : (size_t)0);
-  const long states = (long)g.batch * g.hq * num_splits;
-  a.part_m = (float*)ws;
-  a.part_l = a.part_m + states;
-  a.part_acc = a.part_l + states;
-  st = dispatch_decode<kSplit>(a, g.dtype, g.batch * g.hkv * num_splits, stream);
+  return launch_grid(g, a, ws, ws_bytes, num_splits, true, (hipStream_t)stream_ptr);
+}
+
+// Contiguous K/V [B, Hkv, N, 128] (cuh:128-178).  `baseline` runs one unit per query
+// head that streams its own KV head, as the reference's query-head baseline does
+// (cuh:786-889): virtual Hkv = Hq with kv_div = G, one launch, no split.
+int run_contiguous(const Geometry& g, const void* q, const void* k, const void* v, void* out,
+                   void* ws, size_t ws_bytes, int context, int num_splits, bool baseline,
+                   void* stream_ptr) {
+  if (context <= 0) return fail(PKV_ERR_INVALID_ARGUMENT, "N must be positive");
+  Geometry checked = g;  // no pages: only the head and pointer checks apply
+  checked.page_size = 16;
+  checked.num_pages = 1;
+  checked.max_pages = 1;
+  int st = check_geometry(checked, q, k, v, (const void*)1, out);
   if (st != PKV_OK) return st;
-  MergeArgs m = {};
-  m.part_m = a.part_m;
-  m.part_l = a.part_l;
-  m.part_acc = a.part_acc;
-  m.out_indices = out_idx;
-  m.out = (uint8_t*)out;
-  m.batch = g.batch;
-  m.hq = g.hq;
-  m.out_rows = out_rows;
-  m.num_splits = num_splits;
-  st = dispatch_merge(m, false, g.dtype, stream);
-  return st == PKV_OK ? ok() : st;
+  if (num_splits <= 0) return fail(PKV_ERR_INVALID_ARGUMENT, "num_splits must be positive");
+  const int total_tiles = (context + kTile - 1) / kTile;
+  if (num_splits > total_tiles)  // cuh:1042-1043
+    return fail(PKV_ERR_INVALID_ARGUMENT, "num_splits=%d exceeds ceil(context/32)=%d", num_splits,
+                total_tiles);
+  if (g.batch == 0) return ok();
+  DecodeArgs a = base_args(g, q, g.batch, k, v, nullptr, out, g.batch);
+  a.context = context;
+  a.page_size = context;
+  if (baseline) {
+    a.kv_div = a.group;
+    a.hkv = g.hq;
+    a.group = 1;
+  }
+  return launch_grid(g, a, ws, ws_bytes, num_splits, !baseline, (hipStream_t)stream_ptr);
 }
 
 struct QueueCall {
@@ -1435,6 +1532,23 @@ int pkv_paged_attention_indexed(const void* q_source, int32_t q_rows, const void
   return run_grid(g, q_source, q_rows, k_pages, v_pages, block_table, seq_lens, q_indices,
                   out_indices, output, out_rows, workspace, workspace_bytes, bucket_context,
                   num_splits, stream);
+}
+
+int pkv_attention_contiguous(const void* q, const void* k, const void* v, void* output,
+                             void* workspace, size_t workspace_bytes, int32_t batch,
+                             int32_t num_q_heads, int32_t num_kv_heads, int32_t context,
+                             int32_t head_dim, int32_t num_splits, int32_t dtype, void* stream) {
+  const Geometry g{batch, num_q_heads, num_kv_heads, head_dim, 1, 16, 1, dtype};
+  return run_contiguous(g, q, k, v, output, workspace, workspace_bytes, context, num_splits, false,
+                        stream);
+}
+
+int pkv_attention_query_head_baseline(const void* q, const void* k, const void* v, void* output,
+                                      int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                                      int32_t context, int32_t head_dim, int32_t dtype,
+                                      void* stream) {
+  const Geometry g{batch, num_q_heads, num_kv_heads, head_dim, 1, 16, 1, dtype};
+  return run_contiguous(g, q, k, v, output, nullptr, 0, context, 1, true, stream);
 }
 
 int pkv_paged_attention_workqueue(

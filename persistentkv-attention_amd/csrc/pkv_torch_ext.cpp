@@ -297,6 +297,56 @@ void persistentkv_workqueue_merge(torch::Tensor seq_lens, torch::Tensor split_of
       i32(total_partial_slots, "total_partial_slots"), pkv_dtype_of(dt), stream_of(output)));
 }
 
+namespace {
+
+struct ContiguousShape {
+  at::ScalarType dt;
+  int32_t B, Hq, Hkv, N;
+};
+
+ContiguousShape check_contiguous(const torch::Tensor& q, const torch::Tensor& k,
+                                 const torch::Tensor& v, const torch::Tensor& output) {
+  const auto dt = activation_dtype(q, "q");
+  check_tensor(q, "q", dt, 3);
+  check_tensor(k, "k", dt, 4);
+  check_tensor(v, "v", dt, 4);
+  check_tensor(output, "output", dt, 3);
+  TORCH_CHECK(q.size(2) == PKV_HEAD_DIM && k.size(3) == PKV_HEAD_DIM,
+              "PersistentKV extension currently requires d=128");
+  TORCH_CHECK(k.size(0) == q.size(0), "k batch mismatch");
+  TORCH_CHECK(v.sizes() == k.sizes(), "v shape mismatch");
+  TORCH_CHECK(output.sizes() == q.sizes(), "output shape must match q");
+  const int32_t Hq = i32(q.size(1), "q.size(1)"), Hkv = i32(k.size(1), "k.size(1)");
+  check_supported_gqa(Hq, Hkv);
+  return {dt, i32(q.size(0), "q.size(0)"), Hq, Hkv, i32(k.size(2), "k.size(2)")};
+}
+
+}  // namespace
+
+// Contiguous-layout decode: q [B, Hq, 128], k / v [B, Hkv, N, 128] (the reference's C++
+// entry points persistentkv_dispatch and persistentkv_split_dispatch, cuh:1077-1108).
+void persistentkv_attention_contiguous(torch::Tensor q, torch::Tensor k, torch::Tensor v,
+                                       torch::Tensor output, torch::Tensor workspace,
+                                       int64_t num_splits) {
+  const ContiguousShape t = check_contiguous(q, k, v, output);
+  check_workspace(workspace);
+  const c10::DeviceGuard guard(q.device());
+  raise_on(pkv_attention_contiguous(q.data_ptr(), k.data_ptr(), v.data_ptr(), output.data_ptr(),
+                                    ws_ptr(workspace), ws_bytes(workspace), t.B, t.Hq, t.Hkv, t.N,
+                                    PKV_HEAD_DIM, i32(num_splits, "num_splits"), pkv_dtype_of(t.dt),
+                                    stream_of(q)));
+}
+
+// Query-head baseline over contiguous K/V (persistentkv_baseline_dispatch, cuh:1263-1282).
+void persistentkv_attention_query_head_baseline(torch::Tensor q, torch::Tensor k, torch::Tensor v,
+                                                torch::Tensor output) {
+  const ContiguousShape t = check_contiguous(q, k, v, output);
+  const c10::DeviceGuard guard(q.device());
+  raise_on(pkv_attention_query_head_baseline(q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                             output.data_ptr(), t.B, t.Hq, t.Hkv, t.N, PKV_HEAD_DIM,
+                                             pkv_dtype_of(t.dt), stream_of(q)));
+}
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("paged_attention", &persistentkv_paged_attention, "PersistentKV native paged attention");
   m.def("paged_attention_masked", &persistentkv_paged_attention_masked,
@@ -309,4 +359,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "Work-queue decode stage only (partial states into the workspace)");
   m.def("workqueue_merge", &persistentkv_workqueue_merge,
         "Work-queue segmented LSE merge stage only");
+  m.def("attention_contiguous", &persistentkv_attention_contiguous,
+        "GQA decode over contiguous K/V [B, Hkv, N, 128]");
+  m.def("attention_query_head_baseline", &persistentkv_attention_query_head_baseline,
+        "Query-head baseline over contiguous K/V (each query head streams its KV head)");
 }

@@ -44,6 +44,9 @@ paged_attention_indexed = _ext.paged_attention_indexed
 paged_attention_workqueue = _ext.paged_attention_workqueue
 workqueue_decode = _ext.workqueue_decode
 workqueue_merge = _ext.workqueue_merge
+# Contiguous K/V [B, Hkv, N, 128] (the reference's C++ entry points, cuh:1077-1108, 1263-1282).
+attention_contiguous = _ext.attention_contiguous
+attention_query_head_baseline = _ext.attention_query_head_baseline
 
 HEAD_DIM = 128
 TILE_TOKENS = 32
@@ -61,6 +64,7 @@ def workqueue_workspace_floats(total_partial_slots: int, num_q_heads: int) -> in
 
 __all__ = [
     "paged_attention", "paged_attention_masked", "paged_attention_indexed",
-    "paged_attention_workqueue", "workqueue_decode", "workqueue_merge", "workspace_floats",
+    "paged_attention_workqueue", "workqueue_decode", "workqueue_merge", "attention_contiguous",
+    "attention_query_head_baseline", "workspace_floats",
     "workqueue_workspace_floats", "EXTENSION_PATH", "LIBRARY_PATH",
 ]

@@ -12,6 +12,9 @@ measured on:
   c4  B=8 bimodal continuous-batching trace, 20 work-queue splits (paged_attention_workqueue)
   c5  B=64 Zipf(1.1) lengths, G=32 or 8, bf16, page 32, cost-model splits (work queue)
 
+and the reference's contiguous-layout performance case (smoke_g4_8k, smoke_g4_32k: B=1,
+G=4, N 8192 / 32768, 16 splits, attention_contiguous; tests/smoke_test.cu:313-395).
+
 Per-step metadata comes from the C++ builder in libpkv.so (pkv_native.build_workqueue);
 random values come from torch generators with the reference's seed offsets (pages +99,
 Q +2026, KV +7) so that every run of a configuration sees identical inputs.
@@ -191,6 +194,7 @@ def zipf_lengths(count, seed, s=1.1, lo=128, hi=65536):
 class Workload:
     name: str
     op: str                 # paged_attention | paged_attention_masked | _indexed | _workqueue
+                            # | attention_contiguous
     hq: int
     hkv: int
     page_size: int
@@ -280,22 +284,35 @@ def config_c5(hkv=1, seed=DEFAULT_SEED, steps=48, batch=64):
                     policy=pkv_native.POLICY_MI355X)
 
 
+def config_smoke(context, seed=DEFAULT_SEED, batch=1, hq=32, hkv=8, splits=16):
+    """The reference's contiguous-layout performance case (tests/smoke_test.cu bench_perf,
+    :313-395): K/V ``[B, Hkv, N, 128]`` fp16, B=1, Hq 32 / Hkv 8, 16 splits, published at
+    N = 8192 and 32768 (results/smoke_test.txt:25, :27).  Each row owns one "page" of N
+    tokens: the slab ``[row]`` of K and V."""
+    reqs = [Request(i, 0, context, 1, (i,)) for i in range(batch)]
+    step = StepState(0, tuple(range(batch)), (context,) * batch)
+    return Workload(f"smoke_g{hq // hkv}_{context // 1024}k", "attention_contiguous", hq, hkv,
+                    context, torch.float16, seed, reqs, [step], batch, splits=splits)
+
+
 CONFIGS = {"c1": config_c1, "c2": config_c2, "c3": config_c3,
            "c3_32k": lambda **kw: config_c3(first_bucket=32768, **kw), "c4": config_c4,
-           "c5_g32": lambda **kw: config_c5(hkv=1, **kw), "c5_g8": lambda **kw: config_c5(hkv=4, **kw)}
+           "c5_g32": lambda **kw: config_c5(hkv=1, **kw), "c5_g8": lambda **kw: config_c5(hkv=4, **kw),
+           "smoke_g4_8k": lambda **kw: config_smoke(8192, **kw),
+           "smoke_g4_32k": lambda **kw: config_smoke(32768, **kw)}
 
 
 # ---------------------------------------------------------------------------------
 # Device state and per-step metadata.
 # ---------------------------------------------------------------------------------
 def make_kv_pool(w: Workload, device, seed_offset=7):
-    """K and V pools ``[pages, Hkv, page_size, 128]`` ~ N(0, 1) (reference :1242-1251)."""
+    """K and V pools ``[pages, Hkv, page_size, 128]`` ~ N(0, 1) (reference :1242-1251).
+    For the contiguous op a page is one row's N tokens, so this is ``[B, Hkv, N, 128]``."""
     gen = torch.Generator(device=device)
     gen.manual_seed(w.seed + seed_offset)
-    k = torch.randn(w.physical_pages, w.hkv, w.page_size, HEAD_DIM, generator=gen, device=device,
-                    dtype=w.dtype)
-    v = torch.randn(w.physical_pages, w.hkv, w.page_size, HEAD_DIM, generator=gen, device=device,
-                    dtype=w.dtype)
+    shape = (w.physical_pages, w.hkv, w.page_size, HEAD_DIM)
+    k = torch.randn(*shape, generator=gen, device=device, dtype=w.dtype)
+    v = torch.randn(*shape, generator=gen, device=device, dtype=w.dtype)
     return k, v
 
 
@@ -368,7 +385,7 @@ def bind_queries(metas, q_pool):
     row order (``paged_attention``, ``paged_attention_masked``), so that a timed step runs
     only the op itself."""
     for i, m in enumerate(metas):
-        if m.op in ("paged_attention", "paged_attention_masked"):
+        if m.op in ("paged_attention", "paged_attention_masked", "attention_contiguous"):
             m.q = q_pool[i].index_select(0, m.q_indices.long()).contiguous()
     return metas
 
@@ -392,6 +409,9 @@ def run_step(ext, w: Workload, meta: StepMeta, step_index: int, q_pool, k_pages,
         ext.paged_attention_masked(q, k_pages, v_pages, meta.block_table, meta.seq_lens,
                                    meta.output, workspace, meta.bucket_length, w.page_size,
                                    meta.splits)
+    elif meta.op == "attention_contiguous":
+        q = meta.q if meta.q is not None else q_source.index_select(0, meta.q_indices.long()).contiguous()
+        ext.attention_contiguous(q, k_pages, v_pages, meta.output, workspace, meta.splits)
     elif meta.op == "paged_attention":
         q = meta.q if meta.q is not None else q_source.index_select(0, meta.q_indices.long()).contiguous()
         ext.paged_attention(q, k_pages, v_pages, meta.block_table, meta.output, workspace,

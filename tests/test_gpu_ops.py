@@ -126,6 +126,35 @@ def _run_queue(ext, gpu, case, meta, hq, hkv, fused, out_rows=None):
     return out, counters
 
 
+# (B, Hq, Hkv, N, splits, dtype): contiguous K/V [B, Hkv, N, 128]
+CONTIGUOUS = [
+    (1, 32, 8, 2048, 1, F16),      # direct; few units, so split inside
+    (2, 32, 8, 1000, 4, F16),
+    (3, 8, 8, 77, 1, BF16),        # G = 1; N not a multiple of 16
+    (1, 32, 1, 3001, 8, BF16),     # G = 32
+    (2, 27, 1, 500, 3, F16),       # G = 27
+    (1, 4, 1, 5, 1, F16),          # N shorter than one 16-token block
+    (16, 32, 8, 600, 1, F16),      # 128 units: one launch, no split
+]
+
+
+@pytest.mark.parametrize("b,hq,hkv,n,splits,dtype", CONTIGUOUS)
+def test_attention_contiguous_and_query_head_baseline(ext, gpu, b, hq, hkv, n, splits, dtype):
+    gen = torch.Generator().manual_seed(n * 3 + splits)
+    q = torch.randn(b, hq, 128, generator=gen).to(dtype)
+    k = torch.randn(b, hkv, n, 128, generator=gen).to(dtype)
+    v = torch.randn(b, hkv, n, 128, generator=gen).to(dtype)
+    ref = torch.stack([oracle.sdpa_row(q[i], k[i], v[i]) for i in range(b)])
+    qd, kd, vd = q.to(gpu), k.to(gpu), v.to(gpu)
+    out = torch.full((b, hq, 128), float("nan"), dtype=dtype, device=gpu)
+    ext.attention_contiguous(qd, kd, vd, out, _ws(b, hq, splits, gpu), splits)
+    base = torch.full_like(out, float("nan"))
+    ext.attention_query_head_baseline(qd, kd, vd, base)
+    torch.cuda.synchronize()
+    assert_parity(out, ref)
+    assert_parity(base, ref)
+
+
 # (lengths, Hq, Hkv, page_size, requested splits, auto, dtype)
 QUEUE = [
     ([300, 17000, 700, 256], 32, 8, 16, 20, False, F16),   # c4-like; empty splits on short rows
@@ -311,3 +340,10 @@ def test_validation_errors(ext, gpu):
         ext.paged_attention(q, k.to(BF16), v.to(BF16), bt, out, empty, 64, 16, 1)
     with pytest.raises(RuntimeError, match="block_table has"):
         ext.paged_attention(q, k, v, bt, out, empty, 4096, 16, 1)
+    kc = torch.zeros(1, 8, 64, 128, dtype=F16, device=gpu)
+    with pytest.raises(RuntimeError, match="num_splits"):
+        ext.attention_contiguous(q, kc, kc, out, _ws(1, 32, 4, gpu), 4)  # 4 > ceil(64/32)
+    with pytest.raises(RuntimeError, match="workspace"):
+        ext.attention_contiguous(q, kc, kc, out, empty, 2)
+    with pytest.raises(RuntimeError, match="v shape mismatch"):
+        ext.attention_query_head_baseline(q, kc, kc[:, :, :32].contiguous(), out)
