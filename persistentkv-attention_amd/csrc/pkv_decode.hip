@@ -466,12 +466,31 @@ __device__ inline void stream_range_from(WaveState<HB>& st, const Pager& pg,
                                          const u32x4 (&qf)[HB][4], int t0, int t1, int lim,
                                          int lane, typename Pager::Pages pa,
                                          typename Pager::Pages pb) {
-  TileRegs r;
-  for (int t = t0; t < t1; ++t) {
-    pg.issue(t, pa, r);
-    pa = pb;
-    pb = pg.lookup(t + 2);
-    compute_tile<Elem, HB>(st, r, qf, t, lim, lane);
+  if constexpr (HB == 1) {
+    TileRegs r;
+    for (int t = t0; t < t1; ++t) {
+      pg.issue(t, pa, r);
+      pa = pb;
+      pb = pg.lookup(t + 2);
+      compute_tile<Elem, HB>(st, r, qf, t, lim, lane);
+    }
+  } else {
+    // Two head blocks run one wave per SIMD, half the waves of a CU at one block: each
+    // wave keeps two tiles in flight, so the CU holds as many bytes in flight as there.
+    // Loads of tile t1 (one past the range) cover no valid rows and read nothing.
+    if (t0 >= t1) return;
+    TileRegs ra, rb;
+    pg.issue(t0, pa, ra);
+    for (int t = t0;; t += 2) {
+      pg.issue(t + 1, pb, rb);
+      pa = pg.lookup(t + 2);
+      compute_tile<Elem, HB>(st, ra, qf, t, lim, lane);
+      if (t + 1 >= t1) break;
+      pg.issue(t + 2, pa, ra);
+      pb = pg.lookup(t + 3);
+      compute_tile<Elem, HB>(st, rb, qf, t + 1, lim, lane);
+      if (t + 2 >= t1) break;
+    }
   }
 }
 
