@@ -960,6 +960,87 @@ __device__ inline void combine_waves(const DecodeArgs& a, const WaveState<HB>& s
   }
 }
 
+// Combines the NW waves' states of one unit without a barrier.  Each wave stores its state
+// in LDS and counts itself in `arrivals`; the last wave to arrive combines all NW states
+// and writes the result, and the others return at once.  Waves of one unit finish up to a
+// tile's memory round trip apart; the early ones free their slots for the CU's next
+// workgroup, which starts its own loads instead of waiting at a barrier.  LDS:
+// m[w][32] (reference max), l[w][32], x[w][32] (true max), o[w][G][128].  `arrivals`
+// is zero when the unit starts.  Returns true in the wave that wrote the result.
+template <class Elem, int HB, int NW, bool DIRECT>
+__device__ inline bool combine_async(const DecodeArgs& a, const WaveState<HB>& st, float* lds,
+                                     int* arrivals, int qh0, int out_row, const Dest& d, int lane,
+                                     int wave) {
+  const int G = a.group, c = lane & 15, g = lane >> 4;
+  float* sm_m = lds;
+  float* sm_l = lds + NW * 32;
+  float* sm_x = lds + 2 * NW * 32;
+  float* sm_o = lds + 3 * NW * 32;
+  if (g == 0) {
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) {
+      const int h = hb * 16 + c;
+      if (h < G) {
+        sm_m[wave * 32 + h] = st.m[hb];
+        sm_l[wave * 32 + h] = st.l[hb];
+        sm_x[wave * 32 + h] = st.mx[hb];
+      }
+    }
+  }
+#pragma unroll
+  for (int hb = 0; hb < HB; ++hb) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int h = hb * 16 + 4 * g + i;
+      if (h < G) {
+        float* dst = sm_o + ((long)wave * G + h) * kD + 8 * c;
+        *(f32x4*)dst = f32x4{st.o[hb][0][i], st.o[hb][1][i], st.o[hb][2][i], st.o[hb][3][i]};
+        *(f32x4*)(dst + 4) = f32x4{st.o[hb][4][i], st.o[hb][5][i], st.o[hb][6][i], st.o[hb][7][i]};
+      }
+    }
+  }
+  // Publish this wave's LDS stores, then count the wave (the fences order the whole
+  // wave's LDS accesses around lane 0's atomic).
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  int before = 0;
+  if (lane == 0) before = __hip_atomic_fetch_add(arrivals, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  if (uniform(before) != NW - 1) return false;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  for (int idx = lane; idx < G * (kD / 4); idx += 64) {
+    const int h = idx / (kD / 4), dd = (idx % (kD / 4)) * 4;
+    float M = -FLT_MAX;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, sm_m[w * 32 + h]);
+    float L = 0.f;
+    f32x4 A = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float e = __builtin_amdgcn_exp2f(sm_m[w * 32 + h] - M);
+      L += e * sm_l[w * 32 + h];
+      A += e * *(const f32x4*)(sm_o + ((long)w * G + h) * kD + dd);
+    }
+    if (DIRECT) {
+      if (out_row >= 0 && out_row < a.out_rows) {
+        const float inv = L > 0.f ? 1.f / L : 0.f;
+        store_out4<Elem>(a.out, ((long)out_row * a.hq + qh0 + h) * kD + dd, A * inv);
+      }
+    } else {
+      // (L, A) re-expressed relative to the true max, as in combine_waves.
+      float Mx = -FLT_MAX;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) Mx = fmaxf(Mx, sm_x[w * 32 + h]);
+      const float rescale = __builtin_amdgcn_exp2f(M - Mx);
+      const long s = d.state0 + (long)h * d.stride;
+      put_f32x4(d.acc + s * kD + dd, A * rescale, d.coherent);
+      if (dd == 0) {
+        put_f32(d.m + s, Mx * kLn2, d.coherent);
+        put_f32(d.l + s, L * rescale, d.coherent);
+      }
+    }
+  }
+  return true;
+}
+
 // ---------------------------------------------------------------------------------
 // Small units (at most kSoloTiles tiles) are streamed by one wave alone: its state is
 // final, so it goes straight from registers to its destination without the LDS combine.
@@ -985,12 +1066,16 @@ __device__ void solo_unit(const DecodeArgs& a, const Unit& u, int t0, int t1, co
 // ---------------------------------------------------------------------------------
 // Register budget: G <= 16 (one head block) must fit two waves per SIMD (<= 256 registers
 // each); G <= 32 doubles the accumulators and may use the whole register file.
-template <class Elem, int HB, int PG, int MODE, int NW>
+//
+// ASYNC selects the barrier-free combine (combine_async) for multi-wave units; it pays
+// when the launch has several units per CU, whose next workgroup then starts early.
+template <class Elem, int HB, int PG, int MODE, int NW, bool ASYNC>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(HB == 1 ? 2 : 1)))
 void decode_kernel(DecodeArgs a) {
   constexpr int kWaves = NW;
   constexpr int kThreads = NW * 64;
   extern __shared__ float lds[];
+  __shared__ int arrivals;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = uniform(tid >> 6);
@@ -1036,6 +1121,10 @@ void decode_kernel(DecodeArgs a) {
     return;
   }
 
+  if constexpr (ASYNC) {
+    if (tid == 0) arrivals = 0;
+    __syncthreads();
+  }
   u32x4 qf[HB][4];
   load_q<HB>(a, u.row, qh0, lane, qf);
   WaveState<HB> st;
@@ -1047,8 +1136,14 @@ void decode_kernel(DecodeArgs a) {
   stream_unit<Elem, HB, PG>(a, st, qf, u.row, u.kvh, w0, w1, u.len, lane, w0 == first_tile,
                               first0, first1);
   const int out_row = MODE == kDirect ? (a.out_indices ? a.out_indices[u.row] : u.row) : 0;
-  combine_waves<Elem, HB, NW, MODE == kDirect>(a, st, lds, qh0, out_row, d, tid, lane, wave);
-  if (fused) arrive<Elem>(a, u, qh0, lane, wave, kWaves);
+  if constexpr (ASYNC) {
+    if (!combine_async<Elem, HB, NW, MODE == kDirect>(a, st, lds, &arrivals, qh0, out_row, d, lane, wave))
+      return;
+    if (fused) arrive<Elem>(a, u, qh0, lane, 0, 1);
+  } else {
+    combine_waves<Elem, HB, NW, MODE == kDirect>(a, st, lds, qh0, out_row, d, tid, lane, wave);
+    if (fused) arrive<Elem>(a, u, qh0, lane, wave, kWaves);
+  }
 }
 
 // ---------------------------------------------------------------------------------
@@ -1129,8 +1224,10 @@ int log2_exact(int x) {
   return s;
 }
 
-size_t lds_bytes(int G, int nw) {
-  const int chunk = nw == 8 ? 8 : 16;
+// LDS of a decode workgroup: the barrier combine stages O in chunks of heads (8 with 8
+// waves, 16 with 4); the barrier-free combine holds every wave's O at once.
+size_t lds_bytes(int G, int nw, bool async = false) {
+  const int chunk = async ? G : (nw == 8 ? 8 : 16);
   return (size_t)(3 * nw * 32 + nw * (G < chunk ? G : chunk) * kD) * sizeof(float);
 }
 
@@ -1174,13 +1271,49 @@ int decode_waves(int hb) {
   return 8;
 }
 
+// Compute units of the current device (cached per device).
+int cu_count() {
+  static int cache[64] = {};
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 256;
+  if (cache[device] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || n <= 0)
+      n = 256;
+    cache[device] = n;
+  }
+  return cache[device];
+}
+
+// The barrier-free combine for launches of at least 3 units per CU (measured: C4 with 4.3
+// units per CU and C2 with 8 gain 2 %; C3 with 1 and C5 G=8 with 2.2 lose 2 %, since
+// one wave combining alone lengthens a unit's critical path).  PKV_ASYNC_COMBINE=0|1
+// forces the choice (tuning).
+bool use_async_combine(int units) {
+  static const int forced = [] {
+    const char* e = getenv("PKV_ASYNC_COMBINE");
+    return e ? (e[0] == '0' ? 0 : 1) : -1;
+  }();
+  if (forced >= 0) return forced == 1;
+  return units >= 3 * cu_count();
+}
+
 template <class Elem, int HB, int PG, int MODE>
 hipError_t launch_decode(const DecodeArgs& a, int grid, hipStream_t stream) {
-  if (HB == 1 && decode_waves(HB) == 8)
-    decode_kernel<Elem, HB, PG, MODE, (HB == 1 ? 8 : 4)>
+  if (HB == 1 && decode_waves(HB) == 8) {
+    if constexpr (HB == 1 && PG == kPgFast && MODE != kDirect) {
+      if (use_async_combine(grid)) {
+        decode_kernel<Elem, HB, PG, MODE, 8, true>
+            <<<dim3(grid), dim3(8 * 64), lds_bytes(a.group, 8, true), stream>>>(a);
+        return hipGetLastError();
+      }
+    }
+    decode_kernel<Elem, HB, PG, MODE, (HB == 1 ? 8 : 4), false>
         <<<dim3(grid), dim3(8 * 64), lds_bytes(a.group, 8), stream>>>(a);
-  else
-    decode_kernel<Elem, HB, PG, MODE, 4><<<dim3(grid), dim3(4 * 64), lds_bytes(a.group, 4), stream>>>(a);
+  } else {
+    decode_kernel<Elem, HB, PG, MODE, 4, false>
+        <<<dim3(grid), dim3(4 * 64), lds_bytes(a.group, 4), stream>>>(a);
+  }
   return hipGetLastError();
 }
 
