@@ -157,6 +157,57 @@ int pkv_workqueue_merge(
     int32_t dtype, void* stream);
 
 /* ---------------------------------------------------------------------------------
+ * fp8 K/V: the same ops over K and V pages of OCP fp8 e4m3 (1 byte per element, same
+ * [num_pages, num_kv_heads, page_size, 128] layout) dequantised with per-tensor scales,
+ * K = k_scale * k8 and V = v_scale * v8.  q / output keep `dtype` (fp16 or bf16).
+ * page_size must be a multiple of 16; k_scale must be positive and finite.  The
+ * reference names fp8 / dequantising paged decode as future work
+ * (paper/persistentkv_mlsys_workshop.tex:688-690); these entries have no counterpart
+ * in its code and follow the signatures of the 2-byte ops they extend.
+ * ------------------------------------------------------------------------------- */
+
+/* pkv_paged_attention_indexed with fp8 K/V. */
+int pkv_paged_attention_indexed_fp8(
+    const void* q_source, int32_t q_rows,
+    const void* k_pages, const void* v_pages,
+    const int32_t* block_table, const int32_t* seq_lens,
+    const int32_t* q_indices, const int32_t* out_indices,
+    void* output, int32_t out_rows,
+    void* workspace, size_t workspace_bytes,
+    int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t num_pages, int32_t page_size, int32_t max_pages,
+    int32_t bucket_context, int32_t num_splits, float k_scale, float v_scale,
+    int32_t dtype, void* stream);
+
+/* pkv_paged_attention_workqueue with fp8 K/V. */
+int pkv_paged_attention_workqueue_fp8(
+    const void* q_source, int32_t q_rows,
+    const void* k_pages, const void* v_pages,
+    const int32_t* block_table, const int32_t* seq_lens,
+    const int32_t* work_items, int32_t num_tasks,
+    const int32_t* split_offsets, int32_t* merge_counters,
+    const int32_t* q_indices, const int32_t* out_indices,
+    void* output, int32_t out_rows,
+    void* workspace, size_t workspace_bytes,
+    int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t num_pages, int32_t page_size, int32_t max_pages,
+    int32_t bucket_context, int32_t total_partial_slots, int32_t fused_merge,
+    float k_scale, float v_scale, int32_t dtype, void* stream);
+
+/* pkv_workqueue_decode with fp8 K/V (stage 1 only; pkv_workqueue_merge is unchanged). */
+int pkv_workqueue_decode_fp8(
+    const void* q_source, int32_t q_rows,
+    const void* k_pages, const void* v_pages,
+    const int32_t* block_table, const int32_t* seq_lens,
+    const int32_t* work_items, int32_t num_tasks,
+    const int32_t* split_offsets, const int32_t* q_indices,
+    void* workspace, size_t workspace_bytes,
+    int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t num_pages, int32_t page_size, int32_t max_pages,
+    int32_t bucket_context, int32_t total_partial_slots, float k_scale, float v_scale,
+    int32_t dtype, void* stream);
+
+/* ---------------------------------------------------------------------------------
  * Contiguous-layout decode: K and V are [batch, num_kv_heads, context, 128] (every row
  * holds `context` tokens) and q / output are [batch, num_q_heads, 128].
  * ------------------------------------------------------------------------------- */

@@ -30,6 +30,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <cmath>
 #include <mutex>
 #include <tuple>
 #include <vector>
@@ -73,6 +74,15 @@ struct Half {
   __device__ static inline float value(uint32_t b) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)b);
   }
+  // 8 fp8 (OCP e4m3) values, byte i of the pair = element i, to 8 fp16 (exact).
+  __device__ static inline u32x4 unpack8(u32x2 x) {
+    u32x4 r;
+    r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)x[0], 1.0f, false));
+    r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)x[0], 1.0f, true));
+    r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)x[1], 1.0f, false));
+    r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)x[1], 1.0f, true));
+    return r;
+  }
 };
 
 struct BFloat {
@@ -86,6 +96,15 @@ struct BFloat {
   }
   __device__ static inline float value(uint32_t b) {
     return (float)__builtin_bit_cast(__bf16, (uint16_t)b);
+  }
+  // 8 fp8 (OCP e4m3) values to 8 bf16 (exact).
+  __device__ static inline u32x4 unpack8(u32x2 x) {
+    u32x4 r;
+    r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)x[0], 1.0f, false));
+    r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)x[0], 1.0f, true));
+    r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)x[1], 1.0f, false));
+    r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)x[1], 1.0f, true));
+    return r;
   }
 };
 
@@ -111,6 +130,11 @@ struct DecodeArgs {
   int32_t max_pages, num_pages;
   int32_t num_splits;         // split mode
   int32_t num_tasks, total_slots;  // queue mode
+  // Scores are q.k * score_scale in log2 units (1/sqrt(128) * log2(e), times the K
+  // dequantisation scale for fp8 K); outputs and partial accumulators are scaled by
+  // v_scale (the V dequantisation scale; 1 otherwise).
+  float score_scale, v_scale;
+  int32_t kv_fp8;             // K/V are fp8 (OCP e4m3) with 1-byte elements
   // Contiguous layout only: unit kv head v reads the K/V of head v / kv_div (1, or G for
   // the query-head baseline, whose units are single query heads).
   int32_t kv_div;
@@ -196,10 +220,22 @@ struct TileRegs {
   u32x4 v[8];     // v[j]: V row of token slot j (v_slot_token), dims 8c .. +8
 };
 
+// fp8 K/V tile as loaded: the same lanes and rows as TileRegs, 8 one-byte elements per
+// 16-byte fp16 chunk.
+struct Fp8Tile {
+  u32x2 k[2][4];
+  u32x2 v[8];
+};
+
+// Each pager's issue() fills a Raw tile; unpack() turns it into the MFMA operand layout
+// (the identity for 2-byte K/V).
 struct FastPager {
   struct Pages {
     int page[2];  // physical page of each 16-token block (unused when the block is empty)
   };
+  using Raw = TileRegs;
+  template <class Elem>
+  __device__ static inline const TileRegs& unpack(const TileRegs& r) { return r; }
   const DecodeArgs& a;
   const int32_t* trow;
   int lim;
@@ -265,6 +301,9 @@ struct FastPager {
 // page-16 pager, with no block table to read.
 struct ContigPager {
   struct Pages {};
+  using Raw = TileRegs;
+  template <class Elem>
+  __device__ static inline const TileRegs& unpack(const TileRegs& r) { return r; }
   const DecodeArgs& a;
   long base;         // byte offset of token 0 of (row, kv head)
   int lim;
@@ -304,11 +343,88 @@ struct ContigPager {
   }
 };
 
+// Page-16 pager over fp8 (OCP e4m3) K/V: FastPager's table reads and per-lane rows with
+// 1-byte elements (a token row is 128 bytes), loaded 8 bytes per chunk and unpacked
+// exactly to fp16 / bf16 just before the tile is computed.
+struct Fp8Pager {
+  using Pages = FastPager::Pages;
+  using Raw = Fp8Tile;
+  const DecodeArgs& a;
+  const int32_t* trow;
+  int lim;
+  long head_bytes;   // kvh * ps * 128
+  long page_bytes;   // Hkv * ps * 128
+  uint32_t koff[4];
+  uint32_t voff[8];
+
+  __device__ Fp8Pager(const DecodeArgs& args, int row, int kvh, int limit, int lane)
+      : a(args), lim(limit) {
+    trow = a.block_table + (long)row * a.max_pages;
+    head_bytes = (long)kvh * a.page_size * kD;
+    page_bytes = (long)a.hkv * a.page_size * kD;
+    const int c = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) koff[kk] = c * 128 + kk * 32 + g * 8;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) voff[j] = (4 * g + (j & 3)) * 128 + c * 8;
+  }
+
+  __device__ inline Pages lookup(int tile) const {
+    Pages p;
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int tok0 = (tile < 0 ? 0 : tile) * kTile + b * 16;
+      int logical, in_page;
+      page_of(a, tok0, logical, in_page);
+      logical = logical < a.max_pages ? logical : a.max_pages - 1;
+      p.page[b] = load_scalar(trow + logical);
+    }
+    return p;
+  }
+
+  __device__ inline void issue(int tile, const Pages& p, Fp8Tile& r) const {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int tok0 = tile * kTile + b * 16;
+      int nvalid = lim - tok0;
+      nvalid = nvalid < 0 ? 0 : (nvalid > 16 ? 16 : nvalid);
+      int logical, in_page;
+      page_of(a, tok0, logical, in_page);
+      const long off = nvalid > 0
+          ? (long)clamp_page(a, p.page[b]) * page_bytes + head_bytes + (long)in_page * kD : 0;
+      const int nrec = uniform(nvalid * kD);
+      const __amdgpu_buffer_rsrc_t rk =
+          __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(a.k_pages + off), (short)0, nrec, kRsrcWord3);
+      const __amdgpu_buffer_rsrc_t rv =
+          __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(a.v_pages + off), (short)0, nrec, kRsrcWord3);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) r.k[b][kk] = __builtin_amdgcn_raw_buffer_load_b64(rk, koff[kk], 0, 0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) r.v[b * 4 + j] = __builtin_amdgcn_raw_buffer_load_b64(rv, voff[b * 4 + j], 0, 0);
+    }
+  }
+
+  template <class Elem>
+  __device__ static inline TileRegs unpack(const Fp8Tile& r) {
+    TileRegs t;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) t.k[b][kk] = Elem::unpack8(r.k[b][kk]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t.v[j] = Elem::unpack8(r.v[j]);
+    return t;
+  }
+};
+
 struct GenericPager {
   struct Pages {
     long k[2];  // byte offset of this lane's K chunk per block, or -1
     long v[8];  // byte offset of this lane's V chunk per slot, or -1
   };
+  using Raw = TileRegs;
+  template <class Elem>
+  __device__ static inline const TileRegs& unpack(const TileRegs& r) { return r; }
   const DecodeArgs& a;
   const int32_t* trow;
   int lim;
@@ -378,7 +494,8 @@ struct WaveState {
 
 template <class Elem, int HB>
 __device__ inline void compute_tile(WaveState<HB>& st, const TileRegs& r,
-                                    const u32x4 (&qf)[HB][4], int tile, int lim, int lane) {
+                                    const u32x4 (&qf)[HB][4], int tile, int lim, int lane,
+                                    float qk) {
   const int g = lane >> 4;
   // V transpose: vt[jj] holds, for dim 8c + jj, the 8 tokens of this lane's slots.
   u32x4 vt[8];
@@ -404,8 +521,8 @@ __device__ inline void compute_tile(WaveState<HB>& st, const TileRegs& r,
     float x[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      x[i] = s0[i] * kScaleLog2;
-      x[4 + i] = s1[i] * kScaleLog2;
+      x[i] = s0[i] * qk;
+      x[4 + i] = s1[i] * qk;
     }
     if (partial) {
 #pragma unroll
@@ -464,31 +581,31 @@ __device__ inline void compute_tile(WaveState<HB>& st, const TileRegs& r,
 template <class Elem, int HB, class Pager>
 __device__ inline void stream_range_from(WaveState<HB>& st, const Pager& pg,
                                          const u32x4 (&qf)[HB][4], int t0, int t1, int lim,
-                                         int lane, typename Pager::Pages pa,
+                                         int lane, float qk, typename Pager::Pages pa,
                                          typename Pager::Pages pb) {
   if constexpr (HB == 1) {
-    TileRegs r;
+    typename Pager::Raw r;
     for (int t = t0; t < t1; ++t) {
       pg.issue(t, pa, r);
       pa = pb;
       pb = pg.lookup(t + 2);
-      compute_tile<Elem, HB>(st, r, qf, t, lim, lane);
+      compute_tile<Elem, HB>(st, Pager::template unpack<Elem>(r), qf, t, lim, lane, qk);
     }
   } else {
     // Two head blocks run one wave per SIMD, half the waves of a CU at one block: each
     // wave keeps two tiles in flight, so the CU holds as many bytes in flight as there.
     // Loads of tile t1 (one past the range) cover no valid rows and read nothing.
     if (t0 >= t1) return;
-    TileRegs ra, rb;
+    typename Pager::Raw ra, rb;
     pg.issue(t0, pa, ra);
     for (int t = t0;; t += 2) {
       pg.issue(t + 1, pb, rb);
       pa = pg.lookup(t + 2);
-      compute_tile<Elem, HB>(st, ra, qf, t, lim, lane);
+      compute_tile<Elem, HB>(st, Pager::template unpack<Elem>(ra), qf, t, lim, lane, qk);
       if (t + 1 >= t1) break;
       pg.issue(t + 2, pa, ra);
       pb = pg.lookup(t + 3);
-      compute_tile<Elem, HB>(st, rb, qf, t + 1, lim, lane);
+      compute_tile<Elem, HB>(st, Pager::template unpack<Elem>(rb), qf, t + 1, lim, lane, qk);
       if (t + 2 >= t1) break;
     }
   }
@@ -496,9 +613,9 @@ __device__ inline void stream_range_from(WaveState<HB>& st, const Pager& pg,
 
 template <class Elem, int HB, class Pager>
 __device__ inline void stream_range(WaveState<HB>& st, const Pager& pg, const u32x4 (&qf)[HB][4],
-                                    int t0, int t1, int lim, int lane) {
+                                    int t0, int t1, int lim, int lane, float qk) {
   if (t0 >= t1) return;
-  stream_range_from<Elem, HB>(st, pg, qf, t0, t1, lim, lane, pg.lookup(t0), pg.lookup(t0 + 1));
+  stream_range_from<Elem, HB>(st, pg, qf, t0, t1, lim, lane, qk, pg.lookup(t0), pg.lookup(t0 + 1));
 }
 
 // ---------------------------------------------------------------------------------
@@ -795,7 +912,7 @@ __device__ inline void init_state(WaveState<HB>& st) {
 
 // K/V addressing of a launch: paged with 16-token-aligned pages, paged with any page
 // size, or contiguous.
-enum : int { kPgGeneric = 0, kPgFast = 1, kPgContig = 2 };
+enum : int { kPgGeneric = 0, kPgFast = 1, kPgContig = 2, kPgFp8 = 3 };
 
 template <class Elem, int HB, int PG>
 __device__ inline void stream_unit(const DecodeArgs& a, WaveState<HB>& st, const u32x4 (&qf)[HB][4],
@@ -804,16 +921,21 @@ __device__ inline void stream_unit(const DecodeArgs& a, WaveState<HB>& st, const
                                    FastPager::Pages f1 = {}) {
   const long lim_l = (long)t1 * kTile;
   const int lim = uniform(lim_l < len ? (int)lim_l : len);
+  const float qk = a.score_scale;
   if constexpr (PG == kPgFast) {
     FastPager pg(a, row, kvh, lim, lane);
-    if (have_first) stream_range_from<Elem, HB>(st, pg, qf, t0, t1, lim, lane, f0, f1);
-    else stream_range<Elem, HB>(st, pg, qf, t0, t1, lim, lane);
+    if (have_first) stream_range_from<Elem, HB>(st, pg, qf, t0, t1, lim, lane, qk, f0, f1);
+    else stream_range<Elem, HB>(st, pg, qf, t0, t1, lim, lane, qk);
+  } else if constexpr (PG == kPgFp8) {
+    Fp8Pager pg(a, row, kvh, lim, lane);
+    if (have_first) stream_range_from<Elem, HB>(st, pg, qf, t0, t1, lim, lane, qk, f0, f1);
+    else stream_range<Elem, HB>(st, pg, qf, t0, t1, lim, lane, qk);
   } else if constexpr (PG == kPgContig) {
     ContigPager pg(a, row, kvh, lim, lane);
-    stream_range<Elem, HB>(st, pg, qf, t0, t1, lim, lane);
+    stream_range<Elem, HB>(st, pg, qf, t0, t1, lim, lane, qk);
   } else {
     GenericPager pg(a, row, kvh, lim, lane);
-    stream_range<Elem, HB>(st, pg, qf, t0, t1, lim, lane);
+    stream_range<Elem, HB>(st, pg, qf, t0, t1, lim, lane, qk);
   }
 #pragma unroll
   for (int hb = 0; hb < HB; ++hb) {
@@ -856,7 +978,7 @@ __device__ inline void write_wave_state(const DecodeArgs& a, const WaveState<HB>
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int h = hb * 16 + 4 * g + i;  // lane 4g + i holds the state of head h
-      const float r = __shfl(DIRECT ? inv_l : rescale, 4 * g + i);
+      const float r = __shfl(DIRECT ? inv_l : rescale, 4 * g + i) * a.v_scale;
       const f32x4 lo = f32x4{st.o[hb][0][i], st.o[hb][1][i], st.o[hb][2][i], st.o[hb][3][i]} * r;
       const f32x4 hi = f32x4{st.o[hb][4][i], st.o[hb][5][i], st.o[hb][6][i], st.o[hb][7][i]} * r;
       if (h >= G) continue;
@@ -939,7 +1061,7 @@ __device__ inline void combine_waves(const DecodeArgs& a, const WaveState<HB>& s
         if (DIRECT) {
           if (out_row >= 0 && out_row < a.out_rows) {
             const float inv = L > 0.f ? 1.f / L : 0.f;
-            store_out4<Elem>(a.out, ((long)out_row * a.hq + qh0 + h) * kD + dd, A * inv);
+            store_out4<Elem>(a.out, ((long)out_row * a.hq + qh0 + h) * kD + dd, A * (inv * a.v_scale));
           }
         } else {
           // Re-express (L, A) relative to the true max so the partial state is
@@ -949,7 +1071,7 @@ __device__ inline void combine_waves(const DecodeArgs& a, const WaveState<HB>& s
           for (int w = 0; w < NW; ++w) Mx = fmaxf(Mx, sm_x[w * 32 + h]);
           const float rescale = __builtin_amdgcn_exp2f(M - Mx);
           const long s = d.state0 + (long)h * d.stride;
-          put_f32x4(d.acc + s * kD + dd, A * rescale, d.coherent);
+          put_f32x4(d.acc + s * kD + dd, A * (rescale * a.v_scale), d.coherent);
           if (dd == 0) {
             put_f32(d.m + s, Mx * kLn2, d.coherent);
             put_f32(d.l + s, L * rescale, d.coherent);
@@ -1022,7 +1144,7 @@ __device__ inline bool combine_async(const DecodeArgs& a, const WaveState<HB>& s
     if (DIRECT) {
       if (out_row >= 0 && out_row < a.out_rows) {
         const float inv = L > 0.f ? 1.f / L : 0.f;
-        store_out4<Elem>(a.out, ((long)out_row * a.hq + qh0 + h) * kD + dd, A * inv);
+        store_out4<Elem>(a.out, ((long)out_row * a.hq + qh0 + h) * kD + dd, A * (inv * a.v_scale));
       }
     } else {
       // (L, A) re-expressed relative to the true max, as in combine_waves.
@@ -1031,7 +1153,7 @@ __device__ inline bool combine_async(const DecodeArgs& a, const WaveState<HB>& s
       for (int w = 0; w < NW; ++w) Mx = fmaxf(Mx, sm_x[w * 32 + h]);
       const float rescale = __builtin_amdgcn_exp2f(M - Mx);
       const long s = d.state0 + (long)h * d.stride;
-      put_f32x4(d.acc + s * kD + dd, A * rescale, d.coherent);
+      put_f32x4(d.acc + s * kD + dd, A * (rescale * a.v_scale), d.coherent);
       if (dd == 0) {
         put_f32(d.m + s, Mx * kLn2, d.coherent);
         put_f32(d.l + s, L * rescale, d.coherent);
@@ -1086,7 +1208,7 @@ void decode_kernel(DecodeArgs a) {
   // work item -> row metadata -> table -> K/V by one memory round trip.
   FastPager::Pages first0 = {}, first1 = {};
   int first_tile = -1;
-  if (MODE == kQueue && PG == kPgFast) {
+  if (MODE == kQueue && (PG == kPgFast || PG == kPgFp8)) {
     const int32_t* w = a.work_items + (long)blockIdx.x * 5;
     int row = load_scalar(w + 0), kvh = load_scalar(w + 1);
     const int tb = load_scalar(w + 3), te = load_scalar(w + 4);
@@ -1301,7 +1423,7 @@ bool use_async_combine(int units) {
 template <class Elem, int HB, int PG, int MODE>
 hipError_t launch_decode(const DecodeArgs& a, int grid, hipStream_t stream) {
   if (HB == 1 && decode_waves(HB) == 8) {
-    if constexpr (HB == 1 && PG == kPgFast && MODE != kDirect) {
+    if constexpr (HB == 1 && (PG == kPgFast || PG == kPgFp8) && MODE != kDirect) {
       if (use_async_combine(grid)) {
         decode_kernel<Elem, HB, PG, MODE, 8, true>
             <<<dim3(grid), dim3(8 * 64), lds_bytes(a.group, 8, true), stream>>>(a);
@@ -1323,6 +1445,7 @@ hipError_t launch_layout(const DecodeArgs& a, int grid, hipStream_t stream) {
   if constexpr (MODE != kQueue) {
     if (!a.block_table) return launch_decode<Elem, HB, kPgContig, MODE>(a, grid, stream);
   }
+  if (a.kv_fp8) return launch_decode<Elem, HB, kPgFp8, MODE>(a, grid, stream);
   return (a.page_size % 16) == 0 ? launch_decode<Elem, HB, kPgFast, MODE>(a, grid, stream)
                                  : launch_decode<Elem, HB, kPgGeneric, MODE>(a, grid, stream);
 }
@@ -1444,6 +1567,8 @@ DecodeArgs base_args(const Geometry& g, const void* q, int q_rows, const void* k
   a.max_pages = g.max_pages;
   a.num_pages = g.num_pages;
   a.kv_div = 1;
+  a.score_scale = kScaleLog2;
+  a.v_scale = 1.0f;
   return a;
 }
 
@@ -1492,12 +1617,37 @@ int launch_grid(const Geometry& g, DecodeArgs a, void* ws, size_t ws_bytes, int 
   return st == PKV_OK ? ok() : st;
 }
 
+// K/V storage of a launch: 2-byte (the activation dtype) or fp8 (OCP e4m3) with per-tensor
+// dequantisation scales, K = k_scale * k8 and V = v_scale * v8.
+struct KvQuant {
+  bool fp8 = false;
+  float k_scale = 1.0f, v_scale = 1.0f;
+};
+
+int check_quant(const Geometry& g, const KvQuant& kq) {
+  if (!kq.fp8) return PKV_OK;
+  if (g.page_size % 16 != 0)
+    return fail(PKV_ERR_UNSUPPORTED, "fp8 K/V requires page_size to be a multiple of 16 (got %d)",
+                g.page_size);
+  if (!(kq.k_scale > 0.f) || !std::isfinite(kq.k_scale) || !std::isfinite(kq.v_scale))
+    return fail(PKV_ERR_INVALID_ARGUMENT, "k_scale must be positive and finite and v_scale finite");
+  return PKV_OK;
+}
+
+void apply_quant(DecodeArgs& a, const KvQuant& kq) {
+  a.kv_fp8 = kq.fp8 ? 1 : 0;
+  a.score_scale = kScaleLog2 * kq.k_scale;
+  a.v_scale = kq.v_scale;
+}
+
 // Shared body of the three paged grid ops.
 int run_grid(const Geometry& g, const void* q, int q_rows, const void* k, const void* v,
              const int32_t* table, const int32_t* seq_lens, const int32_t* q_idx,
              const int32_t* out_idx, void* out, int out_rows, void* ws, size_t ws_bytes,
-             int context, int num_splits, void* stream_ptr) {
+             int context, int num_splits, void* stream_ptr, const KvQuant& kq = KvQuant{}) {
   int st = check_geometry(g, q, k, v, table, out);
+  if (st != PKV_OK) return st;
+  st = check_quant(g, kq);
   if (st != PKV_OK) return st;
   if (context <= 0) return fail(PKV_ERR_INVALID_ARGUMENT, "context must be positive");
   if (num_splits <= 0) return fail(PKV_ERR_INVALID_ARGUMENT, "num_splits must be positive");
@@ -1515,6 +1665,7 @@ int run_grid(const Geometry& g, const void* q, int q_rows, const void* k, const 
   a.q_indices = q_idx;
   a.out_indices = out_idx;
   a.context = context;
+  apply_quant(a, kq);
   return launch_grid(g, a, ws, ws_bytes, num_splits, true, (hipStream_t)stream_ptr);
 }
 
@@ -1612,6 +1763,53 @@ MergeArgs queue_merge_args(const DecodeArgs& a) {
   return m;
 }
 
+int run_indexed(const Geometry& g, const void* q_source, int32_t q_rows, const void* k_pages,
+                const void* v_pages, const int32_t* block_table, const int32_t* seq_lens,
+                const int32_t* q_indices, const int32_t* out_indices, void* output,
+                int32_t out_rows, void* workspace, size_t workspace_bytes, int32_t bucket_context,
+                int32_t num_splits, void* stream, const KvQuant& kq) {
+  if (g.batch > 0 && (!seq_lens || !q_indices || !out_indices))
+    return fail(PKV_ERR_INVALID_ARGUMENT, "seq_lens, q_indices and out_indices must be non-null");
+  if (g.batch > 0 && out_rows <= 0) return fail(PKV_ERR_INVALID_ARGUMENT, "output has no rows");
+  return run_grid(g, q_source, q_rows, k_pages, v_pages, block_table, seq_lens, q_indices,
+                  out_indices, output, out_rows, workspace, workspace_bytes, bucket_context,
+                  num_splits, stream, kq);
+}
+
+// The work-queue op (decode, then the segmented merge unless fused).
+int run_workqueue(const QueueCall& c, int32_t fused_merge, hipStream_t stream, const KvQuant& kq) {
+  int st = check_queue(c, true);
+  if (st != PKV_OK) return st;
+  st = check_quant(c.g, kq);
+  if (st != PKV_OK) return st;
+  if (c.out_rows <= 0) return fail(PKV_ERR_INVALID_ARGUMENT, "output has no rows");
+  if (fused_merge && !c.counters) return fail(PKV_ERR_INVALID_ARGUMENT, "merge_counters is null");
+  if (c.g.batch == 0) return ok();
+  DecodeArgs a = queue_args(c);
+  apply_quant(a, kq);
+  a.merge_counters = fused_merge ? c.counters : nullptr;
+  st = dispatch_decode<kQueue>(a, c.g.dtype, c.num_tasks, stream);
+  if (st != PKV_OK) return st;
+  if (!fused_merge) {
+    st = dispatch_merge(queue_merge_args(a), true, c.g.dtype, stream);
+    if (st != PKV_OK) return st;
+  }
+  return ok();
+}
+
+// Stage 1 of the work-queue op: the decode kernel alone.
+int run_queue_decode(const QueueCall& c, hipStream_t stream, const KvQuant& kq) {
+  int st = check_queue(c, false);
+  if (st != PKV_OK) return st;
+  st = check_quant(c.g, kq);
+  if (st != PKV_OK) return st;
+  if (c.g.batch == 0) return ok();
+  DecodeArgs a = queue_args(c);
+  apply_quant(a, kq);
+  st = dispatch_decode<kQueue>(a, c.g.dtype, c.num_tasks, stream);
+  return st == PKV_OK ? ok() : st;
+}
+
 }  // namespace pkv
 
 using namespace pkv;
@@ -1677,13 +1875,25 @@ int pkv_paged_attention_indexed(const void* q_source, int32_t q_rows, const void
                                 int32_t num_pages, int32_t page_size, int32_t max_pages,
                                 int32_t bucket_context, int32_t num_splits, int32_t dtype,
                                 void* stream) {
-  if (batch > 0 && (!seq_lens || !q_indices || !out_indices))
-    return fail(PKV_ERR_INVALID_ARGUMENT, "seq_lens, q_indices and out_indices must be non-null");
-  if (batch > 0 && out_rows <= 0) return fail(PKV_ERR_INVALID_ARGUMENT, "output has no rows");
   const Geometry g{batch, num_q_heads, num_kv_heads, head_dim, num_pages, page_size, max_pages, dtype};
-  return run_grid(g, q_source, q_rows, k_pages, v_pages, block_table, seq_lens, q_indices,
-                  out_indices, output, out_rows, workspace, workspace_bytes, bucket_context,
-                  num_splits, stream);
+  return run_indexed(g, q_source, q_rows, k_pages, v_pages, block_table, seq_lens, q_indices,
+                     out_indices, output, out_rows, workspace, workspace_bytes, bucket_context,
+                     num_splits, stream, KvQuant{});
+}
+
+int pkv_paged_attention_indexed_fp8(const void* q_source, int32_t q_rows, const void* k_pages,
+                                    const void* v_pages, const int32_t* block_table,
+                                    const int32_t* seq_lens, const int32_t* q_indices,
+                                    const int32_t* out_indices, void* output, int32_t out_rows,
+                                    void* workspace, size_t workspace_bytes, int32_t batch,
+                                    int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                    int32_t num_pages, int32_t page_size, int32_t max_pages,
+                                    int32_t bucket_context, int32_t num_splits, float k_scale,
+                                    float v_scale, int32_t dtype, void* stream) {
+  const Geometry g{batch, num_q_heads, num_kv_heads, head_dim, num_pages, page_size, max_pages, dtype};
+  return run_indexed(g, q_source, q_rows, k_pages, v_pages, block_table, seq_lens, q_indices,
+                     out_indices, output, out_rows, workspace, workspace_bytes, bucket_context,
+                     num_splits, stream, KvQuant{true, k_scale, v_scale});
 }
 
 int pkv_attention_contiguous(const void* q, const void* k, const void* v, void* output,
@@ -1712,25 +1922,27 @@ int pkv_paged_attention_workqueue(
     int32_t num_kv_heads, int32_t head_dim, int32_t num_pages, int32_t page_size,
     int32_t max_pages, int32_t bucket_context, int32_t total_partial_slots,
     int32_t fused_merge, int32_t dtype, void* stream) {
-  QueueCall c{{batch, num_q_heads, num_kv_heads, head_dim, num_pages, page_size, max_pages, dtype},
-              q_source, k_pages, v_pages, q_rows, block_table, seq_lens, work_items, split_offsets,
-              q_indices, out_indices, merge_counters, output, out_rows, workspace, workspace_bytes,
-              bucket_context, num_tasks, total_partial_slots};
-  int st = check_queue(c, true);
-  if (st != PKV_OK) return st;
-  if (out_rows <= 0) return fail(PKV_ERR_INVALID_ARGUMENT, "output has no rows");
-  if (fused_merge && !merge_counters) return fail(PKV_ERR_INVALID_ARGUMENT, "merge_counters is null");
-  if (batch == 0) return ok();
-  DecodeArgs a = queue_args(c);
-  a.merge_counters = fused_merge ? merge_counters : nullptr;
-  hipStream_t hs = (hipStream_t)stream;
-  st = dispatch_decode<kQueue>(a, dtype, num_tasks, hs);
-  if (st != PKV_OK) return st;
-  if (!fused_merge) {
-    st = dispatch_merge(queue_merge_args(a), true, dtype, hs);
-    if (st != PKV_OK) return st;
-  }
-  return ok();
+  const QueueCall c{{batch, num_q_heads, num_kv_heads, head_dim, num_pages, page_size, max_pages, dtype},
+                    q_source, k_pages, v_pages, q_rows, block_table, seq_lens, work_items,
+                    split_offsets, q_indices, out_indices, merge_counters, output, out_rows,
+                    workspace, workspace_bytes, bucket_context, num_tasks, total_partial_slots};
+  return run_workqueue(c, fused_merge, (hipStream_t)stream, KvQuant{});
+}
+
+int pkv_paged_attention_workqueue_fp8(
+    const void* q_source, int32_t q_rows, const void* k_pages, const void* v_pages,
+    const int32_t* block_table, const int32_t* seq_lens, const int32_t* work_items,
+    int32_t num_tasks, const int32_t* split_offsets, int32_t* merge_counters,
+    const int32_t* q_indices, const int32_t* out_indices, void* output, int32_t out_rows,
+    void* workspace, size_t workspace_bytes, int32_t batch, int32_t num_q_heads,
+    int32_t num_kv_heads, int32_t head_dim, int32_t num_pages, int32_t page_size,
+    int32_t max_pages, int32_t bucket_context, int32_t total_partial_slots,
+    int32_t fused_merge, float k_scale, float v_scale, int32_t dtype, void* stream) {
+  const QueueCall c{{batch, num_q_heads, num_kv_heads, head_dim, num_pages, page_size, max_pages, dtype},
+                    q_source, k_pages, v_pages, q_rows, block_table, seq_lens, work_items,
+                    split_offsets, q_indices, out_indices, merge_counters, output, out_rows,
+                    workspace, workspace_bytes, bucket_context, num_tasks, total_partial_slots};
+  return run_workqueue(c, fused_merge, (hipStream_t)stream, KvQuant{true, k_scale, v_scale});
 }
 
 int pkv_workqueue_decode(const void* q_source, int32_t q_rows, const void* k_pages,
@@ -1741,15 +1953,27 @@ int pkv_workqueue_decode(const void* q_source, int32_t q_rows, const void* k_pag
                          int32_t num_kv_heads, int32_t head_dim, int32_t num_pages,
                          int32_t page_size, int32_t max_pages, int32_t bucket_context,
                          int32_t total_partial_slots, int32_t dtype, void* stream) {
-  QueueCall c{{batch, num_q_heads, num_kv_heads, head_dim, num_pages, page_size, max_pages, dtype},
-              q_source, k_pages, v_pages, q_rows, block_table, seq_lens, work_items, split_offsets,
-              q_indices, nullptr, nullptr, nullptr, 0, workspace, workspace_bytes,
-              bucket_context, num_tasks, total_partial_slots};
-  int st = check_queue(c, false);
-  if (st != PKV_OK) return st;
-  if (batch == 0) return ok();
-  st = dispatch_decode<kQueue>(queue_args(c), dtype, num_tasks, (hipStream_t)stream);
-  return st == PKV_OK ? ok() : st;
+  const QueueCall c{{batch, num_q_heads, num_kv_heads, head_dim, num_pages, page_size, max_pages, dtype},
+                    q_source, k_pages, v_pages, q_rows, block_table, seq_lens, work_items,
+                    split_offsets, q_indices, nullptr, nullptr, nullptr, 0, workspace,
+                    workspace_bytes, bucket_context, num_tasks, total_partial_slots};
+  return run_queue_decode(c, (hipStream_t)stream, KvQuant{});
+}
+
+int pkv_workqueue_decode_fp8(const void* q_source, int32_t q_rows, const void* k_pages,
+                             const void* v_pages, const int32_t* block_table,
+                             const int32_t* seq_lens, const int32_t* work_items, int32_t num_tasks,
+                             const int32_t* split_offsets, const int32_t* q_indices,
+                             void* workspace, size_t workspace_bytes, int32_t batch,
+                             int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                             int32_t num_pages, int32_t page_size, int32_t max_pages,
+                             int32_t bucket_context, int32_t total_partial_slots, float k_scale,
+                             float v_scale, int32_t dtype, void* stream) {
+  const QueueCall c{{batch, num_q_heads, num_kv_heads, head_dim, num_pages, page_size, max_pages, dtype},
+                    q_source, k_pages, v_pages, q_rows, block_table, seq_lens, work_items,
+                    split_offsets, q_indices, nullptr, nullptr, nullptr, 0, workspace,
+                    workspace_bytes, bucket_context, num_tasks, total_partial_slots};
+  return run_queue_decode(c, (hipStream_t)stream, KvQuant{true, k_scale, v_scale});
 }
 
 int pkv_workqueue_merge(const int32_t* seq_lens, const int32_t* split_offsets,

@@ -136,17 +136,20 @@ void persistentkv_paged_attention_masked(torch::Tensor q, torch::Tensor k_pages,
       i32(num_splits, "num_splits"), pkv_dtype_of(dt), stream_of(q)));
 }
 
-// tests/persistentkv_torch_extension.cu:159-228
-void persistentkv_paged_attention_indexed(torch::Tensor q_source, torch::Tensor k_pages,
-                                          torch::Tensor v_pages, torch::Tensor block_table,
-                                          torch::Tensor seq_lens, torch::Tensor q_indices,
-                                          torch::Tensor out_indices, torch::Tensor output,
-                                          torch::Tensor workspace, int64_t bucket_context,
-                                          int64_t page_size, int64_t num_splits) {
+namespace {
+
+// Shared body of the indexed op and its fp8-K/V variant (kv_fp8: K/V are float8_e4m3fn
+// pages dequantised by k_scale / v_scale).
+void indexed_op(torch::Tensor q_source, torch::Tensor k_pages, torch::Tensor v_pages,
+                torch::Tensor block_table, torch::Tensor seq_lens, torch::Tensor q_indices,
+                torch::Tensor out_indices, torch::Tensor output, torch::Tensor workspace,
+                int64_t bucket_context, int64_t page_size, int64_t num_splits, bool kv_fp8,
+                double k_scale, double v_scale) {
   const auto dt = activation_dtype(q_source, "q_source");
+  const auto kv_dt = kv_fp8 ? at::kFloat8_e4m3fn : dt;
   check_tensor(q_source, "q_source", dt, 3);
-  check_tensor(k_pages, "k_pages", dt, 4);
-  check_tensor(v_pages, "v_pages", dt, 4);
+  check_tensor(k_pages, "k_pages", kv_dt, 4);
+  check_tensor(v_pages, "v_pages", kv_dt, 4);
   check_tensor(block_table, "block_table", at::kInt, 2);
   check_tensor(seq_lens, "seq_lens", at::kInt, 1);
   check_tensor(q_indices, "q_indices", at::kInt, 1);
@@ -167,14 +170,50 @@ void persistentkv_paged_attention_indexed(torch::Tensor q_source, torch::Tensor 
   TORCH_CHECK(page_size > 0, "page_size must be positive");
   TORCH_CHECK(num_splits > 0, "num_splits must be positive");
   const c10::DeviceGuard guard(q_source.device());
-  raise_on(pkv_paged_attention_indexed(
-      q_source.data_ptr(), i32(q_source.size(0), "q_source.size(0)"), k_pages.data_ptr(),
-      v_pages.data_ptr(), block_table.data_ptr<int>(), seq_lens.data_ptr<int>(),
-      q_indices.data_ptr<int>(), out_indices.data_ptr<int>(), output.data_ptr(),
-      i32(output.size(0), "output.size(0)"), ws_ptr(workspace), ws_bytes(workspace), B, Hq, Hkv, d,
-      i32(k_pages.size(0), "k_pages.size(0)"), i32(page_size, "page_size"),
-      i32(block_table.size(1), "block_table.size(1)"), i32(bucket_context, "bucket_context"),
-      i32(num_splits, "num_splits"), pkv_dtype_of(dt), stream_of(q_source)));
+  const int32_t nq = i32(q_source.size(0), "q_source.size(0)");
+  const int32_t no = i32(output.size(0), "output.size(0)");
+  const int32_t np = i32(k_pages.size(0), "k_pages.size(0)");
+  const int32_t mp = i32(block_table.size(1), "block_table.size(1)");
+  if (kv_fp8)
+    raise_on(pkv_paged_attention_indexed_fp8(
+        q_source.data_ptr(), nq, k_pages.data_ptr(), v_pages.data_ptr(), block_table.data_ptr<int>(),
+        seq_lens.data_ptr<int>(), q_indices.data_ptr<int>(), out_indices.data_ptr<int>(),
+        output.data_ptr(), no, ws_ptr(workspace), ws_bytes(workspace), B, Hq, Hkv, d, np,
+        i32(page_size, "page_size"), mp, i32(bucket_context, "bucket_context"),
+        i32(num_splits, "num_splits"), (float)k_scale, (float)v_scale, pkv_dtype_of(dt),
+        stream_of(q_source)));
+  else
+    raise_on(pkv_paged_attention_indexed(
+        q_source.data_ptr(), nq, k_pages.data_ptr(), v_pages.data_ptr(), block_table.data_ptr<int>(),
+        seq_lens.data_ptr<int>(), q_indices.data_ptr<int>(), out_indices.data_ptr<int>(),
+        output.data_ptr(), no, ws_ptr(workspace), ws_bytes(workspace), B, Hq, Hkv, d, np,
+        i32(page_size, "page_size"), mp, i32(bucket_context, "bucket_context"),
+        i32(num_splits, "num_splits"), pkv_dtype_of(dt), stream_of(q_source)));
+}
+
+}  // namespace
+
+// tests/persistentkv_torch_extension.cu:159-228
+void persistentkv_paged_attention_indexed(torch::Tensor q_source, torch::Tensor k_pages,
+                                          torch::Tensor v_pages, torch::Tensor block_table,
+                                          torch::Tensor seq_lens, torch::Tensor q_indices,
+                                          torch::Tensor out_indices, torch::Tensor output,
+                                          torch::Tensor workspace, int64_t bucket_context,
+                                          int64_t page_size, int64_t num_splits) {
+  indexed_op(q_source, k_pages, v_pages, block_table, seq_lens, q_indices, out_indices, output,
+             workspace, bucket_context, page_size, num_splits, false, 1.0, 1.0);
+}
+
+// The indexed op over fp8 (float8_e4m3fn) K/V pages: K = k_scale * k8, V = v_scale * v8.
+void persistentkv_paged_attention_indexed_fp8(torch::Tensor q_source, torch::Tensor k_pages,
+                                              torch::Tensor v_pages, torch::Tensor block_table,
+                                              torch::Tensor seq_lens, torch::Tensor q_indices,
+                                              torch::Tensor out_indices, torch::Tensor output,
+                                              torch::Tensor workspace, int64_t bucket_context,
+                                              int64_t page_size, int64_t num_splits,
+                                              double k_scale, double v_scale) {
+  indexed_op(q_source, k_pages, v_pages, block_table, seq_lens, q_indices, out_indices, output,
+             workspace, bucket_context, page_size, num_splits, true, k_scale, v_scale);
 }
 
 namespace {
@@ -189,12 +228,14 @@ QueueTensors check_queue_tensors(const torch::Tensor& q_source, const torch::Ten
                                  const torch::Tensor& seq_lens, const torch::Tensor& work_items,
                                  const torch::Tensor& split_offsets, const torch::Tensor& q_indices,
                                  const torch::Tensor& workspace, int64_t bucket_context,
-                                 int64_t page_size, int64_t total_partial_slots) {
+                                 int64_t page_size, int64_t total_partial_slots,
+                                 bool kv_fp8 = false) {
   QueueTensors t;
   t.dt = activation_dtype(q_source, "q_source");
+  const auto kv_dt = kv_fp8 ? at::kFloat8_e4m3fn : t.dt;
   check_tensor(q_source, "q_source", t.dt, 3);
-  check_tensor(k_pages, "k_pages", t.dt, 4);
-  check_tensor(v_pages, "v_pages", t.dt, 4);
+  check_tensor(k_pages, "k_pages", kv_dt, 4);
+  check_tensor(v_pages, "v_pages", kv_dt, 4);
   check_tensor(block_table, "block_table", at::kInt, 2);
   check_tensor(seq_lens, "seq_lens", at::kInt, 1);
   check_tensor(work_items, "work_items", at::kInt, 2);
@@ -221,16 +262,20 @@ QueueTensors check_queue_tensors(const torch::Tensor& q_source, const torch::Ten
 
 }  // namespace
 
-// tests/persistentkv_torch_extension.cu:230-317
-void persistentkv_paged_attention_workqueue(
-    torch::Tensor q_source, torch::Tensor k_pages, torch::Tensor v_pages, torch::Tensor block_table,
-    torch::Tensor seq_lens, torch::Tensor work_items, torch::Tensor split_offsets,
-    torch::Tensor merge_counters, torch::Tensor q_indices, torch::Tensor out_indices,
-    torch::Tensor output, torch::Tensor workspace, int64_t bucket_context, int64_t page_size,
-    int64_t total_partial_slots, bool fused_merge) {
+namespace {
+
+// Shared body of the work-queue op and its fp8-K/V variant.
+void workqueue_op(torch::Tensor q_source, torch::Tensor k_pages, torch::Tensor v_pages,
+                  torch::Tensor block_table, torch::Tensor seq_lens, torch::Tensor work_items,
+                  torch::Tensor split_offsets, torch::Tensor merge_counters,
+                  torch::Tensor q_indices, torch::Tensor out_indices, torch::Tensor output,
+                  torch::Tensor workspace, int64_t bucket_context, int64_t page_size,
+                  int64_t total_partial_slots, bool fused_merge, bool kv_fp8, double k_scale,
+                  double v_scale) {
   const QueueTensors t = check_queue_tensors(q_source, k_pages, v_pages, block_table, seq_lens,
                                              work_items, split_offsets, q_indices, workspace,
-                                             bucket_context, page_size, total_partial_slots);
+                                             bucket_context, page_size, total_partial_slots,
+                                             kv_fp8);
   check_tensor(merge_counters, "merge_counters", at::kInt, 2);
   check_tensor(out_indices, "out_indices", at::kInt, 1);
   check_tensor(output, "output", t.dt, 3);
@@ -240,18 +285,92 @@ void persistentkv_paged_attention_workqueue(
               "output shape must match q head dimensions");
   TORCH_CHECK(out_indices.size(0) == t.B, "out_indices batch mismatch");
   const c10::DeviceGuard guard(q_source.device());
-  raise_on(pkv_paged_attention_workqueue(
-      q_source.data_ptr(), i32(q_source.size(0), "q_source.size(0)"), k_pages.data_ptr(),
-      v_pages.data_ptr(), block_table.data_ptr<int>(), seq_lens.data_ptr<int>(),
-      work_items.data_ptr<int>(), i32(work_items.size(0), "work_items.size(0)"),
-      split_offsets.data_ptr<int>(), fused_merge ? merge_counters.data_ptr<int>() : nullptr,
-      q_indices.data_ptr<int>(), out_indices.data_ptr<int>(), output.data_ptr(),
-      i32(output.size(0), "output.size(0)"), ws_ptr(workspace), ws_bytes(workspace), t.B, t.Hq,
-      t.Hkv, t.d, i32(k_pages.size(0), "k_pages.size(0)"), i32(page_size, "page_size"),
-      i32(block_table.size(1), "block_table.size(1)"), i32(bucket_context, "bucket_context"),
-      i32(total_partial_slots, "total_partial_slots"), fused_merge ? 1 : 0, pkv_dtype_of(t.dt),
-      stream_of(q_source)));
+  const int32_t nq = i32(q_source.size(0), "q_source.size(0)");
+  const int32_t nt = i32(work_items.size(0), "work_items.size(0)");
+  const int32_t no = i32(output.size(0), "output.size(0)");
+  const int32_t np = i32(k_pages.size(0), "k_pages.size(0)");
+  const int32_t mp = i32(block_table.size(1), "block_table.size(1)");
+  int32_t* counters = fused_merge ? merge_counters.data_ptr<int>() : nullptr;
+  if (kv_fp8)
+    raise_on(pkv_paged_attention_workqueue_fp8(
+        q_source.data_ptr(), nq, k_pages.data_ptr(), v_pages.data_ptr(), block_table.data_ptr<int>(),
+        seq_lens.data_ptr<int>(), work_items.data_ptr<int>(), nt, split_offsets.data_ptr<int>(),
+        counters, q_indices.data_ptr<int>(), out_indices.data_ptr<int>(), output.data_ptr(), no,
+        ws_ptr(workspace), ws_bytes(workspace), t.B, t.Hq, t.Hkv, t.d, np,
+        i32(page_size, "page_size"), mp, i32(bucket_context, "bucket_context"),
+        i32(total_partial_slots, "total_partial_slots"), fused_merge ? 1 : 0, (float)k_scale,
+        (float)v_scale, pkv_dtype_of(t.dt), stream_of(q_source)));
+  else
+    raise_on(pkv_paged_attention_workqueue(
+        q_source.data_ptr(), nq, k_pages.data_ptr(), v_pages.data_ptr(), block_table.data_ptr<int>(),
+        seq_lens.data_ptr<int>(), work_items.data_ptr<int>(), nt, split_offsets.data_ptr<int>(),
+        counters, q_indices.data_ptr<int>(), out_indices.data_ptr<int>(), output.data_ptr(), no,
+        ws_ptr(workspace), ws_bytes(workspace), t.B, t.Hq, t.Hkv, t.d, np,
+        i32(page_size, "page_size"), mp, i32(bucket_context, "bucket_context"),
+        i32(total_partial_slots, "total_partial_slots"), fused_merge ? 1 : 0, pkv_dtype_of(t.dt),
+        stream_of(q_source)));
 }
+
+}  // namespace
+
+// tests/persistentkv_torch_extension.cu:230-317
+void persistentkv_paged_attention_workqueue(
+    torch::Tensor q_source, torch::Tensor k_pages, torch::Tensor v_pages, torch::Tensor block_table,
+    torch::Tensor seq_lens, torch::Tensor work_items, torch::Tensor split_offsets,
+    torch::Tensor merge_counters, torch::Tensor q_indices, torch::Tensor out_indices,
+    torch::Tensor output, torch::Tensor workspace, int64_t bucket_context, int64_t page_size,
+    int64_t total_partial_slots, bool fused_merge) {
+  workqueue_op(q_source, k_pages, v_pages, block_table, seq_lens, work_items, split_offsets,
+               merge_counters, q_indices, out_indices, output, workspace, bucket_context,
+               page_size, total_partial_slots, fused_merge, false, 1.0, 1.0);
+}
+
+// The work-queue op over fp8 (float8_e4m3fn) K/V pages: K = k_scale * k8, V = v_scale * v8.
+void persistentkv_paged_attention_workqueue_fp8(
+    torch::Tensor q_source, torch::Tensor k_pages, torch::Tensor v_pages, torch::Tensor block_table,
+    torch::Tensor seq_lens, torch::Tensor work_items, torch::Tensor split_offsets,
+    torch::Tensor merge_counters, torch::Tensor q_indices, torch::Tensor out_indices,
+    torch::Tensor output, torch::Tensor workspace, int64_t bucket_context, int64_t page_size,
+    int64_t total_partial_slots, bool fused_merge, double k_scale, double v_scale) {
+  workqueue_op(q_source, k_pages, v_pages, block_table, seq_lens, work_items, split_offsets,
+               merge_counters, q_indices, out_indices, output, workspace, bucket_context,
+               page_size, total_partial_slots, fused_merge, true, k_scale, v_scale);
+}
+
+namespace {
+
+void queue_decode_op(torch::Tensor q_source, torch::Tensor k_pages, torch::Tensor v_pages,
+                     torch::Tensor block_table, torch::Tensor seq_lens, torch::Tensor work_items,
+                     torch::Tensor split_offsets, torch::Tensor q_indices, torch::Tensor workspace,
+                     int64_t bucket_context, int64_t page_size, int64_t total_partial_slots,
+                     bool kv_fp8, double k_scale, double v_scale) {
+  const QueueTensors t = check_queue_tensors(q_source, k_pages, v_pages, block_table, seq_lens,
+                                             work_items, split_offsets, q_indices, workspace,
+                                             bucket_context, page_size, total_partial_slots,
+                                             kv_fp8);
+  const c10::DeviceGuard guard(q_source.device());
+  const int32_t nq = i32(q_source.size(0), "q_source.size(0)");
+  const int32_t nt = i32(work_items.size(0), "work_items.size(0)");
+  const int32_t np = i32(k_pages.size(0), "k_pages.size(0)");
+  const int32_t mp = i32(block_table.size(1), "block_table.size(1)");
+  if (kv_fp8)
+    raise_on(pkv_workqueue_decode_fp8(
+        q_source.data_ptr(), nq, k_pages.data_ptr(), v_pages.data_ptr(), block_table.data_ptr<int>(),
+        seq_lens.data_ptr<int>(), work_items.data_ptr<int>(), nt, split_offsets.data_ptr<int>(),
+        q_indices.data_ptr<int>(), ws_ptr(workspace), ws_bytes(workspace), t.B, t.Hq, t.Hkv, t.d,
+        np, i32(page_size, "page_size"), mp, i32(bucket_context, "bucket_context"),
+        i32(total_partial_slots, "total_partial_slots"), (float)k_scale, (float)v_scale,
+        pkv_dtype_of(t.dt), stream_of(q_source)));
+  else
+    raise_on(pkv_workqueue_decode(
+        q_source.data_ptr(), nq, k_pages.data_ptr(), v_pages.data_ptr(), block_table.data_ptr<int>(),
+        seq_lens.data_ptr<int>(), work_items.data_ptr<int>(), nt, split_offsets.data_ptr<int>(),
+        q_indices.data_ptr<int>(), ws_ptr(workspace), ws_bytes(workspace), t.B, t.Hq, t.Hkv, t.d,
+        np, i32(page_size, "page_size"), mp, i32(bucket_context, "bucket_context"),
+        i32(total_partial_slots, "total_partial_slots"), pkv_dtype_of(t.dt), stream_of(q_source)));
+}
+
+}  // namespace
 
 // Stage 1 of the work-queue op: the decode kernel alone, writing partial states.
 void persistentkv_workqueue_decode(torch::Tensor q_source, torch::Tensor k_pages,
@@ -260,19 +379,22 @@ void persistentkv_workqueue_decode(torch::Tensor q_source, torch::Tensor k_pages
                                    torch::Tensor split_offsets, torch::Tensor q_indices,
                                    torch::Tensor workspace, int64_t bucket_context,
                                    int64_t page_size, int64_t total_partial_slots) {
-  const QueueTensors t = check_queue_tensors(q_source, k_pages, v_pages, block_table, seq_lens,
-                                             work_items, split_offsets, q_indices, workspace,
-                                             bucket_context, page_size, total_partial_slots);
-  const c10::DeviceGuard guard(q_source.device());
-  raise_on(pkv_workqueue_decode(
-      q_source.data_ptr(), i32(q_source.size(0), "q_source.size(0)"), k_pages.data_ptr(),
-      v_pages.data_ptr(), block_table.data_ptr<int>(), seq_lens.data_ptr<int>(),
-      work_items.data_ptr<int>(), i32(work_items.size(0), "work_items.size(0)"),
-      split_offsets.data_ptr<int>(), q_indices.data_ptr<int>(), ws_ptr(workspace),
-      ws_bytes(workspace), t.B, t.Hq, t.Hkv, t.d, i32(k_pages.size(0), "k_pages.size(0)"),
-      i32(page_size, "page_size"), i32(block_table.size(1), "block_table.size(1)"),
-      i32(bucket_context, "bucket_context"), i32(total_partial_slots, "total_partial_slots"),
-      pkv_dtype_of(t.dt), stream_of(q_source)));
+  queue_decode_op(q_source, k_pages, v_pages, block_table, seq_lens, work_items, split_offsets,
+                  q_indices, workspace, bucket_context, page_size, total_partial_slots, false,
+                  1.0, 1.0);
+}
+
+// Stage 1 over fp8 K/V.
+void persistentkv_workqueue_decode_fp8(torch::Tensor q_source, torch::Tensor k_pages,
+                                       torch::Tensor v_pages, torch::Tensor block_table,
+                                       torch::Tensor seq_lens, torch::Tensor work_items,
+                                       torch::Tensor split_offsets, torch::Tensor q_indices,
+                                       torch::Tensor workspace, int64_t bucket_context,
+                                       int64_t page_size, int64_t total_partial_slots,
+                                       double k_scale, double v_scale) {
+  queue_decode_op(q_source, k_pages, v_pages, block_table, seq_lens, work_items, split_offsets,
+                  q_indices, workspace, bucket_context, page_size, total_partial_slots, true,
+                  k_scale, v_scale);
 }
 
 // Stage 2 of the work-queue op: the segmented LSE merge alone.
@@ -359,6 +481,12 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "Work-queue decode stage only (partial states into the workspace)");
   m.def("workqueue_merge", &persistentkv_workqueue_merge,
         "Work-queue segmented LSE merge stage only");
+  m.def("paged_attention_indexed_fp8", &persistentkv_paged_attention_indexed_fp8,
+        "paged_attention_indexed over fp8 (e4m3) K/V pages with per-tensor scales");
+  m.def("paged_attention_workqueue_fp8", &persistentkv_paged_attention_workqueue_fp8,
+        "paged_attention_workqueue over fp8 (e4m3) K/V pages with per-tensor scales");
+  m.def("workqueue_decode_fp8", &persistentkv_workqueue_decode_fp8,
+        "Work-queue decode stage over fp8 (e4m3) K/V pages");
   m.def("attention_contiguous", &persistentkv_attention_contiguous,
         "GQA decode over contiguous K/V [B, Hkv, N, 128]");
   m.def("attention_query_head_baseline", &persistentkv_attention_query_head_baseline,

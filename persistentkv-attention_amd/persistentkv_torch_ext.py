@@ -44,6 +44,10 @@ paged_attention_indexed = _ext.paged_attention_indexed
 paged_attention_workqueue = _ext.paged_attention_workqueue
 workqueue_decode = _ext.workqueue_decode
 workqueue_merge = _ext.workqueue_merge
+# fp8 (float8_e4m3fn) K/V pages with per-tensor scales: K = k_scale * k8, V = v_scale * v8.
+paged_attention_indexed_fp8 = _ext.paged_attention_indexed_fp8
+paged_attention_workqueue_fp8 = _ext.paged_attention_workqueue_fp8
+workqueue_decode_fp8 = _ext.workqueue_decode_fp8
 # Contiguous K/V [B, Hkv, N, 128] (the reference's C++ entry points, cuh:1077-1108, 1263-1282).
 attention_contiguous = _ext.attention_contiguous
 attention_query_head_baseline = _ext.attention_query_head_baseline
@@ -64,7 +68,9 @@ def workqueue_workspace_floats(total_partial_slots: int, num_q_heads: int) -> in
 
 __all__ = [
     "paged_attention", "paged_attention_masked", "paged_attention_indexed",
-    "paged_attention_workqueue", "workqueue_decode", "workqueue_merge", "attention_contiguous",
+    "paged_attention_workqueue", "workqueue_decode", "workqueue_merge",
+    "paged_attention_indexed_fp8", "paged_attention_workqueue_fp8", "workqueue_decode_fp8",
+    "attention_contiguous",
     "attention_query_head_baseline", "workspace_floats",
     "workqueue_workspace_floats", "EXTENSION_PATH", "LIBRARY_PATH",
 ]
