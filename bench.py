@@ -59,6 +59,9 @@ def parse_args():
                    help="configuration (default c4, the headline; the others are reported "
                         "for DESIGN.md and are not the metric)")
     p.add_argument("--fused-merge", action="store_true", help="single-launch fused merge variant")
+    p.add_argument("--kv-fp8", action="store_true",
+                   help="K/V pages in fp8 (OCP e4m3) with per-tensor scales (work-queue and "
+                        "indexed workloads); bytes and GB/s count the 1-byte elements")
     p.add_argument("--graph", action="store_true",
                    help="capture the timed steps into one HIP graph and replay it (as the "
                         "reference harness replays captured steps, benchmark_serving_trace.py:1439-1452)")
@@ -111,6 +114,11 @@ def main():
     dev = torch.device("cuda:0")
     w = wl.CONFIGS[args.workload](seed=args.seed)
     w.fused_merge = args.fused_merge
+    w.kv_fp8 = args.kv_fp8
+    if w.kv_fp8 and w.op not in ("paged_attention_workqueue", "paged_attention_indexed"):
+        print(f"--kv-fp8 applies to the work-queue and indexed workloads, not {w.op}",
+              file=sys.stderr)
+        sys.exit(2)
     metas = [wl.compile_step(w, i, dev) for i in range(len(w.steps))]
     ws = wl.workspace_for(w, metas, dev)
     q_pool = wl.make_q_pool(w, dev)
@@ -169,6 +177,16 @@ def main():
     gpu_ms = start.elapsed_time(stop)
     total_bytes = sum(metas[k % n_trace].kv_bytes for k in range(args.steps))
 
+    def decode_stage(i, m, kp, vp):
+        if w.kv_fp8:
+            ext.workqueue_decode_fp8(q_pool[i], kp, vp, m.block_table, m.seq_lens, m.work_items,
+                                     m.split_offsets, m.q_indices, ws, m.bucket_length,
+                                     w.page_size, m.total_partial_slots, w.k_scale, w.v_scale)
+        else:
+            ext.workqueue_decode(q_pool[i], kp, vp, m.block_table, m.seq_lens, m.work_items,
+                                 m.split_offsets, m.q_indices, ws, m.bucket_length, w.page_size,
+                                 m.total_partial_slots)
+
     # Decode kernel alone (stage 1 of the work-queue op), one event pair per launch on its
     # stream.  The grid ops have no separate stage entry point: their whole op is timed.
     dec_ms, dec_bytes = [], []
@@ -181,9 +199,7 @@ def main():
         kp, vp = pools[k % len(pools)]
         evs[k][0].record()
         if queue:
-            ext.workqueue_decode(q_pool[i], kp, vp, m.block_table, m.seq_lens, m.work_items,
-                                 m.split_offsets, m.q_indices, ws, m.bucket_length, w.page_size,
-                                 m.total_partial_slots)
+            decode_stage(i, m, kp, vp)
         else:
             step(k)
         evs[k][1].record()
@@ -198,9 +214,7 @@ def main():
         m = metas[i]
         kp, vp = pools[k % len(pools)]
         if queue:
-            ext.workqueue_decode(q_pool[i], kp, vp, m.block_table, m.seq_lens, m.work_items,
-                                 m.split_offsets, m.q_indices, ws, m.bucket_length, w.page_size,
-                                 m.total_partial_slots)
+            decode_stage(i, m, kp, vp)
         else:
             step(k)
     b1.record()
@@ -237,9 +251,10 @@ def main():
         "scaling": "weak",
         "vs_baseline": (round(value / PUBLISHED_GBPS[args.workload], 3)
                         if args.workload in PUBLISHED_GBPS else None),
-        "dtype": "fp16" if w.dtype == torch.float16 else "bf16",
+        "dtype": ("fp16" if w.dtype == torch.float16 else "bf16") + (" (fp8 e4m3 K/V)" if w.kv_fp8 else ""),
         "data": "synthetic",
-        "config": {"workload": WORKLOAD_NAMES[args.workload], "requests": len(w.requests),
+        "config": {"workload": WORKLOAD_NAMES[args.workload] + ("_fp8kv" if w.kv_fp8 else ""),
+                   "requests": len(w.requests),
                    "max_active": max(len(s.active_ids) for s in w.steps),
                    "trace_steps": n_trace, "hq": w.hq, "hkv": w.hkv, "head_dim": 128,
                    "page_size": w.page_size,
@@ -250,7 +265,8 @@ def main():
                    "cache_basis": f"HBM-cold ({len(pools)} rotated KV pool replicas)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": traffic if args.workload == "c4" else None, "kernel": kernel,
+                     "traffic": traffic if args.workload == "c4" and not w.kv_fp8 else None,
+                     "kernel": kernel,
                      "mean_launch_us": round(batched_us, 2),
                      "mean_launch_us_event_bracketed": round(sum(dec_ms) / len(dec_ms) * 1e3, 2),
                      "algorithmic_bytes_per_launch": int(sum(dec_bytes) / len(dec_bytes))},
@@ -271,7 +287,8 @@ def main():
                                          "speedup": round(base_us / (gpu_ms * 1e3 / args.steps), 2)}
     if not args.no_cpu_baseline:
         q_cpu = q_pool.cpu()
-        result["cpu_baseline"] = cpu_baseline(w, q_cpu, k0.cpu(), v0.cpu(), metas, args.cpu_seconds)
+        k_cpu, v_cpu = wl.dequantised(w, k0.cpu(), v0.cpu())
+        result["cpu_baseline"] = cpu_baseline(w, q_cpu, k_cpu, v_cpu, metas, args.cpu_seconds)
     print(json.dumps(result), flush=True)
 
 

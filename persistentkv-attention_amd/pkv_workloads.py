@@ -208,6 +208,10 @@ class Workload:
     policy: int = pkv_native.POLICY_REFERENCE
     append_kv: bool = False
     fused_merge: bool = False
+    # fp8 (OCP e4m3) K/V pages with per-tensor scales (indexed and work-queue ops only).
+    kv_fp8: bool = False
+    k_scale: float = 1.0 / 64.0
+    v_scale: float = 1.0 / 64.0
     extra: dict = field(default_factory=dict)
 
     @property
@@ -218,7 +222,7 @@ class Workload:
         """Algorithmic K+V bytes of one decode step:
         sum(lengths) * Hkv * 128 * 2 (K and V) * element bytes (the reference's
         useful_kv_mb_for_state, benchmark_serving_trace.py:511-513, in bytes)."""
-        elem = 2
+        elem = 1 if self.kv_fp8 else 2
         return sum(self.steps[step_index].lengths) * self.hkv * HEAD_DIM * 2 * elem
 
 
@@ -313,7 +317,18 @@ def make_kv_pool(w: Workload, device, seed_offset=7):
     shape = (w.physical_pages, w.hkv, w.page_size, HEAD_DIM)
     k = torch.randn(*shape, generator=gen, device=device, dtype=w.dtype)
     v = torch.randn(*shape, generator=gen, device=device, dtype=w.dtype)
+    if w.kv_fp8:  # N(0, 1) values quantised with the workload's per-tensor scales
+        k = (k.float() / w.k_scale).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+        v = (v.float() / w.v_scale).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
     return k, v
+
+
+def dequantised(w: Workload, k, v):
+    """The K and V values the engine attends to: ``(k8 * k_scale, v8 * v_scale)`` in fp32
+    for fp8 pools, the pools themselves otherwise."""
+    if not w.kv_fp8:
+        return k, v
+    return k.float() * w.k_scale, v.float() * w.v_scale
 
 
 def make_q_pool(w: Workload, device):
@@ -394,12 +409,26 @@ def run_step(ext, w: Workload, meta: StepMeta, step_index: int, q_pool, k_pages,
              workspace):
     """One decode step through the op the workload names; returns ``meta.output``."""
     q_source = q_pool[step_index]
-    if meta.op == "paged_attention_workqueue":
+    if w.kv_fp8 and meta.op not in ("paged_attention_workqueue", "paged_attention_indexed"):
+        raise ValueError(f"fp8 K/V is provided for the work-queue and indexed ops, not {meta.op}")
+    if meta.op == "paged_attention_workqueue" and w.kv_fp8:
+        ext.paged_attention_workqueue_fp8(q_source, k_pages, v_pages, meta.block_table,
+                                          meta.seq_lens, meta.work_items, meta.split_offsets,
+                                          meta.merge_counters, meta.q_indices, meta.out_indices,
+                                          meta.output, workspace, meta.bucket_length, w.page_size,
+                                          meta.total_partial_slots, w.fused_merge, w.k_scale,
+                                          w.v_scale)
+    elif meta.op == "paged_attention_workqueue":
         ext.paged_attention_workqueue(q_source, k_pages, v_pages, meta.block_table, meta.seq_lens,
                                       meta.work_items, meta.split_offsets, meta.merge_counters,
                                       meta.q_indices, meta.out_indices, meta.output, workspace,
                                       meta.bucket_length, w.page_size, meta.total_partial_slots,
                                       w.fused_merge)
+    elif meta.op == "paged_attention_indexed" and w.kv_fp8:
+        ext.paged_attention_indexed_fp8(q_source, k_pages, v_pages, meta.block_table,
+                                        meta.seq_lens, meta.q_indices, meta.out_indices,
+                                        meta.output, workspace, meta.bucket_length, w.page_size,
+                                        meta.splits, w.k_scale, w.v_scale)
     elif meta.op == "paged_attention_indexed":
         ext.paged_attention_indexed(q_source, k_pages, v_pages, meta.block_table, meta.seq_lens,
                                     meta.q_indices, meta.out_indices, meta.output, workspace,
@@ -432,5 +461,8 @@ def append_step_kv(w: Workload, step_index: int, k_pages, v_pages, seed_offset=1
         page = by_id[rid].physical_pages[pos // w.page_size]
         k_new = torch.randn(w.hkv, HEAD_DIM, generator=gen).to(w.dtype)
         v_new = torch.randn(w.hkv, HEAD_DIM, generator=gen).to(w.dtype)
+        if w.kv_fp8:
+            k_new = (k_new.float() / w.k_scale).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+            v_new = (v_new.float() / w.v_scale).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
         k_pages[page, :, pos % w.page_size] = k_new.to(k_pages.device)
         v_pages[page, :, pos % w.page_size] = v_new.to(v_pages.device)
