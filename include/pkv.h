@@ -15,7 +15,8 @@
  *
  * Layouts (all row-major, contiguous):
  *   q / q_source   [rows, num_q_heads, 128]                   fp16 or bf16
- *   k_pages/v_pages[num_pages, num_kv_heads, page_size, 128]  same dtype as q
+ *   k_pages/v_pages[num_pages, num_kv_heads, page_size, 128]  same dtype as q (fp8 e4m3
+ *                                                             for the *_fp8 entries)
  *   block_table    [batch, max_pages]                         int32 physical page ids
  *   seq_lens       [batch]                                    int32 tokens per row
  *   output         [out_rows, num_q_heads, 128]               same dtype as q

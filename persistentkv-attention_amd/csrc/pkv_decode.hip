@@ -3,15 +3,16 @@
 // One workgroup (8 wave64s when G <= 16, 4 when G > 16) owns one unit of work: a
 // (row, kv head) pair and a range of 32-token tiles.  The unit is a whole row (direct
 // op), one sequence split of a row (grid-split ops) or one compact work item (work-queue
-// op).  The waves stream
-// disjoint sub-ranges of the unit's tiles, so one K/V fetch from HBM serves all G query
-// heads of the KV group, then combine their online-softmax states through LDS.
+// op).  The waves stream disjoint sub-ranges of the unit's tiles, so one K/V fetch from
+// HBM serves all G query heads of the KV group, then combine their online-softmax states
+// through LDS.  K/V come from paged pools (fp16 / bf16, or fp8 e4m3 unpacked exactly in
+// registers) or from the contiguous [B, Hkv, N, 128] layout.
 //
 // Per wave and 32-token tile:
 //   * K and V rows are read straight into VGPRs in MFMA operand layout with 16-byte
-//     buffer loads.  Each 16-token block of a page gets its own buffer descriptor whose
-//     size covers only the block's valid rows, so rows at or past seq_len read as zero
-//     and no access can leave the page.
+//     buffer loads (8-byte for fp8).  Each 16-token block of a page gets its own buffer
+//     descriptor whose size covers only the block's valid rows, so rows at or past seq_len
+//     read as zero and no access can leave the page.
 //   * S^T[token, head] = K * Q^T with v_mfma_f32_16x16x32 (heads padded to 16 per block).
 //   * Online softmax in base 2 (v_exp_f32); the running max is wave-uniform per head.
 //   * O[head, dim] += P * V with the same MFMA; V is transposed in registers by byte

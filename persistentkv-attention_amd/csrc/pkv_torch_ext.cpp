@@ -6,6 +6,9 @@
 //   * q / pages / output may be fp16 or bf16 (all four the same dtype);
 //   * G = Hq / Hkv may be any integer in [1, 32] (the reference accepts {1, 2, 4, 8});
 //   * launch failures raise RuntimeError instead of terminating the process.
+// Beyond the reference's four ops: the two work-queue stages, fp8 (float8_e4m3fn) K/V
+// variants of the indexed and work-queue ops, and the contiguous-layout decode and
+// query-head baseline of its C++ API (cuh:1077-1108, :1263-1282).
 // Work is enqueued on the current HIP stream of the tensors' device without a host sync,
 // so the ops can be captured in HIP graphs.
 
