@@ -1314,11 +1314,13 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     base = ((long)row * a.hq + qh) * a.num_splits;
     stride = 1;
   }
-  const int out_row = a.out_indices ? a.out_indices[row] : row;
-  if (out_row < 0 || out_row >= a.out_rows) return;
+  // The output row is read after the states' loads are issued: in split mode the slot
+  // range needs no memory read, so the merge costs one dependent round trip, not two.
   LseAcc acc;
   fold_slots<QUEUE, false>(acc, a.part_m, a.part_l, a.part_acc, base, stride, count, total, nsplit,
                            split0, lane);
+  const int out_row = a.out_indices ? a.out_indices[row] : row;
+  if (out_row < 0 || out_row >= a.out_rows) return;
   acc.store<Elem>(a.out + ((long)out_row * a.hq + qh) * kD * 2, lane);
 }
 
