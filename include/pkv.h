@@ -291,10 +291,12 @@ int32_t pkv_choose_adaptive_route(
     const int32_t* lengths, int32_t count, const pkv_cost_model* model,
     int32_t* out_splits, double* out_estimated_ms);
 
-/* Sizes the compact work queue for one decode step without building it. */
+/* Sizes the compact work queue for one decode step without building it.  num_q_heads
+ * only matters for PKV_POLICY_MI355X, whose item size depends on the kernel that
+ * G = num_q_heads / num_kv_heads selects; the reference policy ignores it. */
 int pkv_workqueue_size(
     const int32_t* lengths, int32_t count, int32_t requested_splits,
-    int32_t auto_splits, int32_t num_kv_heads, int32_t policy,
+    int32_t auto_splits, int32_t num_q_heads, int32_t num_kv_heads, int32_t policy,
     int32_t* out_num_tasks, int32_t* out_total_partial_slots);
 
 /* Builds one decode step's work-queue metadata, bit-exact with the work-queue branch of
@@ -311,7 +313,7 @@ int pkv_build_workqueue(
     const int32_t* lengths, const int32_t* request_ids, int32_t count,
     const int32_t* page_indptr, const int32_t* page_ids,
     int32_t page_size, int32_t requested_splits, int32_t auto_splits,
-    int32_t num_kv_heads, int32_t policy,
+    int32_t num_q_heads, int32_t num_kv_heads, int32_t policy,
     int32_t* block_table, int32_t table_capacity, int32_t* out_table_cols,
     int32_t* seq_lens, int32_t* q_indices, int32_t* out_indices,
     int32_t* work_items, int32_t work_capacity, int32_t* out_num_tasks,

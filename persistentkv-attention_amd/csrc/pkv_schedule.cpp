@@ -38,15 +38,17 @@ inline int32_t round_up4(int64_t v) { return (int32_t)(floordiv(v + 3, 4) * 4); 
 
 inline int64_t tiles_of(int64_t length) { return floordiv(length + 31, 32); }
 
-// MI355X targets: 256 CUs with one decode workgroup each, about 1.5 work items per CU,
-// and at least this many 32-token tiles per work item so the per-item Q load, LDS
-// combine and partial write stay small next to the K/V stream.  Measured on equal-sized
-// items over the C4 and C5 traces: 384 items was the fastest or tied (C5 G=32: 88.7 us
-// per step against 106 us at 1024 items; C5 G=8 and C4 within 1 % or better), since
-// every item pays a fixed chain of dependent loads and one CU streams at most ~35 GB/s.
+// MI355X targets: 256 CUs with one decode workgroup each, about 1.5 work items per CU
+// for G <= 16, and at least this many 32-token tiles per work item so the per-item Q
+// load, LDS combine and partial write stay small next to the K/V stream.  Measured on
+// equal-sized items over the C4 and C5 traces: 384 items was the fastest or tied for
+// G <= 16 (C5 G=8: 242 us per step against 250-293 us at 372-496 items; C4 within 1 %),
+// since every item pays a fixed chain of dependent loads and one CU streams at most
+// ~35 GB/s.  G > 16 plans at most one item per CU instead (plan_row_splits).
 constexpr int kMiComputeUnits = 256;
 constexpr int kMiTargetItems = kMiComputeUnits * 3 / 2;
 constexpr int kMiMinTilesPerItem = 8;
+constexpr int kMiWideGroup = 16;  // G above this runs the two-head-block kernel
 constexpr int kMiMaxSplits = 128;
 
 }  // namespace
@@ -238,20 +240,41 @@ int32_t pkv_choose_adaptive_route(const int32_t* lengths, int32_t count, const p
 }
 
 static void plan_row_splits(const int32_t* lengths, int32_t count, int32_t requested_splits,
-                            int32_t auto_splits, int32_t num_kv_heads, int32_t policy,
-                            std::vector<int32_t>& out) {
+                            int32_t auto_splits, int32_t num_q_heads, int32_t num_kv_heads,
+                            int32_t policy, std::vector<int32_t>& out) {
   out.resize(count);
   if (auto_splits && policy == PKV_POLICY_MI355X) {
     // Joint plan: size items from the step's total tile count.
-    int64_t total = 0;
-    for (int i = 0; i < count; ++i) total += std::max<int64_t>(1, tiles_of(lengths[i]));
-    const int64_t hkv = num_kv_heads > 0 ? num_kv_heads : 1;
-    const int64_t target = kMiTargetItems;
-    const int64_t per_item = std::max<int64_t>(kMiMinTilesPerItem, ceil_div_pos(total * hkv, target));
+    int64_t total = 0, longest = 1;
     for (int i = 0; i < count; ++i) {
-      const int64_t tiles = std::max<int64_t>(1, tiles_of(lengths[i]));
-      out[i] = (int32_t)std::max<int64_t>(1, std::min<int64_t>(ceil_div_pos(tiles, per_item), kMiMaxSplits));
+      const int64_t t = std::max<int64_t>(1, tiles_of(lengths[i]));
+      total += t;
+      longest = std::max(longest, t);
     }
+    const int64_t hkv = num_kv_heads > 0 ? num_kv_heads : 1;
+    const int64_t group = num_q_heads > 0 ? num_q_heads / hkv : 1;
+    auto splits_of = [&](int64_t tiles, int64_t per_item) {
+      return std::max<int64_t>(1, std::min<int64_t>(ceil_div_pos(tiles, per_item), kMiMaxSplits));
+    };
+    int64_t per_item;
+    if (group > kMiWideGroup) {
+      // The G > 16 kernel runs one workgroup per CU, one wave per SIMD, with a long
+      // epilogue: every item should start in the first round.  Measured on C5 G=32
+      // (bf16, B=64 Zipf): 232 items take 76.1 us per step, 259-291 items 90-100 us and
+      // 415 items 86.0 us.  Grow the items until there are at most kMiComputeUnits.
+      per_item = std::max<int64_t>(kMiMinTilesPerItem, ceil_div_pos(total * hkv, kMiComputeUnits));
+      for (;;) {
+        int64_t items = 0;
+        for (int i = 0; i < count; ++i)
+          items += splits_of(std::max<int64_t>(1, tiles_of(lengths[i])), per_item) * hkv;
+        if (items <= kMiComputeUnits || per_item >= longest) break;
+        per_item += std::max<int64_t>(1, per_item / 16);
+      }
+    } else {
+      per_item = std::max<int64_t>(kMiMinTilesPerItem, ceil_div_pos(total * hkv, kMiTargetItems));
+    }
+    for (int i = 0; i < count; ++i)
+      out[i] = (int32_t)splits_of(std::max<int64_t>(1, tiles_of(lengths[i])), per_item);
     return;
   }
   for (int i = 0; i < count; ++i)
@@ -260,11 +283,12 @@ static void plan_row_splits(const int32_t* lengths, int32_t count, int32_t reque
 }
 
 int pkv_workqueue_size(const int32_t* lengths, int32_t count, int32_t requested_splits,
-                       int32_t auto_splits, int32_t num_kv_heads, int32_t policy,
-                       int32_t* out_num_tasks, int32_t* out_total_partial_slots) {
+                       int32_t auto_splits, int32_t num_q_heads, int32_t num_kv_heads,
+                       int32_t policy, int32_t* out_num_tasks, int32_t* out_total_partial_slots) {
   if ((!lengths && count > 0) || count < 0 || num_kv_heads <= 0) return PKV_ERR_INVALID_ARGUMENT;
   std::vector<int32_t> splits;
-  plan_row_splits(lengths, count, requested_splits, auto_splits, num_kv_heads, policy, splits);
+  plan_row_splits(lengths, count, requested_splits, auto_splits, num_q_heads, num_kv_heads, policy,
+                  splits);
   int64_t tasks = 0, slots = 0;
   for (int r = 0; r < count; ++r) {
     const int64_t total_tiles = tiles_of(lengths[r]);
@@ -282,8 +306,9 @@ int pkv_workqueue_size(const int32_t* lengths, int32_t count, int32_t requested_
 // Work-queue branch of compile_persistentkv_metadata, benchmark_serving_trace.py:668-729.
 int pkv_build_workqueue(const int32_t* lengths, const int32_t* request_ids, int32_t count,
                         const int32_t* page_indptr, const int32_t* page_ids, int32_t page_size,
-                        int32_t requested_splits, int32_t auto_splits, int32_t num_kv_heads,
-                        int32_t policy, int32_t* block_table, int32_t table_capacity,
+                        int32_t requested_splits, int32_t auto_splits, int32_t num_q_heads,
+                        int32_t num_kv_heads, int32_t policy, int32_t* block_table,
+                        int32_t table_capacity,
                         int32_t* out_table_cols, int32_t* seq_lens, int32_t* q_indices,
                         int32_t* out_indices, int32_t* work_items, int32_t work_capacity,
                         int32_t* out_num_tasks, int32_t* split_offsets,
@@ -294,8 +319,8 @@ int pkv_build_workqueue(const int32_t* lengths, const int32_t* request_ids, int3
   const int32_t bucket_length = *std::max_element(lengths, lengths + count);  // :669
   const int64_t page_count = bucket_length > 0 ? ceil_div_pos(bucket_length, page_size) : 0;  // :670
   int32_t tasks = 0, slots = 0;
-  int st = pkv_workqueue_size(lengths, count, requested_splits, auto_splits, num_kv_heads, policy,
-                              &tasks, &slots);
+  int st = pkv_workqueue_size(lengths, count, requested_splits, auto_splits, num_q_heads,
+                              num_kv_heads, policy, &tasks, &slots);
   if (st != PKV_OK) return st;
   if (out_table_cols) *out_table_cols = (int32_t)page_count;
   if (out_num_tasks) *out_num_tasks = tasks;
@@ -305,7 +330,8 @@ int pkv_build_workqueue(const int32_t* lengths, const int32_t* request_ids, int3
       (tasks > 0 && !work_items))
     return PKV_ERR_INVALID_ARGUMENT;
   std::vector<int32_t> splits;
-  plan_row_splits(lengths, count, requested_splits, auto_splits, num_kv_heads, policy, splits);
+  plan_row_splits(lengths, count, requested_splits, auto_splits, num_q_heads, num_kv_heads, policy,
+                  splits);
   int32_t n = 0;
   split_offsets[0] = 0;
   for (int32_t r = 0; r < count; ++r) {

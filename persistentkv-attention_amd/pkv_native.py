@@ -81,10 +81,10 @@ def lib():
     so.pkv_choose_adaptive_route.argtypes = [_PI32, _I32, ctypes.POINTER(CostModel), _PI32,
                                              ctypes.POINTER(ctypes.c_double)]
     so.pkv_choose_adaptive_route.restype = _I32
-    so.pkv_workqueue_size.argtypes = [_PI32, _I32, _I32, _I32, _I32, _I32, _PI32, _PI32]
+    so.pkv_workqueue_size.argtypes = [_PI32, _I32, _I32, _I32, _I32, _I32, _I32, _PI32, _PI32]
     so.pkv_workqueue_size.restype = ctypes.c_int
     so.pkv_build_workqueue.argtypes = [
-        _PI32, _PI32, _I32, _PI32, _PI32, _I32, _I32, _I32, _I32, _I32,
+        _PI32, _PI32, _I32, _PI32, _PI32, _I32, _I32, _I32, _I32, _I32, _I32,
         _PI32, _I32, _PI32, _PI32, _PI32, _PI32, _PI32, _I32, _PI32, _PI32, _PI32]
     so.pkv_build_workqueue.restype = ctypes.c_int
     so.pkv_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, _I32, ctypes.c_void_p,
@@ -158,8 +158,9 @@ def choose_adaptive_route(lengths, model: CostModel | None = None):
 
 
 def build_workqueue(lengths, request_ids, page_lists, page_size, requested_splits, auto_splits,
-                    hkv=8, policy=POLICY_REFERENCE):
-    """One step's work-queue metadata as numpy int32 arrays (see pkv_build_workqueue)."""
+                    hkv=8, policy=POLICY_REFERENCE, hq=32):
+    """One step's work-queue metadata as numpy int32 arrays (see pkv_build_workqueue).
+    ``hq`` (query heads) only steers the MI355X policy's item size."""
     count = len(lengths)
     la, lp = _arr(lengths)
     ra, rp = _arr(request_ids)
@@ -169,8 +170,8 @@ def build_workqueue(lengths, request_ids, page_lists, page_size, requested_split
     ids = np.ascontiguousarray(np.concatenate([np.asarray(p, dtype=np.int32) for p in page_lists])
                                if count else np.zeros(0, dtype=np.int32))
     tasks, slots = _I32(), _I32()
-    st = lib().pkv_workqueue_size(lp, count, requested_splits, int(bool(auto_splits)), hkv, policy,
-                                  ctypes.byref(tasks), ctypes.byref(slots))
+    st = lib().pkv_workqueue_size(lp, count, requested_splits, int(bool(auto_splits)), hq, hkv,
+                                  policy, ctypes.byref(tasks), ctypes.byref(slots))
     if st != PKV_OK:
         raise ValueError(f"pkv_workqueue_size failed with status {st}")
     bucket = int(la.max()) if count else 0
@@ -184,7 +185,7 @@ def build_workqueue(lengths, request_ids, page_lists, page_size, requested_split
     out_cols, out_tasks, out_slots = _I32(), _I32(), _I32()
     st = lib().pkv_build_workqueue(
         lp, rp, count, indptr.ctypes.data_as(_PI32), ids.ctypes.data_as(_PI32), page_size,
-        requested_splits, int(bool(auto_splits)), hkv, policy, table.ctypes.data_as(_PI32),
+        requested_splits, int(bool(auto_splits)), hq, hkv, policy, table.ctypes.data_as(_PI32),
         table.size, ctypes.byref(out_cols), seq.ctypes.data_as(_PI32), qi.ctypes.data_as(_PI32),
         oi.ctypes.data_as(_PI32), items.ctypes.data_as(_PI32), items.shape[0],
         ctypes.byref(out_tasks), offs.ctypes.data_as(_PI32), ctypes.byref(out_slots))

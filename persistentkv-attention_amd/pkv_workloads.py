@@ -370,7 +370,8 @@ def compile_step(w: Workload, step_index: int, device) -> StepMeta:
     output = torch.empty(n, w.hq, HEAD_DIM, device=device, dtype=w.dtype)
     if w.op == "paged_attention_workqueue":
         meta = pkv_native.build_workqueue(list(st.lengths), list(st.active_ids), page_lists,
-                                          w.page_size, w.splits, w.auto_splits, w.hkv, w.policy)
+                                          w.page_size, w.splits, w.auto_splits, w.hkv, w.policy,
+                                          hq=w.hq)
         return StepMeta(w.op, meta["bucket_length"], t(meta["block_table"]), t(meta["seq_lens"]),
                         t(meta["q_indices"]), t(meta["out_indices"]), output, meta["splits"],
                         t(meta["work_items"]), t(meta["split_offsets"]),

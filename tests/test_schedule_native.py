@@ -68,8 +68,10 @@ def test_mi355x_planner_invariants():
         n = int(rng.integers(1, 65))
         lengths = [int(x) for x in rng.integers(1, 70000, size=n)]
         hkv = int(rng.choice([1, 4, 8, 32]))
+        group = int(rng.choice([1, 4, 8, 16, 32]))
         pages = [list(range(-(-x // 16) + 1)) for x in lengths]
-        meta = nat.build_workqueue(lengths, list(range(n)), pages, 16, 1, True, hkv, nat.POLICY_MI355X)
+        meta = nat.build_workqueue(lengths, list(range(n)), pages, 16, 1, True, hkv, nat.POLICY_MI355X,
+                                   hq=hkv * group)
         m = {k: (v.tolist() if hasattr(v, "tolist") else v) for k, v in meta.items()}
         check_builder_invariants(m, lengths, hkv, pages, 16)
         row_splits = np.diff(meta["split_offsets"])
@@ -77,6 +79,10 @@ def test_mi355x_planner_invariants():
         assert np.all(row_splits >= 1) and np.all(row_splits <= np.maximum(tiles, 1))
         # no empty splits: every slot has work
         assert len(meta["work_items"]) == int(row_splits.sum()) * hkv
+        # G > 16 (the two-head-block kernel): every item starts in the first round on 256
+        # CUs, unless the rows alone (one split each) are more than that
+        if group > 16:
+            assert len(meta["work_items"]) <= max(256, n * hkv)
 
 
 def test_c4_step_uses_twenty_splits():
