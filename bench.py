@@ -287,7 +287,11 @@ def main():
                                          "speedup": round(base_us / (gpu_ms * 1e3 / args.steps), 2)}
     if not args.no_cpu_baseline:
         q_cpu = q_pool.cpu()
-        k_cpu, v_cpu = wl.dequantised(w, k0.cpu(), v0.cpu())
+        k_cpu, v_cpu = k0.cpu(), v0.cpu()
+        if w.kv_fp8:  # the oracle attends to k_scale * e4m3(k8), v_scale * e4m3(v8)
+            from oracle import attention as oracle
+            k_cpu = oracle.dequantize_e4m3(k_cpu, w.k_scale)
+            v_cpu = oracle.dequantize_e4m3(v_cpu, w.v_scale)
         result["cpu_baseline"] = cpu_baseline(w, q_cpu, k_cpu, v_cpu, metas, args.cpu_seconds)
     print(json.dumps(result), flush=True)
 

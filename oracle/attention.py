@@ -148,3 +148,28 @@ def canonical_block_table(context, page_size=16):
     logical = context // page_size
     physical = logical * 2
     return [(405 * p + 17) % physical for p in range(logical)]
+
+
+def e4m3_value(code):
+    """OCP FP8 E4M3 (the `float8_e4m3fn` format) decoded from the format's definition
+    (OCP 8-bit Floating Point Specification v1.0): sign bit, 4 exponent bits with bias 7,
+    3 mantissa bits; exponent 0 is subnormal (2^-6 * m/8); no infinities; only
+    S.1111.111 is NaN, so the largest finite value is 1.75 * 2^8 = 448.  The reference has
+    no fp8 path; this pins the dequantisation the fp8 K/V ops are checked against."""
+    sign = -1.0 if code & 0x80 else 1.0
+    exponent, mantissa = (code >> 3) & 0xF, code & 0x7
+    if exponent == 0xF and mantissa == 0x7:
+        return float("nan")
+    if exponent == 0:
+        return sign * 2.0 ** -6 * (mantissa / 8.0)
+    return sign * 2.0 ** (exponent - 7) * (1.0 + mantissa / 8.0)
+
+
+E4M3_TABLE = np.array([e4m3_value(c) for c in range(256)], dtype=np.float32)
+
+
+def dequantize_e4m3(pages, scale):
+    """fp32 ``scale * e4m3(pages)`` for a tensor of e4m3 bytes (``float8_e4m3fn`` or
+    ``uint8``)."""
+    codes = _cpu(pages).contiguous().view(torch.uint8).numpy()
+    return torch.from_numpy(E4M3_TABLE[codes] * np.float32(scale))

@@ -323,14 +323,6 @@ def make_kv_pool(w: Workload, device, seed_offset=7):
     return k, v
 
 
-def dequantised(w: Workload, k, v):
-    """The K and V values the engine attends to: ``(k8 * k_scale, v8 * v_scale)`` in fp32
-    for fp8 pools, the pools themselves otherwise."""
-    if not w.kv_fp8:
-        return k, v
-    return k.float() * w.k_scale, v.float() * w.v_scale
-
-
 def make_q_pool(w: Workload, device):
     """Q ``[steps, requests, Hq, 128]`` ~ N(0, 1) drawn on the CPU with ``seed + 2026``
     (reference :301-309), then moved to ``device``."""

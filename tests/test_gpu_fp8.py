@@ -1,9 +1,10 @@
 """fp8 (OCP e4m3) K/V ops against the repack + fp32 SDPA oracle on the dequantised K/V.
 
 K and V pages are quantised on the host with torch's float8_e4m3fn (round to nearest even,
-after clamping to +-448) under per-tensor scales; the oracle attends to k8.float() *
-k_scale and v8.float() * v_scale.  The engine unpacks e4m3 exactly to fp16 / bf16 in
-registers, so the comparison keeps the 2e-3 / 3e-4 gate of the 2-byte ops.  One case fills
+after clamping to +-448) under per-tensor scales; the oracle attends to k_scale * e4m3(k8)
+and v_scale * e4m3(v8), decoded by oracle.attention.dequantize_e4m3 from the format's
+definition (pinned in tests/test_oracle_fp8.py).  The engine unpacks e4m3 exactly to
+fp16 / bf16 in registers, so the comparison keeps the 2e-3 / 3e-4 gate of the 2-byte ops.  One case fills
 a K and a V page with every finite e4m3 code (both signs, subnormals, +-448), which pins
 the unpacking instruction's format and byte order: a misread code moves its token's
 score or value.
@@ -25,7 +26,7 @@ def quantise(x, scale):
 
 
 def dequantise(x8, scale):
-    return x8.float() * scale
+    return oracle.dequantize_e4m3(x8, scale)  # the closed-form decode, pinned on the CPU
 
 
 def every_code_page(page_size, hkv, seed):
