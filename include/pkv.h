@@ -339,6 +339,14 @@ int pkv_probe_copy(const void* src, void* dst, size_t bytes, void* stream);
 int pkv_probe_read_cus(const void* src, size_t bytes, int32_t pattern, int32_t workgroups,
                        void* sink, void* stream);
 
+/* pkv_probe_read_cus with `waves` (4, 8 or 16) waves per workgroup, each keeping
+ * `chunks_per_wave` (1, 2 or 4) 4 KB chunks in flight: read bandwidth and loaded latency
+ * (bytes in flight / bandwidth) against how the bytes in flight are spread over waves.
+ * No counterpart in the reference. */
+int pkv_probe_read_inflight(const void* src, size_t bytes, int32_t pattern, int32_t waves,
+                            int32_t chunks_per_wave, int32_t workgroups, void* sink,
+                            void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

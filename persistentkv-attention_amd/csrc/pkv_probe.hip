@@ -59,6 +59,39 @@ __global__ __launch_bounds__(512) void probe_read_kernel(const uint8_t* src, uin
   if (x == 0x9e3779b9u) sink[blockIdx.x] = x;  // keeps the loads alive; practically never true
 }
 
+// Per-CU bandwidth against bytes in flight: each wave keeps U chunks (U x 4 KB) in flight
+// and workgroups have `blockDim.x / 64` waves (4, 8 or 16).
+template <int U>
+__global__ __launch_bounds__(1024) void probe_inflight_kernel(const uint8_t* src, uint64_t chunks,
+                                                              uint64_t stride, int pattern,
+                                                              uint32_t* sink) {
+  const int lane = threadIdx.x & 63;
+  const int waves_per_group = blockDim.x >> 6;
+  const uint64_t wave = (uint64_t)blockIdx.x * waves_per_group + (threadIdx.x >> 6);
+  const uint64_t nwaves = (uint64_t)gridDim.x * waves_per_group;
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  for (uint64_t base = wave; base < chunks; base += U * nwaves) {
+    u32x4 v[U][4];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint64_t idx = base + u * nwaves;
+      const uint64_t chunk = (idx * stride) % chunks;
+      const int nrec = idx < chunks ? 4096 : 0;
+      const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(src + chunk * 4096), (short)0, __builtin_amdgcn_readfirstlane(nrec), kRsrcWord3);
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        v[u][k] = __builtin_amdgcn_raw_buffer_load_b128(r, lane_offset(pattern, lane, k), 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) acc ^= v[u][k];
+  }
+  const uint32_t x = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+  if (x == 0x9e3779b9u) sink[blockIdx.x] = x;
+}
+
 __global__ __launch_bounds__(256) void probe_copy_kernel(const u32x4* src, u32x4* dst, uint64_t n16) {
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride)
@@ -96,6 +129,31 @@ int pkv_probe_read_cus(const void* src, size_t bytes, int32_t pattern, int32_t w
   const uint64_t stride = chunks > 1 ? 2147483647ull % chunks : 1;
   hipLaunchKernelGGL(probe_read_kernel, dim3(workgroups), dim3(512), 96 * 1024, (hipStream_t)stream,
                      (const uint8_t*)src, chunks, stride ? stride : 1, pattern, (uint32_t*)sink);
+  return hipGetLastError() == hipSuccess ? PKV_OK : PKV_ERR_LAUNCH;
+}
+
+// pkv_probe_read_cus with `waves` (4, 8 or 16) waves per workgroup, each keeping
+// `chunks_per_wave` (1, 2 or 4) chunks of 4 KB in flight.
+int pkv_probe_read_inflight(const void* src, size_t bytes, int32_t pattern, int32_t waves,
+                            int32_t chunks_per_wave, int32_t workgroups, void* sink, void* stream) {
+  if (!src || !sink || bytes < 4096 || bytes % 4096 || bytes / 4096 >= 2147483647ull ||
+      pattern < 0 || pattern > 2 || workgroups <= 0 || workgroups > 65536 ||
+      (waves != 4 && waves != 8 && waves != 16) ||
+      (chunks_per_wave != 1 && chunks_per_wave != 2 && chunks_per_wave != 4))
+    return PKV_ERR_INVALID_ARGUMENT;
+  const uint64_t chunks = bytes / 4096;
+  const uint64_t stride = chunks > 1 ? 2147483647ull % chunks : 1;
+  const dim3 grid(workgroups), block(waves * 64);
+  const size_t lds = 96 * 1024;  // at most one workgroup per CU
+  hipStream_t s = (hipStream_t)stream;
+  const uint8_t* p = (const uint8_t*)src;
+  const uint64_t st = stride ? stride : 1;
+  if (chunks_per_wave == 1)
+    hipLaunchKernelGGL(probe_inflight_kernel<1>, grid, block, lds, s, p, chunks, st, pattern, (uint32_t*)sink);
+  else if (chunks_per_wave == 2)
+    hipLaunchKernelGGL(probe_inflight_kernel<2>, grid, block, lds, s, p, chunks, st, pattern, (uint32_t*)sink);
+  else
+    hipLaunchKernelGGL(probe_inflight_kernel<4>, grid, block, lds, s, p, chunks, st, pattern, (uint32_t*)sink);
   return hipGetLastError() == hipSuccess ? PKV_OK : PKV_ERR_LAUNCH;
 }
 

@@ -6,6 +6,7 @@ The MI355X counterpart of the reference's micro_benchmarks/01_hbm_bandwidth.cu:2
   python hbm_probe.py read            # read bandwidth for the decode kernel's access patterns
   python hbm_probe.py copy --mib 1024 # one known-size copy per launch, for rocprofv3 --pmc
   python hbm_probe.py cus             # read bandwidth of 8 .. 256 CUs, one workgroup each
+  python hbm_probe.py inflight        # bandwidth and loaded latency vs bytes in flight per wave
 
 ``read`` reports GB/s per pattern (contiguous, K-operand 16 rows x 64 B, V-operand 4 rows
 x 256 B) and size; sizes above the 256 MB Infinity Cache measure HBM.  ``copy`` launches
@@ -85,6 +86,35 @@ def run_cus(counts, mib, iters):
               f"per workgroup ({ms * 1e3:8.1f} us)", flush=True)
 
 
+def run_inflight(counts, mib, iters, patterns):
+    """Read bandwidth of `n` workgroups (at most one per CU) for 8 and 16 waves per
+    workgroup and 1, 2 or 4 chunks of 4 KB in flight per wave.  Latency is Little's law:
+    bytes in flight per CU / bandwidth per CU."""
+    import torch
+
+    import pkv_native
+
+    lib = pkv_native.lib()
+    dev = torch.device("cuda:0")
+    nbytes = mib << 20
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=dev).random_(0, 256)
+    sink = torch.zeros(65536, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    print("| pattern | waves | KB in flight per wave | workgroups | GB/s | GB/s per CU | latency us |")
+    print("|---|---:|---:|---:|---:|---:|---:|")
+    for pattern in patterns:
+        for waves in (8, 16):
+            for u in (1, 2, 4):
+                for n in counts:
+                    ms = _time_ms(torch, lambda: _check(lib, lib.pkv_probe_read_inflight(
+                        buf.data_ptr(), nbytes, pattern, waves, u, n, sink.data_ptr(), stream)), iters)
+                    gbps = nbytes / ms / 1e6
+                    per_cu = gbps / n
+                    kb = waves * u * 4
+                    print(f"| {PATTERNS[pattern]} | {waves} | {4 * u} | {n} | {gbps:.0f} | "
+                          f"{per_cu:.1f} | {kb * 1024 / (per_cu * 1e3):.2f} |", flush=True)
+
+
 def run_copy(mib, iters):
     import torch
 
@@ -114,6 +144,11 @@ def main(argv=None):
     u.add_argument("--workgroups", type=int, nargs="+", default=[8, 32, 64, 128, 160, 192, 256])
     u.add_argument("--mib", type=int, default=1024)
     u.add_argument("--iters", type=int, default=3)
+    f = sub.add_parser("inflight")
+    f.add_argument("--workgroups", type=int, nargs="+", default=[8, 128, 256])
+    f.add_argument("--mib", type=int, default=4096)
+    f.add_argument("--iters", type=int, default=2)
+    f.add_argument("--patterns", type=int, nargs="+", default=[1, 2])
     c = sub.add_parser("copy")
     c.add_argument("--mib", type=int, default=1024)
     c.add_argument("--iters", type=int, default=4)
@@ -122,6 +157,8 @@ def main(argv=None):
         run_read(a.mib, a.iters)
     elif a.cmd == "cus":
         run_cus(a.workgroups, a.mib, a.iters)
+    elif a.cmd == "inflight":
+        run_inflight(a.workgroups, a.mib, a.iters, a.patterns)
     else:
         run_copy(a.mib, a.iters)
 

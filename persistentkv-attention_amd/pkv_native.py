@@ -96,6 +96,9 @@ def lib():
     so.pkv_probe_read_cus.argtypes = [ctypes.c_void_p, ctypes.c_size_t, _I32, _I32,
                                       ctypes.c_void_p, ctypes.c_void_p]
     so.pkv_probe_read_cus.restype = ctypes.c_int
+    so.pkv_probe_read_inflight.argtypes = [ctypes.c_void_p, ctypes.c_size_t, _I32, _I32, _I32,
+                                           _I32, ctypes.c_void_p, ctypes.c_void_p]
+    so.pkv_probe_read_inflight.restype = ctypes.c_int
     _lib = so
     return so
 
