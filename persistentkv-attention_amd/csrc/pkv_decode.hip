@@ -205,6 +205,15 @@ __device__ inline int load_scalar(const int32_t* p) {
   return uniform(*(const __attribute__((address_space(4))) int32_t*)p);
 }
 
+// Vector (buffer) load of a wave-uniform int.  Unlike a scalar load, whose completion can
+// only be waited for together with every other scalar load in flight (kernel-argument
+// reads included), it completes in issue order with the wave's other vector loads.
+__device__ inline int load_vector_uniform(const int32_t* p) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(p), (short)0, 4, kRsrcWord3);
+  return uniform((int)__builtin_amdgcn_raw_buffer_load_b32(r, 0, 0, 0));
+}
+
 // ---------------------------------------------------------------------------------
 // Page loaders.  A wave streams tiles [t0, t1) of one (row, kv head); tokens at or past
 // `lim` = min(row length, 32 * t1) are never read.  Each loader splits a tile into
@@ -789,27 +798,67 @@ struct LseAcc {
   }
 };
 
+// Up to 32 slot states as one wave loads them: lane j holds (m, l) of slot c0 + j and
+// v[j] this lane's two dims of that slot's acc.  All loads are issued together; slots
+// past the chunk re-read its last one.
+struct SlotChunk {
+  float ms, ls;
+  f32x2 v[kMergeChunk];
+};
+
+template <bool COHERENT>
+__device__ inline void load_chunk(SlotChunk& c, const float* pm, const float* pl, const float* pacc,
+                                  long base, long stride, int c0, int n, int lane) {
+  const int s_lane = c0 + (lane < n ? lane : n - 1);
+  c.ms = get_f32<COHERENT>(pm + base + (long)s_lane * stride);
+  c.ls = get_f32<COHERENT>(pl + base + (long)s_lane * stride);
+#pragma unroll
+  for (int j = 0; j < kMergeChunk; ++j) {
+    const int s = c0 + (j < n ? j : n - 1);
+    c.v[j] = get_f32x2<COHERENT>(pacc + (base + (long)s * stride) * kD + 2 * lane);
+  }
+}
+
+// load_chunk through buffer descriptors that cover the chunk's states (n >= 1): when
+// `enable` is false they cover nothing, and the loads return zeros without reading memory.
+__device__ inline void load_chunk_if(SlotChunk& c, const float* pm, const float* pl, const float* pacc,
+                                     long base, long stride, int n, int lane, bool enable) {
+  const int span = enable ? (int)((long)(n - 1) * stride + 1) : 0;  // states from base
+  const __amdgpu_buffer_rsrc_t rm =
+      __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(pm + base), (short)0, uniform(span * 4), kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rl =
+      __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(pl + base), (short)0, uniform(span * 4), kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+      uniform_ptr(pacc + base * kD), (short)0, uniform(span * kD * 4), kRsrcWord3);
+  const int s_lane = lane < n ? lane : n - 1;
+  c.ms = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rm, (int)(s_lane * stride * 4), 0, 0));
+  c.ls = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, (int)(s_lane * stride * 4), 0, 0));
+#pragma unroll
+  for (int j = 0; j < kMergeChunk; ++j) {
+    const int s = j < n ? j : n - 1;
+    c.v[j] = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                                           ra, (int)((s * stride * kD + 2 * lane) * 4), 0, 0));
+  }
+}
+
+// Whether slot s of a row holds a state: in queue mode the builder leaves splits with no
+// tiles empty (split0 + s of nsplit splits over `total` tiles).
+template <bool QUEUE>
+__device__ inline bool slot_live(int s, int count, int total, int nsplit, int split0) {
+  return s < count &&
+         !(QUEUE && (long)total * (split0 + s) / nsplit == (long)total * (split0 + s + 1) / nsplit);
+}
+
+// Folds slot states [c_begin, count) into acc, 32 at a time.
 template <bool QUEUE, bool COHERENT>
 __device__ inline void fold_slots(LseAcc& acc, const float* pm, const float* pl, const float* pacc,
                                   long base, long stride, int count, int total, int nsplit,
-                                  int split0, int lane) {
-  auto live = [&](int s) {
-    return s < count &&
-           !(QUEUE && (long)total * (split0 + s) / nsplit == (long)total * (split0 + s + 1) / nsplit);
-  };
-  for (int c0 = 0; c0 < count; c0 += kMergeChunk) {
+                                  int split0, int lane, int c_begin = 0) {
+  for (int c0 = c_begin; c0 < count; c0 += kMergeChunk) {
     const int n = count - c0 < kMergeChunk ? count - c0 : kMergeChunk;
-    // Issue the chunk's loads together (tail slots re-read the last index).
-    const int s_lane = c0 + (lane < n ? lane : n - 1);
-    const float ms = get_f32<COHERENT>(pm + base + (long)s_lane * stride);
-    const float ls = get_f32<COHERENT>(pl + base + (long)s_lane * stride);
-    f32x2 v[kMergeChunk];
-#pragma unroll
-    for (int j = 0; j < kMergeChunk; ++j) {
-      const int s = c0 + (j < n ? j : n - 1);
-      v[j] = get_f32x2<COHERENT>(pacc + (base + (long)s * stride) * kD + 2 * lane);
-    }
-    acc.fold(lane < n && live(c0 + lane), ms, ls, v);
+    SlotChunk c;
+    load_chunk<COHERENT>(c, pm, pl, pacc, base, stride, c0, n, lane);
+    acc.fold(lane < n && slot_live<QUEUE>(c0 + lane, count, total, nsplit, split0), c.ms, c.ls, c.v);
   }
 }
 
@@ -1297,14 +1346,26 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   const int qh = uniform(wave_id - row * a.hq);
   int count, total = 0, nsplit = 1, split0 = 0;
   long base, stride;
+  SlotChunk guessed;
+  bool hit = false;
   if (QUEUE) {
-    const int o0 = uniform(a.split_offsets[row]), o1 = uniform(a.split_offsets[row + 1]);
+    // With a fixed split count every row owns total_slots / batch slots.  The first chunk
+    // of that slot range is loaded right behind the row's offsets and length and used when
+    // the offsets match: the merge then waits for one memory round trip instead of two.
+    // (Vector loads complete in issue order, so the offsets can be waited for alone.)
+    const int o0 = load_vector_uniform(a.split_offsets + row);
+    const int o1 = load_vector_uniform(a.split_offsets + row + 1);
+    int len = load_vector_uniform(a.seq_lens + row);
+    const int per_row = a.total_slots / a.batch;
+    const bool guess = per_row > 0 && per_row * a.batch == a.total_slots;
+    load_chunk_if(guessed, a.part_m, a.part_l, a.part_acc, (long)row * per_row * a.hq + qh, a.hq,
+                  per_row < 1 ? 1 : (per_row < kMergeChunk ? per_row : kMergeChunk), lane, guess);
+    hit = guess && o0 == row * per_row && o1 - o0 == per_row;
     const int first = o0 < 0 ? 0 : o0;
     const int last = o1 > a.total_slots ? a.total_slots : o1;
     count = last - first;
     nsplit = o1 - o0;
     split0 = first - o0;
-    int len = uniform(a.seq_lens[row]);
     if (len > a.max_tokens) len = a.max_tokens;
     total = ceil_tiles(len < 0 ? 0 : len);
     base = (long)first * a.hq + qh;
@@ -1317,8 +1378,24 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   // The output row is read after the states' loads are issued: in split mode the slot
   // range needs no memory read, so the merge costs one dependent round trip, not two.
   LseAcc acc;
+  int c_begin = 0;
+  if (QUEUE) {
+    // Chunk 0: the guessed loads when the offsets matched, else loaded now (a descriptor
+    // that covers nothing when the row has no slots).  The guessed values are selected,
+    // not branched on, so their loads stay ahead of the wait for the offsets.
+    const int n = count < 1 ? 1 : (count < kMergeChunk ? count : kMergeChunk);
+    SlotChunk c;
+    if (!hit) load_chunk_if(c, a.part_m, a.part_l, a.part_acc, base, stride, n, lane, count > 0);
+    c.ms = hit ? guessed.ms : c.ms;
+    c.ls = hit ? guessed.ls : c.ls;
+#pragma unroll
+    for (int j = 0; j < kMergeChunk; ++j) c.v[j] = hit ? guessed.v[j] : c.v[j];
+    acc.fold(lane < count && lane < kMergeChunk && slot_live<QUEUE>(lane, count, total, nsplit, split0),
+             c.ms, c.ls, c.v);
+    c_begin = kMergeChunk;
+  }
   fold_slots<QUEUE, false>(acc, a.part_m, a.part_l, a.part_acc, base, stride, count, total, nsplit,
-                           split0, lane);
+                           split0, lane, c_begin);
   const int out_row = a.out_indices ? a.out_indices[row] : row;
   if (out_row < 0 || out_row >= a.out_rows) return;
   acc.store<Elem>(a.out + ((long)out_row * a.hq + qh) * kD * 2, lane);
