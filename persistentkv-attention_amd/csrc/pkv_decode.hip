@@ -213,6 +213,13 @@ __device__ inline int load_vector_uniform(const int32_t* p) {
       __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(p), (short)0, 4, kRsrcWord3);
   return uniform((int)__builtin_amdgcn_raw_buffer_load_b32(r, 0, 0, 0));
 }
+// The same load issued without waiting for it: the result stays in a VGPR (0 when p is
+// null, which reads nothing) until uniform() is applied where it is used.
+__device__ inline int load_vector_deferred(const int32_t* p) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(p), (short)0, p ? 4 : 0, kRsrcWord3);
+  return (int)__builtin_amdgcn_raw_buffer_load_b32(r, 0, 0, 0);
+}
 
 // ---------------------------------------------------------------------------------
 // Page loaders.  A wave streams tiles [t0, t1) of one (row, kv head); tokens at or past
@@ -1344,6 +1351,8 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   if (wave_id >= a.batch * a.hq) return;
   const int row = uniform(wave_id / a.hq);
   const int qh = uniform(wave_id - row * a.hq);
+  // The output row is loaded first and waited for last, so it costs no round trip of its own.
+  const int out_row_loaded = load_vector_deferred(a.out_indices ? a.out_indices + row : nullptr);
   int count, total = 0, nsplit = 1, split0 = 0;
   long base, stride;
   SlotChunk guessed;
@@ -1375,8 +1384,8 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     base = ((long)row * a.hq + qh) * a.num_splits;
     stride = 1;
   }
-  // The output row is read after the states' loads are issued: in split mode the slot
-  // range needs no memory read, so the merge costs one dependent round trip, not two.
+  // In split mode the slot range needs no memory read: the merge costs one memory round
+  // trip (the states), as it does in queue mode when the fixed-split guess holds.
   LseAcc acc;
   int c_begin = 0;
   if (QUEUE) {
@@ -1396,7 +1405,7 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   }
   fold_slots<QUEUE, false>(acc, a.part_m, a.part_l, a.part_acc, base, stride, count, total, nsplit,
                            split0, lane, c_begin);
-  const int out_row = a.out_indices ? a.out_indices[row] : row;
+  const int out_row = a.out_indices ? uniform(out_row_loaded) : row;
   if (out_row < 0 || out_row >= a.out_rows) return;
   acc.store<Elem>(a.out + ((long)out_row * a.hq + qh) * kD * 2, lane);
 }
