@@ -646,6 +646,37 @@ struct Unit {
 
 __device__ inline int ceil_tiles(int len) { return (len + kTile - 1) / kTile; }
 
+// Work-queue unit from a work item and its row's length and slot offsets.  Malformed
+// items are marked invalid (and skipped) instead of addressing outside the buffers.
+__device__ inline Unit queue_unit(const DecodeArgs& a, int row, int kvh, int split, int tb, int te,
+                                  int len, int so0, int so1) {
+  Unit u;
+  u.valid = true;
+  u.row = row;
+  u.kvh = kvh;
+  u.split = split;
+  u.tb = tb < 0 ? 0 : tb;
+  u.te = te;
+  u.len = 0;
+  u.slot_base = 0;
+  u.row_splits = 1;
+  if (row < 0 || row >= a.batch || kvh < 0 || kvh >= a.hkv || split < 0) {
+    u.valid = false;
+    return u;
+  }
+  // The reference trusts seq_lens (cuh:217-219); clamping to the table width keeps every
+  // page lookup inside the row for any input.
+  const long cap = (long)a.max_pages * a.page_size;
+  u.len = len > cap ? (int)cap : (len < 0 ? 0 : len);
+  u.slot_base = so0;
+  u.row_splits = so1 - so0;
+  const int total = ceil_tiles(u.len);
+  if (split >= u.row_splits) u.valid = false;
+  if (u.te > total) u.te = total;
+  if (u.slot_base < 0 || u.slot_base + split >= a.total_slots) u.valid = false;
+  return u;
+}
+
 template <int MODE>
 __device__ inline Unit resolve_unit(const DecodeArgs& a, int idx) {
   Unit u;
@@ -672,24 +703,11 @@ __device__ inline Unit resolve_unit(const DecodeArgs& a, int idx) {
     u.te = (int)(((long)total * (u.split + 1)) / a.num_splits);
   } else {
     const int32_t* w = a.work_items + (long)idx * 5;
-    u.row = load_scalar(w + 0);
-    u.kvh = load_scalar(w + 1);
-    u.split = load_scalar(w + 2);
-    u.tb = load_scalar(w + 3);
-    u.te = load_scalar(w + 4);
-    // Malformed items are skipped instead of addressing outside the buffers.
-    if (u.row < 0 || u.row >= a.batch || u.kvh < 0 || u.kvh >= a.hkv || u.split < 0) {
-      u.valid = false;
-      return u;
-    }
-    u.len = row_length(a, u.row);
-    u.slot_base = uniform(a.split_offsets[u.row]);
-    u.row_splits = uniform(a.split_offsets[u.row + 1]) - u.slot_base;
-    const int total = ceil_tiles(u.len);
-    if (u.split >= u.row_splits) u.valid = false;
-    if (u.tb < 0) u.tb = 0;
-    if (u.te > total) u.te = total;
-    if (u.slot_base < 0 || u.slot_base + u.split >= a.total_slots) u.valid = false;
+    const int row = load_scalar(w + 0), kvh = load_scalar(w + 1), split = load_scalar(w + 2);
+    const int tb = load_scalar(w + 3), te = load_scalar(w + 4);
+    const int row_c = row < 0 ? 0 : (row >= a.batch ? a.batch - 1 : row);
+    u = queue_unit(a, row, kvh, split, tb, te, uniform(a.seq_lens[row_c]),
+                   uniform(a.split_offsets[row_c]), uniform(a.split_offsets[row_c + 1]));
   }
   return u;
 }
@@ -939,9 +957,8 @@ __device__ inline void unit_states(const DecodeArgs& a, const Unit& u, int qh0, 
 
 // Q^T operand: lane (g, c) holds head hb*16 + c, dims 32kk + 8g .. +8.
 template <int HB>
-__device__ inline void load_q(const DecodeArgs& a, int row, int qh0, int lane, u32x4 (&qf)[HB][4]) {
+__device__ inline void load_q(const DecodeArgs& a, int q_row, int qh0, int lane, u32x4 (&qf)[HB][4]) {
   const int c = lane & 15, g = lane >> 4;
-  int q_row = a.q_indices ? a.q_indices[row] : row;
   q_row = q_row < 0 ? 0 : (q_row >= a.q_rows ? a.q_rows - 1 : q_row);
 #pragma unroll
   for (int hb = 0; hb < HB; ++hb) {
@@ -1227,11 +1244,12 @@ __device__ inline bool combine_async(const DecodeArgs& a, const WaveState<HB>& s
 constexpr int kSoloTiles = 2;
 
 template <class Elem, int HB, int PG, int MODE>
-__device__ void solo_unit(const DecodeArgs& a, const Unit& u, int t0, int t1, const Dest& d,
-                          int lane, bool have_first, FastPager::Pages f0, FastPager::Pages f1) {
+__device__ void solo_unit(const DecodeArgs& a, const Unit& u, int q_row, int t0, int t1,
+                          const Dest& d, int lane, bool have_first, FastPager::Pages f0,
+                          FastPager::Pages f1) {
   const int qh0 = u.kvh * a.group;
   u32x4 qf[HB][4];
-  load_q<HB>(a, u.row, qh0, lane, qf);
+  load_q<HB>(a, q_row, qh0, lane, qf);
   WaveState<HB> st;
   init_state<HB>(st);
   stream_unit<Elem, HB, PG>(a, st, qf, u.row, u.kvh, t0, t1, u.len, lane, have_first, f0, f1);
@@ -1260,25 +1278,38 @@ void decode_kernel(DecodeArgs a) {
   const int wave = uniform(tid >> 6);
   const int G = a.group;
 
-  // Work-queue units: issue this wave's first two block-table reads together with the
-  // row metadata loads (they need only the work item), shortening the dependent chain
-  // work item -> row metadata -> table -> K/V by one memory round trip.
+  // Work-queue units: one dependent round trip for the work item, then one for all it
+  // points to, issued together: the row's length, slot offsets and query row (vector
+  // loads, waited for together) and this wave's first two block-table reads (scalar
+  // loads).  Q and the first K/V tile are issued after that, so the chain before the
+  // first K/V request is two round trips.
   FastPager::Pages first0 = {}, first1 = {};
   int first_tile = -1;
-  if (MODE == kQueue && (PG == kPgFast || PG == kPgFp8)) {
+  Unit u;
+  int q_row;
+  if constexpr (MODE == kQueue && (PG == kPgFast || PG == kPgFp8)) {
     const int32_t* w = a.work_items + (long)blockIdx.x * 5;
-    int row = load_scalar(w + 0), kvh = load_scalar(w + 1);
+    const int row = load_scalar(w + 0), kvh = load_scalar(w + 1), split = load_scalar(w + 2);
     const int tb = load_scalar(w + 3), te = load_scalar(w + 4);
-    row = row < 0 ? 0 : (row >= a.batch ? a.batch - 1 : row);
-    kvh = kvh < 0 ? 0 : (kvh >= a.hkv ? a.hkv - 1 : kvh);
+    const int row_c = row < 0 ? 0 : (row >= a.batch ? a.batch - 1 : row);
+    const int kvh_c = kvh < 0 ? 0 : (kvh >= a.hkv ? a.hkv - 1 : kvh);
+    const int len_l = load_vector_deferred(a.seq_lens + row_c);
+    const int so0_l = load_vector_deferred(a.split_offsets + row_c);
+    const int so1_l = load_vector_deferred(a.split_offsets + row_c + 1);
+    const int qi_l = load_vector_deferred(a.q_indices ? a.q_indices + row_c : nullptr);
     const int n = te > tb ? te - tb : 0;
     first_tile = uniform(tb + (n * wave) / kWaves);
-    const FastPager pg(a, row, kvh, 0, lane);
+    const FastPager pg(a, row_c, kvh_c, 0, lane);
     first0 = pg.lookup(first_tile);
     first1 = pg.lookup(first_tile + 1);
+    u = queue_unit(a, row, kvh, split, tb, te, uniform(len_l), uniform(so0_l), uniform(so1_l));
+    q_row = a.q_indices ? uniform(qi_l) : row;
+  } else {
+    u = resolve_unit<MODE>(a, blockIdx.x);
+    // The query row needs only the unit's row: load it alongside the unit's metadata.
+    q_row = u.row;
+    if (a.q_indices && u.valid) q_row = uniform(load_vector_deferred(a.q_indices + u.row));
   }
-
-  const Unit u = resolve_unit<MODE>(a, blockIdx.x);
   if (!u.valid) return;
   const int qh0 = u.kvh * G;
   long state0, state_stride;
@@ -1296,7 +1327,8 @@ void decode_kernel(DecodeArgs a) {
   const int n = u.te - u.tb;
   if (n <= kSoloTiles) {
     if (wave == 0)
-      solo_unit<Elem, HB, PG, MODE>(a, u, u.tb, u.te, d, lane, u.tb == first_tile, first0, first1);
+      solo_unit<Elem, HB, PG, MODE>(a, u, q_row, u.tb, u.te, d, lane, u.tb == first_tile, first0,
+                                    first1);
     return;
   }
 
@@ -1305,7 +1337,7 @@ void decode_kernel(DecodeArgs a) {
     __syncthreads();
   }
   u32x4 qf[HB][4];
-  load_q<HB>(a, u.row, qh0, lane, qf);
+  load_q<HB>(a, q_row, qh0, lane, qf);
   WaveState<HB> st;
   init_state<HB>(st);
 
