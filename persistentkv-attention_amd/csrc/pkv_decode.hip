@@ -153,13 +153,15 @@ __device__ inline void* uniform_ptr(const void* p) {
   return (void*)(((uint64_t)hi << 32) | lo);
 }
 
-__device__ inline int row_length(const DecodeArgs& a, int row) {
-  int len = a.seq_lens ? a.seq_lens[row] : a.context;
-  // The reference trusts seq_lens (cuh:217-219); clamping to the table width keeps
-  // every page lookup inside the row for any input.
+// A row length as the kernels use it.  The reference trusts seq_lens (cuh:217-219);
+// clamping to the table width keeps every page lookup inside the row for any input.
+__device__ inline int clamp_length(const DecodeArgs& a, int len) {
   const long cap = (long)a.max_pages * a.page_size;
   if (len > cap) len = (int)cap;
   return len < 0 ? 0 : len;
+}
+__device__ inline int row_length(const DecodeArgs& a, int row) {
+  return clamp_length(a, a.seq_lens ? a.seq_lens[row] : a.context);
 }
 
 __device__ inline int clamp_page(const DecodeArgs& a, int page) {
@@ -219,6 +221,15 @@ __device__ inline int load_vector_deferred(const int32_t* p) {
   const __amdgpu_buffer_rsrc_t r =
       __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(p), (short)0, p ? 4 : 0, kRsrcWord3);
   return (int)__builtin_amdgcn_raw_buffer_load_b32(r, 0, 0, 0);
+}
+// load_vector_deferred whose result the compiler must treat as per-lane, so it is not
+// copied to an SGPR (and waited for) at once: its offset is `lane_zero`, a per-lane value
+// that is 0 at run time but not provably so.
+__device__ inline int load_vector_lanes(const int32_t* p, int lane_zero) {
+  const int zero = lane_zero;
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(p), (short)0, p ? 4 : 0, kRsrcWord3);
+  return (int)__builtin_amdgcn_raw_buffer_load_b32(r, zero, 0, 0);
 }
 
 // ---------------------------------------------------------------------------------
@@ -664,10 +675,7 @@ __device__ inline Unit queue_unit(const DecodeArgs& a, int row, int kvh, int spl
     u.valid = false;
     return u;
   }
-  // The reference trusts seq_lens (cuh:217-219); clamping to the table width keeps every
-  // page lookup inside the row for any input.
-  const long cap = (long)a.max_pages * a.page_size;
-  u.len = len > cap ? (int)cap : (len < 0 ? 0 : len);
+  u.len = clamp_length(a, len);
   u.slot_base = so0;
   u.row_splits = so1 - so0;
   const int total = ceil_tiles(u.len);
@@ -955,10 +963,15 @@ __device__ inline void unit_states(const DecodeArgs& a, const Unit& u, int qh0, 
   }
 }
 
-// Q^T operand: lane (g, c) holds head hb*16 + c, dims 32kk + 8g .. +8.
+// Q^T operand: lane (g, c) holds head hb*16 + c, dims 32kk + 8g .. +8.  The query row is
+// `row`, or `q_loaded` (q_indices[row], the same in every lane) when q_indices is set.
+// q_loaded may still be in flight: the address is formed per lane, so its wait falls
+// right before the Q loads.
 template <int HB>
-__device__ inline void load_q(const DecodeArgs& a, int q_row, int qh0, int lane, u32x4 (&qf)[HB][4]) {
+__device__ inline void load_q(const DecodeArgs& a, int q_loaded, int row, int qh0, int lane,
+                              u32x4 (&qf)[HB][4]) {
   const int c = lane & 15, g = lane >> 4;
+  int q_row = a.q_indices ? q_loaded : row;
   q_row = q_row < 0 ? 0 : (q_row >= a.q_rows ? a.q_rows - 1 : q_row);
 #pragma unroll
   for (int hb = 0; hb < HB; ++hb) {
@@ -1244,12 +1257,12 @@ __device__ inline bool combine_async(const DecodeArgs& a, const WaveState<HB>& s
 constexpr int kSoloTiles = 2;
 
 template <class Elem, int HB, int PG, int MODE>
-__device__ void solo_unit(const DecodeArgs& a, const Unit& u, int q_row, int t0, int t1,
+__device__ void solo_unit(const DecodeArgs& a, const Unit& u, int q_loaded, int t0, int t1,
                           const Dest& d, int lane, bool have_first, FastPager::Pages f0,
                           FastPager::Pages f1) {
   const int qh0 = u.kvh * a.group;
   u32x4 qf[HB][4];
-  load_q<HB>(a, q_row, qh0, lane, qf);
+  load_q<HB>(a, q_loaded, u.row, qh0, lane, qf);
   WaveState<HB> st;
   init_state<HB>(st);
   stream_unit<Elem, HB, PG>(a, st, qf, u.row, u.kvh, t0, t1, u.len, lane, have_first, f0, f1);
@@ -1286,7 +1299,7 @@ void decode_kernel(DecodeArgs a) {
   FastPager::Pages first0 = {}, first1 = {};
   int first_tile = -1;
   Unit u;
-  int q_row;
+  int q_loaded = 0;  // q_indices[row] when q_indices is set, left in a VGPR (see load_q)
   if constexpr (MODE == kQueue && (PG == kPgFast || PG == kPgFp8)) {
     const int32_t* w = a.work_items + (long)blockIdx.x * 5;
     const int row = load_scalar(w + 0), kvh = load_scalar(w + 1), split = load_scalar(w + 2);
@@ -1303,12 +1316,17 @@ void decode_kernel(DecodeArgs a) {
     first0 = pg.lookup(first_tile);
     first1 = pg.lookup(first_tile + 1);
     u = queue_unit(a, row, kvh, split, tb, te, uniform(len_l), uniform(so0_l), uniform(so1_l));
-    q_row = a.q_indices ? uniform(qi_l) : row;
+    q_loaded = uniform(qi_l);
+  } else if constexpr (MODE != kQueue) {
+    // The row follows from the workgroup index: its query row is requested (vector load,
+    // waited for only by the Q loads) before its length (scalar load) is read.
+    const int row = MODE == kDirect ? (int)blockIdx.x / a.hkv : (int)blockIdx.x / (a.hkv * a.num_splits);
+    q_loaded = load_vector_lanes(a.q_indices ? a.q_indices + row : nullptr,
+                                 a.batch < 0 ? lane : 0);  // batch >= 0 (checked on the host)
+    u = resolve_unit<MODE>(a, blockIdx.x);
   } else {
     u = resolve_unit<MODE>(a, blockIdx.x);
-    // The query row needs only the unit's row: load it alongside the unit's metadata.
-    q_row = u.row;
-    if (a.q_indices && u.valid) q_row = uniform(load_vector_deferred(a.q_indices + u.row));
+    if (a.q_indices && u.valid) q_loaded = a.q_indices[u.row];
   }
   if (!u.valid) return;
   const int qh0 = u.kvh * G;
@@ -1327,7 +1345,7 @@ void decode_kernel(DecodeArgs a) {
   const int n = u.te - u.tb;
   if (n <= kSoloTiles) {
     if (wave == 0)
-      solo_unit<Elem, HB, PG, MODE>(a, u, q_row, u.tb, u.te, d, lane, u.tb == first_tile, first0,
+      solo_unit<Elem, HB, PG, MODE>(a, u, q_loaded, u.tb, u.te, d, lane, u.tb == first_tile, first0,
                                     first1);
     return;
   }
@@ -1337,7 +1355,7 @@ void decode_kernel(DecodeArgs a) {
     __syncthreads();
   }
   u32x4 qf[HB][4];
-  load_q<HB>(a, q_row, qh0, lane, qf);
+  load_q<HB>(a, q_loaded, u.row, qh0, lane, qf);
   WaveState<HB> st;
   init_state<HB>(st);
 
