@@ -182,6 +182,50 @@ def test_paged_attention_workqueue(ext, gpu, lengths, hq, hkv, ps, req, auto, dt
     assert int(counters.abs().sum()) == 0  # the fused merge leaves the counters at zero
 
 
+def _with_row_splits(case, meta, row_splits, hkv):
+    """Work items and split_offsets for per-row split counts (the builder's emission
+    order: row, then split, then kv head; empty splits counted in split_offsets)."""
+    items, offsets = [], [0]
+    for r, (length, splits) in enumerate(zip(meta["seq_lens"], row_splits)):
+        tiles = -(-int(length) // 32)
+        for s in range(splits):
+            tb, te = tiles * s // splits, tiles * (s + 1) // splits
+            if te > tb:
+                items += [[r, k, s, tb, te] for k in range(hkv)]
+        offsets.append(offsets[-1] + splits)
+    return dict(meta, work_items=items, split_offsets=offsets, total_partial_slots=offsets[-1])
+
+
+# (lengths, per-row split counts): the merge guesses a row's slot range as
+# [row * S, row * S + S) when every row could have S = total_slots / batch slots.
+ROW_SPLITS = [
+    ([900, 1500], [3, 1]),               # total divisible by the batch, guess wrong
+    ([700, 300, 2500], [2, 2, 5]),       # divisible, wrong for every row
+    ([1200, 800], [4, 4]),               # uniform: guess right
+    ([3000, 2000], [40, 40]),            # uniform, more than one 32-slot chunk
+    ([3000, 1600], [40, 24]),            # divisible (32 per row), wrong, 40 > 32
+    ([1100, 1000], [33, 31]),            # divisible, wrong by one slot
+    ([500, 60, 90], [1, 1, 1]),          # one slot per row
+    ([400, 2000, 30], [2, 7, 1]),        # total not divisible: no guess
+]
+
+
+@pytest.mark.parametrize("lengths,row_splits", ROW_SPLITS)
+def test_workqueue_per_row_split_counts(ext, gpu, lengths, row_splits):
+    """Merges of rows whose split counts differ, including totals that make the merge's
+    fixed-split guess of the slot range look possible but wrong."""
+    case = make_case(lengths, 32, 8, 16, F16, seed=sum(row_splits), q_rows=len(lengths) + 1)
+    ids = [len(lengths) - i for i in range(len(lengths))]
+    meta = _with_row_splits(case, _queue(case, 1, False, 8, request_ids=ids), row_splits, 8)
+    unfused, _ = _run_queue(ext, gpu, case, meta, 32, 8, False)
+    fused, counters = _run_queue(ext, gpu, case, meta, 32, 8, True)
+    ref = oracle.paged_decode(case.q, case.k_pages, case.v_pages, meta["block_table"],
+                              meta["seq_lens"], meta["q_indices"], meta["out_indices"])
+    assert_parity(unfused, ref)
+    assert torch.equal(unfused, fused)  # same states, same fold order in both merges
+    assert int(counters.abs().sum()) == 0
+
+
 def test_workqueue_mi355x_policy(ext, gpu):
     lengths = [300, 17000, 700, 256, 31000, 900, 512, 640]
     case = make_case(lengths, 32, 8, 16, F16, seed=99)
