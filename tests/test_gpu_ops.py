@@ -48,6 +48,10 @@ PAGED = [
     (2, 48, 2, 600, 16, 3, BF16, "reversed"),    # G = 24
     (2, 40, 2, 333, 8, 1, F16, "random"),        # G = 20, page 8 (generic pager)
     (1, 27, 1, 300, 16, 2, F16, "random"),       # G = 27
+    (2, 32, 8, 3000, 256, 4, F16, "random"),     # page 256
+    (1, 32, 2, 131072, 16, 64, BF16, "random"),  # 128k-token row, G = 16
+    (2, 64, 8, 1500, 16, 3, F16, "reversed"),    # Hq = 64, G = 8
+    (1, 64, 2, 900, 32, 1, BF16, "random"),      # Hq = 64, G = 32, direct
 ]
 
 
@@ -71,6 +75,7 @@ MASKED = [
     ([300, 17], 32, 4, 8, 3, F16),
     ([0, 45, 96], 32, 8, 16, 2, F16),            # empty row -> zeros
     ([1024, 7000, 333], 32, 1, 32, 12, BF16),
+    ([1 + (37 * i * i + 11 * i) % 600 for i in range(256)], 32, 8, 16, 2, F16),  # 256 rows
 ]
 
 
