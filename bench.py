@@ -233,8 +233,10 @@ def main():
     kernel = {"paged_attention_workqueue": "decode_kernel<*,kQueue> (stage 1 only)",
               "paged_attention_indexed": "decode_kernel<*,kSplit> + merge_kernel (whole op)",
               "paged_attention_masked": "decode_kernel<*,kSplit> + merge_kernel (whole op)",
-              "paged_attention": "decode_kernel<*,kDirect> (whole op)",
-              "attention_contiguous": "decode_kernel<*,kDirect> (whole op)"}[w.op]
+              "paged_attention": "decode_kernel<*,kDirect> (whole op; split internally into "
+                                 "decode_kernel<*,kSplit> + merge_kernel when few units)",
+              "attention_contiguous": "decode_kernel<*,kDirect> (whole op; split internally into "
+                                      "decode_kernel<*,kSplit> + merge_kernel when few units)"}[w.op]
     if w.op in ("paged_attention", "attention_contiguous") and w.splits > 1:
         kernel = "decode_kernel<*,kSplit> + merge_kernel (whole op)"
     result = {
