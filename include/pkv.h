@@ -320,6 +320,32 @@ int pkv_build_workqueue(
     int32_t* split_offsets, int32_t* out_total_partial_slots);
 
 /* ---------------------------------------------------------------------------------
+ * KV-cache append: the write of each row's newest token before its decode step.
+ * No counterpart in the reference, whose harness grows the lengths without writing K/V
+ * (tests/benchmark_serving_trace.py:285-298); fused KV-cache writes are future work in
+ * paper/persistentkv_mlsys_workshop.tex:689.
+ * ------------------------------------------------------------------------------- */
+
+/* Writes k_new[b] and v_new[b] ([num_kv_heads, 128] each, dtype f16 or bf16, batch rows)
+ * into the pools ([num_pages, num_kv_heads, page_size, 128], same dtype) at token position
+ * seq_lens[b] - 1: page block_table[b * max_pages + pos / page_size], slot
+ * pos % page_size.  Rows with seq_lens[b] <= 0, a position past the table, or a page id
+ * outside [0, num_pages) are skipped.  Asynchronous on `stream`. */
+int pkv_append_kv(const void* k_new, const void* v_new, void* k_pages, void* v_pages,
+                  const int32_t* block_table, const int32_t* seq_lens, int32_t batch,
+                  int32_t num_kv_heads, int32_t head_dim, int32_t num_pages, int32_t page_size,
+                  int32_t max_pages, int32_t dtype, void* stream);
+
+/* pkv_append_kv into fp8 (OCP e4m3) pools: each element is stored as
+ * e4m3(clamp(x / scale, -448, 448)), rounded to nearest even (torch's float8_e4m3fn cast),
+ * with k_scale for K and v_scale for V.  `dtype` is that of k_new and v_new. */
+int pkv_append_kv_fp8(const void* k_new, const void* v_new, void* k_pages, void* v_pages,
+                      const int32_t* block_table, const int32_t* seq_lens, int32_t batch,
+                      int32_t num_kv_heads, int32_t head_dim, int32_t num_pages,
+                      int32_t page_size, int32_t max_pages, float k_scale, float v_scale,
+                      int32_t dtype, void* stream);
+
+/* ---------------------------------------------------------------------------------
  * HBM calibration probes (counterparts of the reference's
  * micro_benchmarks/01_hbm_bandwidth.cu:20-51 read/copy kernels).
  * ------------------------------------------------------------------------------- */

@@ -173,3 +173,52 @@ def dequantize_e4m3(pages, scale):
     ``uint8``)."""
     codes = _cpu(pages).contiguous().view(torch.uint8).numpy()
     return torch.from_numpy(E4M3_TABLE[codes] * np.float32(scale))
+
+
+# Positive finite e4m3 codes 0x00..0x7e in increasing value (the format is monotone over
+# them), for the nearest-value search below.
+_E4M3_POS_CODES = np.arange(0x7F, dtype=np.int64)
+_E4M3_POS_VALUES = E4M3_TABLE[:0x7F].astype(np.float64)
+
+
+def quantize_e4m3(x, scale):
+    """e4m3 bytes (uint8 numpy array) of ``clamp(x / scale, -448, 448)`` rounded to the
+    nearest representable value, ties to the even code: the conversion the fp8 K/V
+    producers use (torch's ``float8_e4m3fn`` cast after the clamp).  The quotient is taken
+    in fp32.  NaN keeps its sign (0x7f, 0xff).  The reference has no fp8 path.
+
+    Found by searching the decoded value table rather than by bit manipulation, so the
+    check of a bit-level encoder against it is independent."""
+    with np.errstate(over="ignore", invalid="ignore"):
+        y = np.asarray(x, dtype=np.float32) / np.float32(scale)
+    sign = np.signbit(y).astype(np.uint8) << 7
+    a = np.minimum(np.abs(y).astype(np.float64), 448.0)
+    hi = np.clip(np.searchsorted(_E4M3_POS_VALUES, a, side="left"), 0, 0x7E)
+    lo = np.clip(hi - 1, 0, 0x7E)
+    d_lo, d_hi = a - _E4M3_POS_VALUES[lo], _E4M3_POS_VALUES[hi] - a
+    pick_hi = (d_hi < d_lo) | ((d_hi == d_lo) & (_E4M3_POS_CODES[hi] % 2 == 0))
+    code = np.where(pick_hi, _E4M3_POS_CODES[hi], _E4M3_POS_CODES[lo]).astype(np.uint8)
+    code = np.where(np.isnan(y), np.uint8(0x7F), code)
+    return code | sign
+
+
+def append_kv(k_pages, v_pages, block_table, seq_lens, k_new, v_new):
+    """Pools after each row's newest token is written to its tail page: row b's
+    ``k_new[b], v_new[b]`` ([Hkv, 128]) go to token position ``seq_lens[b] - 1``, i.e. page
+    ``block_table[b, pos // ps]``, slot ``pos % ps`` of the [pages, Hkv, ps, 128] pools.
+    Rows with no tokens, or whose position falls outside the table or whose page falls
+    outside the pool, are left alone.  (The reference's harness grows lengths without
+    writing K/V, benchmark_serving_trace.py:285-298; this is the write a serving loop
+    makes before the decode step.)  Returns new CPU tensors."""
+    k_out, v_out = _cpu(k_pages).clone(), _cpu(v_pages).clone()
+    table = _cpu(block_table)
+    ps, pages = k_out.shape[2], k_out.shape[0]
+    for b, length in enumerate(_cpu(seq_lens).tolist()):
+        pos = int(length) - 1
+        if pos < 0 or pos // ps >= table.shape[1]:
+            continue
+        page = int(table[b, pos // ps])
+        if 0 <= page < pages:
+            k_out[page, :, pos % ps] = _cpu(k_new)[b].to(k_out.dtype)
+            v_out[page, :, pos % ps] = _cpu(v_new)[b].to(v_out.dtype)
+    return k_out, v_out

@@ -7,8 +7,9 @@
 //   * G = Hq / Hkv may be any integer in [1, 32] (the reference accepts {1, 2, 4, 8});
 //   * launch failures raise RuntimeError instead of terminating the process.
 // Beyond the reference's four ops: the two work-queue stages, fp8 (float8_e4m3fn) K/V
-// variants of the indexed and work-queue ops, and the contiguous-layout decode and
-// query-head baseline of its C++ API (cuh:1077-1108, :1263-1282).
+// variants of the indexed and work-queue ops, the contiguous-layout decode and
+// query-head baseline of its C++ API (cuh:1077-1108, :1263-1282), and the KV-cache append
+// (fp16 / bf16 / fp8 pools) that a serving loop runs before each decode step.
 // Work is enqueued on the current HIP stream of the tensors' device without a host sync,
 // so the ops can be captured in HIP graphs.
 
@@ -472,6 +473,57 @@ void persistentkv_attention_query_head_baseline(torch::Tensor q, torch::Tensor k
                                              pkv_dtype_of(t.dt), stream_of(q)));
 }
 
+namespace {
+
+// KV-cache append (no counterpart in the reference): row b's k_new[b], v_new[b]
+// ([Hkv, 128]) go to token position seq_lens[b] - 1 of its block-table row.
+void append_op(const torch::Tensor& k_new, const torch::Tensor& v_new, torch::Tensor& k_pages,
+               torch::Tensor& v_pages, const torch::Tensor& block_table,
+               const torch::Tensor& seq_lens, bool kv_fp8, double k_scale, double v_scale) {
+  const auto dt = activation_dtype(k_new, "k_new");
+  check_tensor(k_new, "k_new", dt, 3);
+  check_tensor(v_new, "v_new", dt, 3);
+  const auto kv_dt = kv_fp8 ? at::kFloat8_e4m3fn : dt;
+  check_tensor(k_pages, "k_pages", kv_dt, 4);
+  check_tensor(v_pages, "v_pages", kv_dt, 4);
+  check_tensor(block_table, "block_table", at::kInt, 2);
+  check_tensor(seq_lens, "seq_lens", at::kInt, 1);
+  const int64_t B = k_new.size(0), Hkv = k_new.size(1);
+  TORCH_CHECK(k_new.size(2) == PKV_HEAD_DIM, "PersistentKV extension currently requires d=128");
+  TORCH_CHECK(v_new.sizes() == k_new.sizes(), "v_new shape mismatch");
+  TORCH_CHECK(k_pages.size(1) == Hkv, "k_pages Hkv mismatch");
+  check_pages(k_pages, v_pages, k_pages.size(2), PKV_HEAD_DIM);
+  TORCH_CHECK(block_table.size(0) == B && seq_lens.size(0) == B, "batch size mismatch");
+  const c10::DeviceGuard guard(k_pages.device());
+  const int32_t batch = i32(B, "k_new.size(0)"), hkv = i32(Hkv, "Hkv");
+  const int32_t pages = i32(k_pages.size(0), "k_pages.size(0)");
+  const int32_t ps = i32(k_pages.size(2), "page_size"), cols = i32(block_table.size(1), "max_pages");
+  if (kv_fp8)
+    raise_on(pkv_append_kv_fp8(k_new.data_ptr(), v_new.data_ptr(), k_pages.data_ptr(),
+                               v_pages.data_ptr(), block_table.data_ptr<int>(),
+                               seq_lens.data_ptr<int>(), batch, hkv, PKV_HEAD_DIM, pages, ps, cols,
+                               (float)k_scale, (float)v_scale, pkv_dtype_of(dt), stream_of(k_pages)));
+  else
+    raise_on(pkv_append_kv(k_new.data_ptr(), v_new.data_ptr(), k_pages.data_ptr(),
+                           v_pages.data_ptr(), block_table.data_ptr<int>(), seq_lens.data_ptr<int>(),
+                           batch, hkv, PKV_HEAD_DIM, pages, ps, cols, pkv_dtype_of(dt),
+                           stream_of(k_pages)));
+}
+
+}  // namespace
+
+void persistentkv_append_kv(torch::Tensor k_new, torch::Tensor v_new, torch::Tensor k_pages,
+                            torch::Tensor v_pages, torch::Tensor block_table,
+                            torch::Tensor seq_lens) {
+  append_op(k_new, v_new, k_pages, v_pages, block_table, seq_lens, false, 1.0, 1.0);
+}
+
+void persistentkv_append_kv_fp8(torch::Tensor k_new, torch::Tensor v_new, torch::Tensor k_pages,
+                                torch::Tensor v_pages, torch::Tensor block_table,
+                                torch::Tensor seq_lens, double k_scale, double v_scale) {
+  append_op(k_new, v_new, k_pages, v_pages, block_table, seq_lens, true, k_scale, v_scale);
+}
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("paged_attention", &persistentkv_paged_attention, "PersistentKV native paged attention");
   m.def("paged_attention_masked", &persistentkv_paged_attention_masked,
@@ -492,6 +544,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "Work-queue decode stage over fp8 (e4m3) K/V pages");
   m.def("attention_contiguous", &persistentkv_attention_contiguous,
         "GQA decode over contiguous K/V [B, Hkv, N, 128]");
+  m.def("append_kv", &persistentkv_append_kv,
+        "write each row's newest token's K/V into its tail page (position seq_lens - 1)");
+  m.def("append_kv_fp8", &persistentkv_append_kv_fp8,
+        "append_kv into float8_e4m3fn pools, quantising x / scale with round-to-nearest-even");
   m.def("attention_query_head_baseline", &persistentkv_attention_query_head_baseline,
         "Query-head baseline over contiguous K/V (each query head streams its KV head)");
 }

@@ -51,6 +51,10 @@ workqueue_decode_fp8 = _ext.workqueue_decode_fp8
 # Contiguous K/V [B, Hkv, N, 128] (the reference's C++ entry points, cuh:1077-1108, 1263-1282).
 attention_contiguous = _ext.attention_contiguous
 attention_query_head_baseline = _ext.attention_query_head_baseline
+# KV-cache append: k_new / v_new [B, Hkv, 128] to position seq_lens[b] - 1 of each row
+# (fp8 pools store e4m3(x / scale), rounded to nearest even).
+append_kv = _ext.append_kv
+append_kv_fp8 = _ext.append_kv_fp8
 
 HEAD_DIM = 128
 TILE_TOKENS = 32
@@ -71,6 +75,6 @@ __all__ = [
     "paged_attention_workqueue", "workqueue_decode", "workqueue_merge",
     "paged_attention_indexed_fp8", "paged_attention_workqueue_fp8", "workqueue_decode_fp8",
     "attention_contiguous",
-    "attention_query_head_baseline", "workspace_floats",
+    "attention_query_head_baseline", "append_kv", "append_kv_fp8", "workspace_floats",
     "workqueue_workspace_floats", "EXTENSION_PATH", "LIBRARY_PATH",
 ]

@@ -443,9 +443,38 @@ def run_step(ext, w: Workload, meta: StepMeta, step_index: int, q_pool, k_pages,
     return meta.output
 
 
+def new_token_kv(w: Workload, step_index: int, seed_offset=11):
+    """K and V ``[active rows, Hkv, 128]`` of each active row's newest token at a step,
+    drawn on the CPU from ``seed + seed_offset + step`` (row by row, K then V), in the
+    workload's dtype."""
+    st = w.steps[step_index]
+    gen = torch.Generator().manual_seed(w.seed + seed_offset + step_index)
+    ks, vs = [], []
+    for _ in st.active_ids:
+        ks.append(torch.randn(w.hkv, HEAD_DIM, generator=gen).to(w.dtype))
+        vs.append(torch.randn(w.hkv, HEAD_DIM, generator=gen).to(w.dtype))
+    return torch.stack(ks), torch.stack(vs)
+
+
+def append_step_kv_native(w: Workload, step_index: int, k_pages, v_pages, meta, ext,
+                          new_kv=None, seed_offset=11):
+    """append_step_kv on the GPU: one ``append_kv`` (``append_kv_fp8`` for fp8 pools)
+    launch over the step's rows, using the step's compiled block table and lengths.
+    ``new_kv`` is the step's (K, V) already on the device (new_token_kv otherwise)."""
+    if new_kv is None:
+        new_kv = tuple(t.to(k_pages.device) for t in new_token_kv(w, step_index, seed_offset))
+    k_new, v_new = new_kv
+    if w.kv_fp8:
+        ext.append_kv_fp8(k_new, v_new, k_pages, v_pages, meta.block_table, meta.seq_lens,
+                          w.k_scale, w.v_scale)
+    else:
+        ext.append_kv(k_new, v_new, k_pages, v_pages, meta.block_table, meta.seq_lens)
+
+
 def append_step_kv(w: Workload, step_index: int, k_pages, v_pages, seed_offset=11):
     """Writes the K/V of each active row's newest token (position length - 1) into its
-    tail page, with values drawn from ``seed + seed_offset + step``."""
+    tail page, with values drawn from ``seed + seed_offset + step``: the host-side
+    restatement of append_step_kv_native (one indexed write per row)."""
     st = w.steps[step_index]
     by_id = {r.request_id: r for r in w.requests}
     gen = torch.Generator().manual_seed(w.seed + seed_offset + step_index)

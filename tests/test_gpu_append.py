@@ -1,0 +1,144 @@
+"""KV-cache append (append_kv / append_kv_fp8) against the oracle's restatement.
+
+The pools after the op must equal oracle.append_kv bit for bit: a copy for fp16 / bf16
+pools, and for fp8 pools the bytes of oracle.quantize_e4m3 (itself pinned against torch's
+float8_e4m3fn cast on every 16-bit input, tests/test_oracle_fp8.py).  Cases cover
+positions at both ends of a page, rows that must be skipped (no tokens, a position past
+the table, a page id outside the pool), every fp16 bit pattern through the fp8 encoder,
+and decoding after the append.
+"""
+import pytest
+import torch
+
+from oracle import attention as oracle
+from paged_cases import assert_parity, make_case
+
+pytestmark = pytest.mark.gpu
+
+F16, BF16, F8 = torch.float16, torch.bfloat16, torch.float8_e4m3fn
+
+
+def _pools(pages, hkv, ps, dtype, seed):
+    gen = torch.Generator().manual_seed(seed)
+    k = torch.randn(pages, hkv, ps, 128, generator=gen)
+    v = torch.randn(pages, hkv, ps, 128, generator=gen)
+    if dtype == F8:
+        return (k / 0.05).clamp(-448, 448).to(F8), (v / 0.05).clamp(-448, 448).to(F8)
+    return k.to(dtype), v.to(dtype)
+
+
+# rows: (seq_len, block-table row); the pool has 12 pages
+ROWS = [
+    (1, [3, 0, 0]),        # first slot of the first page
+    (16, [5, 7, 0]),       # last slot of page 0 (page size 16)
+    (17, [1, 2, 0]),       # first slot of the second page
+    (40, [9, 10, 11]),     # last page of the table
+    (0, [4, 4, 4]),        # no tokens: skipped
+    (49, [6, 6, 6]),       # position 48 is past the 3-column table: skipped
+    (20, [8, -1, 0]),      # page id -1: skipped
+    (33, [0, 2, 12]),      # page id 12 is outside the pool: skipped
+]
+
+
+@pytest.mark.parametrize("dtype", [F16, BF16])
+def test_append_matches_oracle(ext, gpu, dtype):
+    ps, hkv, pages = 16, 4, 12
+    k, v = _pools(pages, hkv, ps, dtype, seed=1)
+    table = torch.tensor([r for _, r in ROWS], dtype=torch.int32)
+    lens = torch.tensor([n for n, _ in ROWS], dtype=torch.int32)
+    gen = torch.Generator().manual_seed(2)
+    kn = torch.randn(len(ROWS), hkv, 128, generator=gen).to(dtype)
+    vn = torch.randn(len(ROWS), hkv, 128, generator=gen).to(dtype)
+    kg, vg = k.to(gpu), v.to(gpu)
+    ext.append_kv(kn.to(gpu), vn.to(gpu), kg, vg, table.to(gpu), lens.to(gpu))
+    torch.cuda.synchronize()
+    k_ref, v_ref = oracle.append_kv(k, v, table, lens, kn, vn)
+    assert torch.equal(kg.cpu(), k_ref) and torch.equal(vg.cpu(), v_ref)
+    assert not torch.equal(k_ref, k)  # something was written
+
+
+@pytest.mark.parametrize("in_dtype", [F16, BF16])
+@pytest.mark.parametrize("ks,vs", [(0.05, 0.02), (1.0, 1.0 / 448)])
+def test_append_fp8_matches_oracle(ext, gpu, in_dtype, ks, vs):
+    ps, hkv, pages = 16, 4, 12
+    k8, v8 = _pools(pages, hkv, ps, F8, seed=3)
+    table = torch.tensor([r for _, r in ROWS], dtype=torch.int32)
+    lens = torch.tensor([n for n, _ in ROWS], dtype=torch.int32)
+    gen = torch.Generator().manual_seed(4)
+    kn = (torch.randn(len(ROWS), hkv, 128, generator=gen) * 8).to(in_dtype)
+    vn = (torch.randn(len(ROWS), hkv, 128, generator=gen) * 8).to(in_dtype)
+    kn[0, 0, :4] = torch.tensor([0.0, -0.0, 1e4, -1e4]).to(in_dtype)  # signed zeros, saturation
+    kg, vg = k8.to(gpu), v8.to(gpu)
+    ext.append_kv_fp8(kn.to(gpu), vn.to(gpu), kg, vg, table.to(gpu), lens.to(gpu), ks, vs)
+    torch.cuda.synchronize()
+    kq = torch.from_numpy(oracle.quantize_e4m3(kn.float().numpy(), ks)).view(F8)
+    vq = torch.from_numpy(oracle.quantize_e4m3(vn.float().numpy(), vs)).view(F8)
+    k_ref, v_ref = oracle.append_kv(k8, v8, table, lens, kq, vq)
+    assert torch.equal(kg.cpu().view(torch.uint8), k_ref.view(torch.uint8))
+    assert torch.equal(vg.cpu().view(torch.uint8), v_ref.view(torch.uint8))
+
+
+@pytest.mark.parametrize("scale", [1.0, 1.0 / 64])
+def test_append_fp8_every_fp16_code(ext, gpu, scale):
+    """All 65536 fp16 bit patterns (NaNs, infinities, subnormals, ties) through the
+    kernel's e4m3 encoder: 64 rows x 8 KV heads x 128 dims, each row to its own page."""
+    rows, hkv, ps = 64, 8, 16
+    codes = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(F16)
+    kn = codes.view(rows, hkv, 128)
+    vn = codes.flip(0).view(rows, hkv, 128)
+    k8 = torch.zeros(rows, hkv, ps, 128, dtype=torch.uint8).view(F8)
+    v8 = torch.zeros_like(k8)
+    table = torch.arange(rows, dtype=torch.int32).view(rows, 1)
+    lens = torch.full((rows,), 5, dtype=torch.int32)  # slot 4 of each row's page
+    kg, vg = k8.to(gpu), v8.to(gpu)
+    ext.append_kv_fp8(kn.to(gpu), vn.to(gpu), kg, vg, table.to(gpu), lens.to(gpu), scale, scale)
+    torch.cuda.synchronize()
+    got_k = kg.cpu().view(torch.uint8)[:, :, 4].reshape(-1).numpy()
+    got_v = vg.cpu().view(torch.uint8)[:, :, 4].reshape(-1).numpy()
+    want_k = oracle.quantize_e4m3(kn.float().reshape(-1).numpy(), scale)
+    want_v = oracle.quantize_e4m3(vn.float().reshape(-1).numpy(), scale)
+    assert (got_k == want_k).all() and (got_v == want_v).all()
+    assert int(kg.cpu().view(torch.uint8)[:, :, :4].abs().sum()) == 0  # other slots untouched
+
+
+@pytest.mark.parametrize("dtype,ps", [(F16, 16), (BF16, 32), (F16, 5)])
+def test_decode_after_append(ext, gpu, dtype, ps):
+    """Append one token to each row, then the masked op attends to the grown rows."""
+    lengths = [300, 17, 64, 1]
+    case = make_case([n + 1 for n in lengths], 32, 8, ps, dtype, seed=ps)
+    gen = torch.Generator().manual_seed(9)
+    kn = torch.randn(len(lengths), 8, 128, generator=gen).to(dtype)
+    vn = torch.randn(len(lengths), 8, 128, generator=gen).to(dtype)
+    k, v = case.k_pages.to(gpu), case.v_pages.to(gpu)
+    bt, sl = case.block_table.to(gpu), case.seq_lens.to(gpu)
+    ext.append_kv(kn.to(gpu), vn.to(gpu), k, v, bt, sl)
+    out = torch.full((len(lengths), 32, 128), float("nan"), dtype=dtype, device=gpu)
+    ws = torch.empty(len(lengths) * 32 * 2 * 130, dtype=torch.float32, device=gpu)
+    bucket = max(case.seq_lens.tolist())
+    ext.paged_attention_masked(case.q.to(gpu), k, v, bt, sl, out, ws, bucket, ps, 2)
+    torch.cuda.synchronize()
+    k_ref, v_ref = oracle.append_kv(case.k_pages, case.v_pages, case.block_table, case.seq_lens,
+                                    kn, vn)
+    assert torch.equal(k.cpu(), k_ref)
+    ref = oracle.paged_decode(case.q, k_ref, v_ref, case.block_table, case.seq_lens)
+    assert_parity(out, ref)
+
+
+def test_append_validation(ext, gpu):
+    k, v = _pools(4, 2, 16, F16, seed=0)
+    k, v = k.to(gpu), v.to(gpu)
+    kn = torch.zeros(1, 2, 128, dtype=F16, device=gpu)
+    bt = torch.zeros(1, 2, dtype=torch.int32, device=gpu)
+    sl = torch.ones(1, dtype=torch.int32, device=gpu)
+    with pytest.raises(RuntimeError, match="wrong dtype"):
+        ext.append_kv(kn.to(BF16), kn.to(BF16), k, v, bt, sl)
+    with pytest.raises(RuntimeError, match="Hkv mismatch"):
+        ext.append_kv(torch.zeros(1, 3, 128, dtype=F16, device=gpu),
+                      torch.zeros(1, 3, 128, dtype=F16, device=gpu), k, v, bt, sl)
+    with pytest.raises(RuntimeError, match="batch size mismatch"):
+        ext.append_kv(kn, kn, k, v, bt, torch.ones(2, dtype=torch.int32, device=gpu))
+    k8, v8 = _pools(4, 2, 16, F8, seed=0)
+    with pytest.raises(RuntimeError, match="k_scale"):
+        ext.append_kv_fp8(kn, kn, k8.to(gpu), v8.to(gpu), bt, sl, 0.0, 1.0)
+    with pytest.raises(RuntimeError, match="wrong dtype"):
+        ext.append_kv_fp8(kn, kn, k, v, bt, sl, 1.0, 1.0)
