@@ -255,15 +255,13 @@ struct Fp8Tile {
   u32x2 v[8];
 };
 
-// Each pager's issue() fills a Raw tile; unpack() turns it into the MFMA operand layout
-// (the identity for 2-byte K/V).
+// Each pager's issue() fills a Raw tile, which compute_tile reads through tile_k / tile_v
+// (fp8 tiles are unpacked there).
 struct FastPager {
   struct Pages {
     int page[2];  // physical page of each 16-token block (unused when the block is empty)
   };
   using Raw = TileRegs;
-  template <class Elem>
-  __device__ static inline const TileRegs& unpack(const TileRegs& r) { return r; }
   const DecodeArgs& a;
   const int32_t* trow;
   int lim;
@@ -330,8 +328,6 @@ struct FastPager {
 struct ContigPager {
   struct Pages {};
   using Raw = TileRegs;
-  template <class Elem>
-  __device__ static inline const TileRegs& unpack(const TileRegs& r) { return r; }
   const DecodeArgs& a;
   long base;         // byte offset of token 0 of (row, kv head)
   int lim;
@@ -431,18 +427,6 @@ struct Fp8Pager {
       for (int j = 0; j < 4; ++j) r.v[b * 4 + j] = __builtin_amdgcn_raw_buffer_load_b64(rv, voff[b * 4 + j], 0, 0);
     }
   }
-
-  template <class Elem>
-  __device__ static inline TileRegs unpack(const Fp8Tile& r) {
-    TileRegs t;
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) t.k[b][kk] = Elem::unpack8(r.k[b][kk]);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) t.v[j] = Elem::unpack8(r.v[j]);
-    return t;
-  }
 };
 
 struct GenericPager {
@@ -451,8 +435,6 @@ struct GenericPager {
     long v[8];  // byte offset of this lane's V chunk per slot, or -1
   };
   using Raw = TileRegs;
-  template <class Elem>
-  __device__ static inline const TileRegs& unpack(const TileRegs& r) { return r; }
   const DecodeArgs& a;
   const int32_t* trow;
   int lim;
@@ -520,22 +502,39 @@ struct WaveState {
   float l[HB];     // lane-partial sum of exp2(x - m)
 };
 
-template <class Elem, int HB>
-__device__ inline void compute_tile(WaveState<HB>& st, const TileRegs& r,
+// MFMA operands of a tile as loaded: 2-byte K/V as is, fp8 K/V unpacked where used, so
+// that the K half is unpacked for QK and the V half only for PV.
+template <class Elem>
+__device__ inline u32x4 tile_k(const TileRegs& r, int b, int kk) { return r.k[b][kk]; }
+template <class Elem>
+__device__ inline u32x4 tile_v(const TileRegs& r, int j) { return r.v[j]; }
+template <class Elem>
+__device__ inline u32x4 tile_k(const Fp8Tile& r, int b, int kk) { return Elem::unpack8(r.k[b][kk]); }
+template <class Elem>
+__device__ inline u32x4 tile_v(const Fp8Tile& r, int j) { return Elem::unpack8(r.v[j]); }
+
+template <class Elem, int HB, class Tile>
+__device__ inline void compute_tile(WaveState<HB>& st, const Tile& r,
                                     const u32x4 (&qf)[HB][4], int tile, int lim, int lane,
                                     float qk) {
   const int g = lane >> 4;
-  // V transpose: vt[jj] holds, for dim 8c + jj, the 8 tokens of this lane's slots.
+  // V transpose (done before the first PV product): vt[jj] holds, for dim 8c + jj, the 8
+  // tokens of this lane's slots.
   u32x4 vt[8];
+  auto transpose_v = [&]() {
+    u32x4 v[8];
 #pragma unroll
-  for (int jj = 0; jj < 8; ++jj) {
-    const int w = jj >> 1;
+    for (int j = 0; j < 8; ++j) v[j] = tile_v<Elem>(r, j);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t lo = r.v[2 * q][w], hi = r.v[2 * q + 1][w];
-      vt[jj][q] = (jj & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+    for (int jj = 0; jj < 8; ++jj) {
+      const int w = jj >> 1;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t lo = v[2 * q][w], hi = v[2 * q + 1][w];
+        vt[jj][q] = (jj & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+      }
     }
-  }
+  };
   const int tok_base = tile * kTile + 4 * g;
   const bool partial = (tile + 1) * kTile > lim;  // wave-uniform
 #pragma unroll
@@ -543,8 +542,8 @@ __device__ inline void compute_tile(WaveState<HB>& st, const TileRegs& r,
     f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      s0 = Elem::mma(r.k[0][kk], qf[hb][kk], s0);
-      s1 = Elem::mma(r.k[1][kk], qf[hb][kk], s1);
+      s0 = Elem::mma(tile_k<Elem>(r, 0, kk), qf[hb][kk], s0);
+      s1 = Elem::mma(tile_k<Elem>(r, 1, kk), qf[hb][kk], s1);
     }
     float x[8];
 #pragma unroll
@@ -582,6 +581,7 @@ __device__ inline void compute_tile(WaveState<HB>& st, const TileRegs& r,
       psum += p[j];
     }
     st.l[hb] += psum;
+    if (hb == 0) transpose_v();
 #pragma unroll
     for (int pass = 0; pass < Elem::kPasses; ++pass) {
       u32x4 pa;
@@ -617,7 +617,7 @@ __device__ inline void stream_range_from(WaveState<HB>& st, const Pager& pg,
       pg.issue(t, pa, r);
       pa = pb;
       pb = pg.lookup(t + 2);
-      compute_tile<Elem, HB>(st, Pager::template unpack<Elem>(r), qf, t, lim, lane, qk);
+      compute_tile<Elem, HB>(st, r, qf, t, lim, lane, qk);
     }
   } else {
     // Two head blocks run one wave per SIMD, half the waves of a CU at one block: each
@@ -629,11 +629,11 @@ __device__ inline void stream_range_from(WaveState<HB>& st, const Pager& pg,
     for (int t = t0;; t += 2) {
       pg.issue(t + 1, pb, rb);
       pa = pg.lookup(t + 2);
-      compute_tile<Elem, HB>(st, Pager::template unpack<Elem>(ra), qf, t, lim, lane, qk);
+      compute_tile<Elem, HB>(st, ra, qf, t, lim, lane, qk);
       if (t + 1 >= t1) break;
       pg.issue(t + 2, pa, ra);
       pb = pg.lookup(t + 3);
-      compute_tile<Elem, HB>(st, Pager::template unpack<Elem>(rb), qf, t + 1, lim, lane, qk);
+      compute_tile<Elem, HB>(st, rb, qf, t + 1, lim, lane, qk);
       if (t + 2 >= t1) break;
     }
   }
