@@ -1668,8 +1668,8 @@ StreamScratch* stream_scratch(hipStream_t stream, size_t need) {
   return &table[used++];
 }
 
-// Internal split count for a direct (num_splits == 1) launch.  One workgroup per
-// (row, kv head) streams at most ~37 GB/s (the per-CU load bandwidth of MI355X), so with
+// Internal split count for a direct (num_splits == 1) launch.  One decode workgroup per
+// (row, kv head) streams at most ~37 GB/s (one MI355X CU with 8 waves of one tile each), so with
 // few rows the op is split into about 256 units of at least 4 tiles, merged by the merge
 // kernel from scratch partial states.  PKV_DIRECT_SPLIT=0 keeps the single launch.
 int direct_splits(const Geometry& g, int context) {

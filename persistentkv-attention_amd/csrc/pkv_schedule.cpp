@@ -43,8 +43,8 @@ inline int64_t tiles_of(int64_t length) { return floordiv(length + 31, 32); }
 // load, LDS combine and partial write stay small next to the K/V stream.  Measured on
 // equal-sized items over the C4 and C5 traces: 384 items was the fastest or tied for
 // G <= 16 (C5 G=8: 242 us per step against 250-293 us at 372-496 items; C4 within 1 %),
-// since every item pays a fixed chain of dependent loads and one CU streams at most
-// ~35 GB/s.  G > 16 plans at most one item per CU instead (plan_row_splits).
+// since every item pays a fixed chain of dependent loads and one decode workgroup (8
+// waves, one tile in flight each) streams at most ~35 GB/s.  G > 16 plans at most one item per CU instead (plan_row_splits).
 constexpr int kMiComputeUnits = 256;
 constexpr int kMiTargetItems = kMiComputeUnits * 3 / 2;
 constexpr int kMiMinTilesPerItem = 8;
