@@ -142,3 +142,43 @@ def test_append_validation(ext, gpu):
         ext.append_kv_fp8(kn, kn, k8.to(gpu), v8.to(gpu), bt, sl, 0.0, 1.0)
     with pytest.raises(RuntimeError, match="wrong dtype"):
         ext.append_kv_fp8(kn, kn, k, v, bt, sl, 1.0, 1.0)
+
+
+def test_append_then_decode_in_a_hip_graph(ext, gpu):
+    """append_kv + the masked op captured in one HIP graph and replayed several times,
+    with eager work (pool reset, output clear) between replays: every replay gives the
+    eager result."""
+    lengths = [700, 33, 129]
+    case = make_case(lengths, 32, 8, 16, F16, seed=21)
+    gen = torch.Generator().manual_seed(22)
+    kn = torch.randn(3, 8, 128, generator=gen).to(F16).to(gpu)
+    vn = torch.randn(3, 8, 128, generator=gen).to(F16).to(gpu)
+    k0, v0 = case.k_pages.to(gpu), case.v_pages.to(gpu)
+    k, v = k0.clone(), v0.clone()
+    q, bt, sl = case.q.to(gpu), case.block_table.to(gpu), case.seq_lens.to(gpu)
+    out = torch.zeros(3, 32, 128, dtype=F16, device=gpu)
+    ws = torch.empty(3 * 32 * 4 * 130, dtype=torch.float32, device=gpu)
+
+    def step():
+        ext.append_kv(kn, vn, k, v, bt, sl)
+        ext.paged_attention_masked(q, k, v, bt, sl, out, ws, max(lengths), 16, 4)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.synchronize()
+    eager_out, eager_k = out.clone(), k.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            step()
+    torch.cuda.synchronize()
+    for _ in range(4):
+        k.copy_(k0)
+        v.copy_(v0)
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager_out) and torch.equal(k, eager_k)
