@@ -396,3 +396,32 @@ def test_validation_errors(ext, gpu):
         ext.attention_contiguous(q, kc, kc, out, empty, 2)
     with pytest.raises(RuntimeError, match="v shape mismatch"):
         ext.attention_query_head_baseline(q, kc, kc[:, :, :32].contiguous(), out)
+
+
+@pytest.mark.parametrize("op", ["masked", "indexed"])
+def test_lengths_and_page_ids_outside_the_table_are_clamped(ext, gpu, op):
+    """Inputs the reference would read out of bounds with: a length past the table's
+    capacity is clamped to max_pages * page_size, a negative length counts as 0 (zeros),
+    and a page id outside the pool is clamped into it (-7 -> 0, 10**6 -> pages - 1).  The
+    expected result is the oracle on the same inputs with those rules applied on the host."""
+    lengths = [100, 64, 40, 77]
+    case = make_case(lengths, 32, 8, 16, F16, seed=31)
+    pages, cols = case.k_pages.shape[0], case.block_table.shape[1]
+    bt = case.block_table.clone()
+    bt[1, 1], bt[1, 2] = -7, 10 ** 6
+    sl = torch.tensor([100 + 500, 64, 40, -5], dtype=torch.int32)
+    bt_ref = bt.clamp(0, pages - 1)
+    sl_ref = sl.clamp(0, cols * 16)
+    ref = oracle.paged_decode(case.q, case.k_pages, case.v_pages, bt_ref, sl_ref)
+    q, k, v = case.q.to(gpu), case.k_pages.to(gpu), case.v_pages.to(gpu)
+    out = torch.full((4, 32, 128), float("nan"), dtype=F16, device=gpu)
+    ws = _ws(4, 32, 2, gpu)
+    if op == "masked":
+        ext.paged_attention_masked(q, k, v, bt.to(gpu), sl.to(gpu), out, ws, cols * 16, 16, 2)
+    else:
+        idx = torch.arange(4, dtype=torch.int32, device=gpu)
+        ext.paged_attention_indexed(q, k, v, bt.to(gpu), sl.to(gpu), idx, idx, out, ws,
+                                    cols * 16, 16, 2)
+    torch.cuda.synchronize()
+    assert sl_ref.tolist() == [cols * 16, 64, 40, 0]
+    assert_parity(out, ref)
