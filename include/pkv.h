@@ -345,6 +345,41 @@ int pkv_append_kv_fp8(const void* k_new, const void* v_new, void* k_pages, void*
                       int32_t page_size, int32_t max_pages, float k_scale, float v_scale,
                       int32_t dtype, void* stream);
 
+/* Decode with the append fused in: the result and the pools afterwards equal
+ * pkv_append_kv(k_new, v_new, ...) followed by the op without the suffix, in one decode
+ * launch.  The newest token of each row (position seq_lens[b] - 1) is read from k_new /
+ * v_new ([batch, num_kv_heads, 128], `dtype`) by the one wave whose tiles hold it, which
+ * also writes it into the pools.  2-byte pools only; page sizes that are not multiples
+ * of 16 run pkv_append_kv first on the same stream.  A row's tail slot must not be read
+ * through another (row, position) of the same step (no two rows share a tail page, as
+ * in any copy-on-write cache).  No counterpart in the reference (see pkv_append_kv). */
+int pkv_paged_attention_indexed_append(
+    const void* q_source, int32_t q_rows,
+    const void* k_pages, const void* v_pages,
+    const int32_t* block_table, const int32_t* seq_lens,
+    const int32_t* q_indices, const int32_t* out_indices,
+    void* output, int32_t out_rows,
+    void* workspace, size_t workspace_bytes,
+    int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t num_pages, int32_t page_size, int32_t max_pages,
+    int32_t bucket_context, int32_t num_splits, const void* k_new, const void* v_new,
+    int32_t dtype, void* stream);
+
+/* pkv_paged_attention_workqueue with the append fused in (as above). */
+int pkv_paged_attention_workqueue_append(
+    const void* q_source, int32_t q_rows,
+    const void* k_pages, const void* v_pages,
+    const int32_t* block_table, const int32_t* seq_lens,
+    const int32_t* work_items, int32_t num_tasks,
+    const int32_t* split_offsets, int32_t* merge_counters,
+    const int32_t* q_indices, const int32_t* out_indices,
+    void* output, int32_t out_rows,
+    void* workspace, size_t workspace_bytes,
+    int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t num_pages, int32_t page_size, int32_t max_pages,
+    int32_t bucket_context, int32_t total_partial_slots, int32_t fused_merge,
+    const void* k_new, const void* v_new, int32_t dtype, void* stream);
+
 /* ---------------------------------------------------------------------------------
  * HBM calibration probes (counterparts of the reference's
  * micro_benchmarks/01_hbm_bandwidth.cu:20-51 read/copy kernels).

@@ -139,6 +139,10 @@ struct DecodeArgs {
   // Contiguous layout only: unit kv head v reads the K/V of head v / kv_div (1, or G for
   // the query-head baseline, whose units are single query heads).
   int32_t kv_div;
+  // Fused append (paged fp16 / bf16, pages a multiple of 16), else null: each row's
+  // newest token, [B, Hkv, 128] in the KV dtype, written to position seq_lens[b] - 1.
+  const uint8_t* k_new;
+  const uint8_t* v_new;
 };
 
 // ---------------------------------------------------------------------------------
@@ -319,6 +323,62 @@ struct FastPager {
 #pragma unroll
       for (int j = 0; j < 4; ++j) r.v[b * 4 + j] = __builtin_amdgcn_raw_buffer_load_b128(rv, voff[b * 4 + j], 0, 0);
     }
+  }
+};
+
+// FastPager for a step that also appends each row's newest token, the write of
+// pkv_append_kv: position seq_lens[row] - 1, page block_table[row, pos / ps].  That
+// token's K and V rows are taken from k_new / v_new instead of the pool, and the wave
+// whose tiles hold it also writes it into the pool.  No other wave of the launch reads
+// those bytes (each row's tail slot belongs to one (row, kv head) unit), so the result
+// equals pkv_append_kv followed by the same decode.  Rows whose append pkv_append_kv
+// skips (no tokens, a position past the table, a page id outside the pool) are decoded
+// from the pool as they are.
+struct AppendPager : FastPager {
+  int pos;             // the new token's position, or -1 when this wave does not hold it
+  int lane;
+  const uint8_t* kn;   // k_new[row, kvh, :], 256 bytes
+  const uint8_t* vn;
+
+  __device__ AppendPager(const DecodeArgs& args, int row, int kvh, int limit, int lane_id)
+      : FastPager(args, row, kvh, limit, lane_id), lane(lane_id) {
+    const int raw = load_scalar(args.seq_lens + row);
+    const long cap = (long)args.max_pages * args.page_size;
+    // limit = min(32 * t1, clamped length): the token is this wave's when its tile is
+    // below t1 (tiles below t0 are never issued).
+    pos = raw >= 1 && (long)raw <= cap && raw - 1 < limit ? raw - 1 : -1;
+    const long src = ((long)row * args.hkv + kvh) * (kD * 2);
+    kn = args.k_new + src;
+    vn = args.v_new + src;
+  }
+
+  __device__ inline void issue(int tile, const Pages& p, TileRegs& r) const {
+    FastPager::issue(tile, p, r);
+    const int rel = pos - tile * kTile;  // wave-uniform
+    if (pos < 0 || rel < 0 || rel >= kTile) return;
+    const int b = rel >> 4, prow = rel & 15;
+    const int page = b ? p.page[1] : p.page[0];
+    if ((unsigned)page >= (unsigned)a.num_pages) return;  // the append skips this row
+    // Lane (c, g) holds K row c of each block at bytes 64kk + 16g, and V row 4g + jj of
+    // block slot jj at bytes 16c (FastPager's koff / voff).
+    // The lanes that hold the token reload those registers from k_new / v_new; the
+    // loads return in issue order, after the pool loads of the same registers.
+    const int c = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int bb = 0; bb < 2; ++bb) {
+      if (bb == b && c == prow) {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) r.k[bb][kk] = *(const u32x4*)(kn + kk * 64 + g * 16);
+      }
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+        if (bb == b && 4 * g + jj == prow) r.v[bb * 4 + jj] = *(const u32x4*)(vn + c * 16);
+    }
+    int logical, in_page;
+    page_of(a, pos, logical, in_page);
+    const long dst = (long)page * page_bytes + head_bytes + (long)in_page * (kD * 2) + lane * 4;
+    *(uint32_t*)(const_cast<uint8_t*>(a.k_pages) + dst) = *(const uint32_t*)(kn + lane * 4);
+    *(uint32_t*)(const_cast<uint8_t*>(a.v_pages) + dst) = *(const uint32_t*)(vn + lane * 4);
   }
 };
 
@@ -999,7 +1059,7 @@ __device__ inline void init_state(WaveState<HB>& st) {
 
 // K/V addressing of a launch: paged with 16-token-aligned pages, paged with any page
 // size, or contiguous.
-enum : int { kPgGeneric = 0, kPgFast = 1, kPgContig = 2, kPgFp8 = 3 };
+enum : int { kPgGeneric = 0, kPgFast = 1, kPgContig = 2, kPgFp8 = 3, kPgAppend = 4 };
 
 template <class Elem, int HB, int PG>
 __device__ inline void stream_unit(const DecodeArgs& a, WaveState<HB>& st, const u32x4 (&qf)[HB][4],
@@ -1011,6 +1071,10 @@ __device__ inline void stream_unit(const DecodeArgs& a, WaveState<HB>& st, const
   const float qk = a.score_scale;
   if constexpr (PG == kPgFast) {
     FastPager pg(a, row, kvh, lim, lane);
+    if (have_first) stream_range_from<Elem, HB>(st, pg, qf, t0, t1, lim, lane, qk, f0, f1);
+    else stream_range<Elem, HB>(st, pg, qf, t0, t1, lim, lane, qk);
+  } else if constexpr (PG == kPgAppend) {
+    AppendPager pg(a, row, kvh, lim, lane);
     if (have_first) stream_range_from<Elem, HB>(st, pg, qf, t0, t1, lim, lane, qk, f0, f1);
     else stream_range<Elem, HB>(st, pg, qf, t0, t1, lim, lane, qk);
   } else if constexpr (PG == kPgFp8) {
@@ -1300,7 +1364,7 @@ void decode_kernel(DecodeArgs a) {
   int first_tile = -1;
   Unit u;
   int q_loaded = 0;  // q_indices[row] when q_indices is set, left in a VGPR (see load_q)
-  if constexpr (MODE == kQueue && (PG == kPgFast || PG == kPgFp8)) {
+  if constexpr (MODE == kQueue && (PG == kPgFast || PG == kPgFp8 || PG == kPgAppend)) {
     const int32_t* w = a.work_items + (long)blockIdx.x * 5;
     const int row = load_scalar(w + 0), kvh = load_scalar(w + 1), split = load_scalar(w + 2);
     const int tb = load_scalar(w + 3), te = load_scalar(w + 4);
@@ -1562,7 +1626,7 @@ bool use_async_combine(int units) {
 template <class Elem, int HB, int PG, int MODE>
 hipError_t launch_decode(const DecodeArgs& a, int grid, hipStream_t stream) {
   if (HB == 1 && decode_waves(HB) == 8) {
-    if constexpr (HB == 1 && (PG == kPgFast || PG == kPgFp8) && MODE != kDirect) {
+    if constexpr (HB == 1 && (PG == kPgFast || PG == kPgFp8 || PG == kPgAppend) && MODE != kDirect) {
       if (use_async_combine(grid)) {
         decode_kernel<Elem, HB, PG, MODE, 8, true>
             <<<dim3(grid), dim3(8 * 64), lds_bytes(a.group, 8, true), stream>>>(a);
@@ -1585,6 +1649,7 @@ hipError_t launch_layout(const DecodeArgs& a, int grid, hipStream_t stream) {
     if (!a.block_table) return launch_decode<Elem, HB, kPgContig, MODE>(a, grid, stream);
   }
   if (a.kv_fp8) return launch_decode<Elem, HB, kPgFp8, MODE>(a, grid, stream);
+  if (a.k_new) return launch_decode<Elem, HB, kPgAppend, MODE>(a, grid, stream);  // pages % 16 == 0
   return (a.page_size % 16) == 0 ? launch_decode<Elem, HB, kPgFast, MODE>(a, grid, stream)
                                  : launch_decode<Elem, HB, kPgGeneric, MODE>(a, grid, stream);
 }
@@ -1779,11 +1844,38 @@ void apply_quant(DecodeArgs& a, const KvQuant& kq) {
   a.v_scale = kq.v_scale;
 }
 
+// Each row's newest token for the *_append ops ([B, Hkv, 128] in the KV dtype), or null.
+struct NewToken {
+  const void* k = nullptr;
+  const void* v = nullptr;
+};
+
+// The fused append of the *_append ops.  Pages that are multiples of 16 take the new
+// token inside the decode (AppendPager); other page sizes run pkv_append_kv first, on the
+// same stream.  Call after apply_quant.
+int apply_new_token(const Geometry& g, DecodeArgs& a, const NewToken& nt, hipStream_t stream) {
+  if (!nt.k && !nt.v) return PKV_OK;
+  if (!nt.k || !nt.v) return fail(PKV_ERR_INVALID_ARGUMENT, "k_new and v_new must both be set");
+  if (a.kv_fp8)
+    return fail(PKV_ERR_UNSUPPORTED,
+                "the fused append takes fp16 / bf16 pools (append to fp8 pools with pkv_append_kv_fp8)");
+  if (!a.seq_lens) return fail(PKV_ERR_INVALID_ARGUMENT, "the fused append needs seq_lens");
+  if (g.page_size % 16 == 0) {
+    a.k_new = (const uint8_t*)nt.k;
+    a.v_new = (const uint8_t*)nt.v;
+    return PKV_OK;
+  }
+  return pkv_append_kv(nt.k, nt.v, const_cast<uint8_t*>(a.k_pages), const_cast<uint8_t*>(a.v_pages),
+                       a.block_table, a.seq_lens, g.batch, g.hkv, kD, g.num_pages, g.page_size,
+                       g.max_pages, g.dtype, stream);
+}
+
 // Shared body of the three paged grid ops.
 int run_grid(const Geometry& g, const void* q, int q_rows, const void* k, const void* v,
              const int32_t* table, const int32_t* seq_lens, const int32_t* q_idx,
              const int32_t* out_idx, void* out, int out_rows, void* ws, size_t ws_bytes,
-             int context, int num_splits, void* stream_ptr, const KvQuant& kq = KvQuant{}) {
+             int context, int num_splits, void* stream_ptr, const KvQuant& kq = KvQuant{},
+             const NewToken& nt = NewToken{}) {
   int st = check_geometry(g, q, k, v, table, out);
   if (st != PKV_OK) return st;
   st = check_quant(g, kq);
@@ -1805,6 +1897,8 @@ int run_grid(const Geometry& g, const void* q, int q_rows, const void* k, const 
   a.out_indices = out_idx;
   a.context = context;
   apply_quant(a, kq);
+  st = apply_new_token(g, a, nt, (hipStream_t)stream_ptr);
+  if (st != PKV_OK) return st;
   return launch_grid(g, a, ws, ws_bytes, num_splits, true, (hipStream_t)stream_ptr);
 }
 
@@ -1906,17 +2000,19 @@ int run_indexed(const Geometry& g, const void* q_source, int32_t q_rows, const v
                 const void* v_pages, const int32_t* block_table, const int32_t* seq_lens,
                 const int32_t* q_indices, const int32_t* out_indices, void* output,
                 int32_t out_rows, void* workspace, size_t workspace_bytes, int32_t bucket_context,
-                int32_t num_splits, void* stream, const KvQuant& kq) {
+                int32_t num_splits, void* stream, const KvQuant& kq,
+                const NewToken& nt = NewToken{}) {
   if (g.batch > 0 && (!seq_lens || !q_indices || !out_indices))
     return fail(PKV_ERR_INVALID_ARGUMENT, "seq_lens, q_indices and out_indices must be non-null");
   if (g.batch > 0 && out_rows <= 0) return fail(PKV_ERR_INVALID_ARGUMENT, "output has no rows");
   return run_grid(g, q_source, q_rows, k_pages, v_pages, block_table, seq_lens, q_indices,
                   out_indices, output, out_rows, workspace, workspace_bytes, bucket_context,
-                  num_splits, stream, kq);
+                  num_splits, stream, kq, nt);
 }
 
 // The work-queue op (decode, then the segmented merge unless fused).
-int run_workqueue(const QueueCall& c, int32_t fused_merge, hipStream_t stream, const KvQuant& kq) {
+int run_workqueue(const QueueCall& c, int32_t fused_merge, hipStream_t stream, const KvQuant& kq,
+                  const NewToken& nt = NewToken{}) {
   int st = check_queue(c, true);
   if (st != PKV_OK) return st;
   st = check_quant(c.g, kq);
@@ -1926,6 +2022,8 @@ int run_workqueue(const QueueCall& c, int32_t fused_merge, hipStream_t stream, c
   if (c.g.batch == 0) return ok();
   DecodeArgs a = queue_args(c);
   apply_quant(a, kq);
+  st = apply_new_token(c.g, a, nt, stream);
+  if (st != PKV_OK) return st;
   a.merge_counters = fused_merge ? c.counters : nullptr;
   st = dispatch_decode<kQueue>(a, c.g.dtype, c.num_tasks, stream);
   if (st != PKV_OK) return st;
@@ -2066,6 +2164,38 @@ int pkv_paged_attention_workqueue(
                     split_offsets, q_indices, out_indices, merge_counters, output, out_rows,
                     workspace, workspace_bytes, bucket_context, num_tasks, total_partial_slots};
   return run_workqueue(c, fused_merge, (hipStream_t)stream, KvQuant{});
+}
+
+int pkv_paged_attention_indexed_append(
+    const void* q_source, int32_t q_rows, const void* k_pages, const void* v_pages,
+    const int32_t* block_table, const int32_t* seq_lens, const int32_t* q_indices,
+    const int32_t* out_indices, void* output, int32_t out_rows, void* workspace,
+    size_t workspace_bytes, int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+    int32_t head_dim, int32_t num_pages, int32_t page_size, int32_t max_pages,
+    int32_t bucket_context, int32_t num_splits, const void* k_new, const void* v_new,
+    int32_t dtype, void* stream) {
+  const Geometry g{batch, num_q_heads, num_kv_heads, head_dim, num_pages, page_size, max_pages, dtype};
+  if (batch > 0 && (!k_new || !v_new)) return fail(PKV_ERR_INVALID_ARGUMENT, "k_new or v_new is null");
+  return run_indexed(g, q_source, q_rows, k_pages, v_pages, block_table, seq_lens, q_indices,
+                     out_indices, output, out_rows, workspace, workspace_bytes, bucket_context,
+                     num_splits, stream, KvQuant{}, NewToken{k_new, v_new});
+}
+
+int pkv_paged_attention_workqueue_append(
+    const void* q_source, int32_t q_rows, const void* k_pages, const void* v_pages,
+    const int32_t* block_table, const int32_t* seq_lens, const int32_t* work_items,
+    int32_t num_tasks, const int32_t* split_offsets, int32_t* merge_counters,
+    const int32_t* q_indices, const int32_t* out_indices, void* output, int32_t out_rows,
+    void* workspace, size_t workspace_bytes, int32_t batch, int32_t num_q_heads,
+    int32_t num_kv_heads, int32_t head_dim, int32_t num_pages, int32_t page_size,
+    int32_t max_pages, int32_t bucket_context, int32_t total_partial_slots,
+    int32_t fused_merge, const void* k_new, const void* v_new, int32_t dtype, void* stream) {
+  const QueueCall c{{batch, num_q_heads, num_kv_heads, head_dim, num_pages, page_size, max_pages, dtype},
+                    q_source, k_pages, v_pages, q_rows, block_table, seq_lens, work_items,
+                    split_offsets, q_indices, out_indices, merge_counters, output, out_rows,
+                    workspace, workspace_bytes, bucket_context, num_tasks, total_partial_slots};
+  if (batch > 0 && (!k_new || !v_new)) return fail(PKV_ERR_INVALID_ARGUMENT, "k_new or v_new is null");
+  return run_workqueue(c, fused_merge, (hipStream_t)stream, KvQuant{}, NewToken{k_new, v_new});
 }
 
 int pkv_paged_attention_workqueue_fp8(

@@ -9,7 +9,8 @@
 // Beyond the reference's four ops: the two work-queue stages, fp8 (float8_e4m3fn) K/V
 // variants of the indexed and work-queue ops, the contiguous-layout decode and
 // query-head baseline of its C++ API (cuh:1077-1108, :1263-1282), and the KV-cache append
-// (fp16 / bf16 / fp8 pools) that a serving loop runs before each decode step.
+// (fp16 / bf16 / fp8 pools) that a serving loop runs before each decode step, alone or
+// fused into the indexed and work-queue ops (*_append).
 // Work is enqueued on the current HIP stream of the tensors' device without a host sync,
 // so the ops can be captured in HIP graphs.
 
@@ -144,11 +145,23 @@ namespace {
 
 // Shared body of the indexed op and its fp8-K/V variant (kv_fp8: K/V are float8_e4m3fn
 // pages dequantised by k_scale / v_scale).
+// k_new / v_new of the *_append ops: each row's newest token, [B, Hkv, 128] in the
+// activation dtype.
+void check_new_token(const torch::Tensor& k_new, const torch::Tensor& v_new, at::ScalarType dt,
+                     int64_t B, int64_t Hkv) {
+  check_tensor(k_new, "k_new", dt, 3);
+  check_tensor(v_new, "v_new", dt, 3);
+  TORCH_CHECK(k_new.size(0) == B && k_new.size(1) == Hkv && k_new.size(2) == PKV_HEAD_DIM,
+              "k_new must have shape [B, Hkv, 128]");
+  TORCH_CHECK(v_new.sizes() == k_new.sizes(), "v_new shape mismatch");
+}
+
 void indexed_op(torch::Tensor q_source, torch::Tensor k_pages, torch::Tensor v_pages,
                 torch::Tensor block_table, torch::Tensor seq_lens, torch::Tensor q_indices,
                 torch::Tensor out_indices, torch::Tensor output, torch::Tensor workspace,
                 int64_t bucket_context, int64_t page_size, int64_t num_splits, bool kv_fp8,
-                double k_scale, double v_scale) {
+                double k_scale, double v_scale, const torch::Tensor* k_new = nullptr,
+                const torch::Tensor* v_new = nullptr) {
   const auto dt = activation_dtype(q_source, "q_source");
   const auto kv_dt = kv_fp8 ? at::kFloat8_e4m3fn : dt;
   check_tensor(q_source, "q_source", dt, 3);
@@ -178,7 +191,16 @@ void indexed_op(torch::Tensor q_source, torch::Tensor k_pages, torch::Tensor v_p
   const int32_t no = i32(output.size(0), "output.size(0)");
   const int32_t np = i32(k_pages.size(0), "k_pages.size(0)");
   const int32_t mp = i32(block_table.size(1), "block_table.size(1)");
-  if (kv_fp8)
+  if (k_new) {
+    check_new_token(*k_new, *v_new, dt, B, Hkv);
+    raise_on(pkv_paged_attention_indexed_append(
+        q_source.data_ptr(), nq, k_pages.data_ptr(), v_pages.data_ptr(), block_table.data_ptr<int>(),
+        seq_lens.data_ptr<int>(), q_indices.data_ptr<int>(), out_indices.data_ptr<int>(),
+        output.data_ptr(), no, ws_ptr(workspace), ws_bytes(workspace), B, Hq, Hkv, d, np,
+        i32(page_size, "page_size"), mp, i32(bucket_context, "bucket_context"),
+        i32(num_splits, "num_splits"), k_new->data_ptr(), v_new->data_ptr(), pkv_dtype_of(dt),
+        stream_of(q_source)));
+  } else if (kv_fp8)
     raise_on(pkv_paged_attention_indexed_fp8(
         q_source.data_ptr(), nq, k_pages.data_ptr(), v_pages.data_ptr(), block_table.data_ptr<int>(),
         seq_lens.data_ptr<int>(), q_indices.data_ptr<int>(), out_indices.data_ptr<int>(),
@@ -218,6 +240,17 @@ void persistentkv_paged_attention_indexed_fp8(torch::Tensor q_source, torch::Ten
                                               double k_scale, double v_scale) {
   indexed_op(q_source, k_pages, v_pages, block_table, seq_lens, q_indices, out_indices, output,
              workspace, bucket_context, page_size, num_splits, true, k_scale, v_scale);
+}
+
+// The indexed op with the KV append fused in: equals append_kv(k_new, v_new, k_pages,
+// v_pages, block_table, seq_lens) followed by paged_attention_indexed (2-byte pools).
+void persistentkv_paged_attention_indexed_append(
+    torch::Tensor q_source, torch::Tensor k_pages, torch::Tensor v_pages, torch::Tensor block_table,
+    torch::Tensor seq_lens, torch::Tensor q_indices, torch::Tensor out_indices,
+    torch::Tensor output, torch::Tensor workspace, int64_t bucket_context, int64_t page_size,
+    int64_t num_splits, torch::Tensor k_new, torch::Tensor v_new) {
+  indexed_op(q_source, k_pages, v_pages, block_table, seq_lens, q_indices, out_indices, output,
+             workspace, bucket_context, page_size, num_splits, false, 1.0, 1.0, &k_new, &v_new);
 }
 
 namespace {
@@ -275,7 +308,8 @@ void workqueue_op(torch::Tensor q_source, torch::Tensor k_pages, torch::Tensor v
                   torch::Tensor q_indices, torch::Tensor out_indices, torch::Tensor output,
                   torch::Tensor workspace, int64_t bucket_context, int64_t page_size,
                   int64_t total_partial_slots, bool fused_merge, bool kv_fp8, double k_scale,
-                  double v_scale) {
+                  double v_scale, const torch::Tensor* k_new = nullptr,
+                  const torch::Tensor* v_new = nullptr) {
   const QueueTensors t = check_queue_tensors(q_source, k_pages, v_pages, block_table, seq_lens,
                                              work_items, split_offsets, q_indices, workspace,
                                              bucket_context, page_size, total_partial_slots,
@@ -295,7 +329,17 @@ void workqueue_op(torch::Tensor q_source, torch::Tensor k_pages, torch::Tensor v
   const int32_t np = i32(k_pages.size(0), "k_pages.size(0)");
   const int32_t mp = i32(block_table.size(1), "block_table.size(1)");
   int32_t* counters = fused_merge ? merge_counters.data_ptr<int>() : nullptr;
-  if (kv_fp8)
+  if (k_new) {
+    check_new_token(*k_new, *v_new, t.dt, t.B, t.Hkv);
+    raise_on(pkv_paged_attention_workqueue_append(
+        q_source.data_ptr(), nq, k_pages.data_ptr(), v_pages.data_ptr(), block_table.data_ptr<int>(),
+        seq_lens.data_ptr<int>(), work_items.data_ptr<int>(), nt, split_offsets.data_ptr<int>(),
+        counters, q_indices.data_ptr<int>(), out_indices.data_ptr<int>(), output.data_ptr(), no,
+        ws_ptr(workspace), ws_bytes(workspace), t.B, t.Hq, t.Hkv, t.d, np,
+        i32(page_size, "page_size"), mp, i32(bucket_context, "bucket_context"),
+        i32(total_partial_slots, "total_partial_slots"), fused_merge ? 1 : 0, k_new->data_ptr(),
+        v_new->data_ptr(), pkv_dtype_of(t.dt), stream_of(q_source)));
+  } else if (kv_fp8)
     raise_on(pkv_paged_attention_workqueue_fp8(
         q_source.data_ptr(), nq, k_pages.data_ptr(), v_pages.data_ptr(), block_table.data_ptr<int>(),
         seq_lens.data_ptr<int>(), work_items.data_ptr<int>(), nt, split_offsets.data_ptr<int>(),
@@ -339,6 +383,18 @@ void persistentkv_paged_attention_workqueue_fp8(
   workqueue_op(q_source, k_pages, v_pages, block_table, seq_lens, work_items, split_offsets,
                merge_counters, q_indices, out_indices, output, workspace, bucket_context,
                page_size, total_partial_slots, fused_merge, true, k_scale, v_scale);
+}
+
+// The work-queue op with the KV append fused in (as paged_attention_indexed_append).
+void persistentkv_paged_attention_workqueue_append(
+    torch::Tensor q_source, torch::Tensor k_pages, torch::Tensor v_pages, torch::Tensor block_table,
+    torch::Tensor seq_lens, torch::Tensor work_items, torch::Tensor split_offsets,
+    torch::Tensor merge_counters, torch::Tensor q_indices, torch::Tensor out_indices,
+    torch::Tensor output, torch::Tensor workspace, int64_t bucket_context, int64_t page_size,
+    int64_t total_partial_slots, bool fused_merge, torch::Tensor k_new, torch::Tensor v_new) {
+  workqueue_op(q_source, k_pages, v_pages, block_table, seq_lens, work_items, split_offsets,
+               merge_counters, q_indices, out_indices, output, workspace, bucket_context,
+               page_size, total_partial_slots, fused_merge, false, 1.0, 1.0, &k_new, &v_new);
 }
 
 namespace {
@@ -544,6 +600,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "Work-queue decode stage over fp8 (e4m3) K/V pages");
   m.def("attention_contiguous", &persistentkv_attention_contiguous,
         "GQA decode over contiguous K/V [B, Hkv, N, 128]");
+  m.def("paged_attention_indexed_append", &persistentkv_paged_attention_indexed_append,
+        "paged_attention_indexed with the KV append fused in (k_new, v_new)");
+  m.def("paged_attention_workqueue_append", &persistentkv_paged_attention_workqueue_append,
+        "paged_attention_workqueue with the KV append fused in (k_new, v_new)");
   m.def("append_kv", &persistentkv_append_kv,
         "write each row's newest token's K/V into its tail page (position seq_lens - 1)");
   m.def("append_kv_fp8", &persistentkv_append_kv_fp8,

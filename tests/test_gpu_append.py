@@ -5,11 +5,13 @@ pools, and for fp8 pools the bytes of oracle.quantize_e4m3 (itself pinned agains
 float8_e4m3fn cast on every 16-bit input, tests/test_oracle_fp8.py).  Cases cover
 positions at both ends of a page, rows that must be skipped (no tokens, a position past
 the table, a page id outside the pool), every fp16 bit pattern through the fp8 encoder,
-and decoding after the append.
+decoding after the append, and the *_append ops, which fuse the append into the decode and
+must give bit for bit the pools and output of append_kv followed by the op.
 """
 import pytest
 import torch
 
+import pkv_native
 from oracle import attention as oracle
 from paged_cases import assert_parity, make_case
 
@@ -182,3 +184,111 @@ def test_append_then_decode_in_a_hip_graph(ext, gpu):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager_out) and torch.equal(k, eager_k)
+
+
+def _new_tokens(b, hkv, dtype, seed):
+    gen = torch.Generator().manual_seed(seed)
+    return (torch.randn(b, hkv, 128, generator=gen).to(dtype),
+            torch.randn(b, hkv, 128, generator=gen).to(dtype))
+
+
+# (lengths, Hq, Hkv, page_size, splits, dtype); lengths count the appended token
+FUSED_INDEXED = [
+    ([300, 17, 64, 1], 32, 8, 16, 3, F16),
+    ([700, 33, 1], 32, 4, 32, 2, BF16),        # G = 8, page 32
+    ([1000, 65], 32, 1, 16, 4, BF16),          # G = 32 (two head blocks)
+    ([2048], 32, 8, 16, 1, F16),               # direct launch, split inside
+    ([129, 0, 96], 32, 8, 16, 2, F16),         # a row with no tokens: no append, zeros
+    ([90, 41], 32, 8, 5, 2, F16),              # page 5: append kernel, then the decode
+    ([31, 32, 33, 48, 49, 64], 8, 8, 16, 1, F16),  # the token at both ends of tiles and blocks
+]
+
+
+@pytest.mark.parametrize("lengths,hq,hkv,ps,splits,dtype", FUSED_INDEXED)
+def test_fused_append_indexed_equals_append_then_decode(ext, gpu, lengths, hq, hkv, ps, splits,
+                                                        dtype):
+    """paged_attention_indexed_append gives bit for bit the output and the pools of
+    append_kv followed by paged_attention_indexed, and matches the oracle."""
+    b = len(lengths)
+    case = make_case(lengths, hq, hkv, ps, dtype, seed=sum(lengths) + ps, q_rows=b + 1)
+    kn, vn = _new_tokens(b, hkv, dtype, seed=len(lengths))
+    bt, sl = case.block_table.to(gpu), case.seq_lens.to(gpu)
+    qi = torch.arange(b, dtype=torch.int32, device=gpu).flip(0)
+    oi = torch.arange(b, dtype=torch.int32, device=gpu)
+    bucket = max(max(lengths), 32 * splits)
+    ws = torch.empty(max(1, b * hq * splits * 130), dtype=torch.float32, device=gpu)
+    q = case.q.to(gpu)
+
+    k1, v1 = case.k_pages.to(gpu), case.v_pages.to(gpu)
+    out1 = torch.full((b, hq, 128), float("nan"), dtype=dtype, device=gpu)
+    ext.append_kv(kn.to(gpu), vn.to(gpu), k1, v1, bt, sl)
+    ext.paged_attention_indexed(q, k1, v1, bt, sl, qi, oi, out1, ws, bucket, ps, splits)
+    k2, v2 = case.k_pages.to(gpu), case.v_pages.to(gpu)
+    out2 = torch.full((b, hq, 128), float("nan"), dtype=dtype, device=gpu)
+    ext.paged_attention_indexed_append(q, k2, v2, bt, sl, qi, oi, out2, ws, bucket, ps, splits,
+                                       kn.to(gpu), vn.to(gpu))
+    torch.cuda.synchronize()
+    assert torch.equal(k2, k1) and torch.equal(v2, v1)
+    assert torch.equal(out2, out1)
+    k_ref, v_ref = oracle.append_kv(case.k_pages, case.v_pages, case.block_table, case.seq_lens,
+                                    kn, vn)
+    ref = oracle.paged_decode(case.q, k_ref, v_ref, case.block_table, case.seq_lens,
+                              qi.cpu(), oi.cpu())
+    assert_parity(out2, ref)
+
+
+@pytest.mark.parametrize("fused_merge", [False, True])
+@pytest.mark.parametrize("lengths,hkv,dtype", [([40, 700, 1500, 33], 8, F16),
+                                               ([3000, 65, 900], 1, BF16)])
+def test_fused_append_workqueue_equals_append_then_decode(ext, gpu, lengths, hkv, dtype,
+                                                          fused_merge):
+    hq, ps = 32, 16
+    case = make_case(lengths, hq, hkv, ps, dtype, seed=len(lengths) + hkv)
+    meta = pkv_native.build_workqueue(lengths, list(range(len(lengths))), case.page_lists, ps, 6,
+                                      False, hkv)
+    t = lambda a: torch.as_tensor(a, dtype=torch.int32, device=gpu)
+    bt, sl, wi, so, qi, oi = (t(meta[k]) for k in ("block_table", "seq_lens", "work_items",
+                                                   "split_offsets", "q_indices", "out_indices"))
+    kn, vn = _new_tokens(len(lengths), hkv, dtype, seed=7)
+    slots = meta["total_partial_slots"]
+    q = case.q.to(gpu)
+    results = []
+    for fused_append in (False, True):
+        k, v = case.k_pages.to(gpu), case.v_pages.to(gpu)
+        out = torch.full((len(lengths), hq, 128), float("nan"), dtype=dtype, device=gpu)
+        ws = torch.empty(slots * hq * 130, dtype=torch.float32, device=gpu)
+        counters = torch.zeros(len(lengths), hkv, dtype=torch.int32, device=gpu)
+        args = (q, k, v, bt, sl, wi, so, counters, qi, oi, out, ws, meta["bucket_length"], ps,
+                slots, fused_merge)
+        if fused_append:
+            ext.paged_attention_workqueue_append(*args, kn.to(gpu), vn.to(gpu))
+        else:
+            ext.append_kv(kn.to(gpu), vn.to(gpu), k, v, bt, sl)
+            ext.paged_attention_workqueue(*args)
+        torch.cuda.synchronize()
+        results.append((out.cpu(), k.cpu(), v.cpu()))
+    (o1, k1, v1), (o2, k2, v2) = results
+    assert torch.equal(k2, k1) and torch.equal(v2, v1)
+    assert torch.equal(o2, o1)
+    k_ref, v_ref = oracle.append_kv(case.k_pages, case.v_pages, case.block_table, case.seq_lens,
+                                    kn, vn)
+    assert torch.equal(k2, k_ref) and torch.equal(v2, v_ref)
+    ref = oracle.paged_decode(case.q, k_ref, v_ref, meta["block_table"], meta["seq_lens"],
+                              meta["q_indices"], meta["out_indices"])
+    assert_parity(o2, ref)
+
+
+def test_fused_append_validation(ext, gpu):
+    case = make_case([64], 32, 8, 16, F16)
+    q, k, v = case.q.to(gpu), case.k_pages.to(gpu), case.v_pages.to(gpu)
+    bt, sl = case.block_table.to(gpu), case.seq_lens.to(gpu)
+    idx = torch.zeros(1, dtype=torch.int32, device=gpu)
+    out = torch.empty(1, 32, 128, dtype=F16, device=gpu)
+    ws = torch.empty(0, dtype=torch.float32, device=gpu)
+    kn = torch.zeros(1, 8, 128, dtype=F16, device=gpu)
+    with pytest.raises(RuntimeError, match=r"k_new must have shape"):
+        ext.paged_attention_indexed_append(q, k, v, bt, sl, idx, idx, out, ws, 64, 16, 1,
+                                           kn[:, :4].contiguous(), kn[:, :4].contiguous())
+    with pytest.raises(RuntimeError, match="wrong dtype"):
+        ext.paged_attention_indexed_append(q, k, v, bt, sl, idx, idx, out, ws, 64, 16, 1,
+                                           kn.to(BF16), kn.to(BF16))
