@@ -62,9 +62,10 @@ def parse_args():
     p.add_argument("--kv-fp8", action="store_true",
                    help="K/V pages in fp8 (OCP e4m3) with per-tensor scales (work-queue and "
                         "indexed workloads); bytes and GB/s count the 1-byte elements")
-    p.add_argument("--append", action="store_true",
-                   help="each step first writes its rows' newest token K/V into the pool "
-                        "(append_kv; the reference harness writes none)")
+    p.add_argument("--append", nargs="?", const="separate", choices=("separate", "fused"),
+                   help="each step also writes its rows' newest token K/V into the pool: "
+                        "'separate' runs append_kv before the op, 'fused' the op's *_append "
+                        "variant (the reference harness writes none)")
     p.add_argument("--graph", action="store_true",
                    help="capture the timed steps into one HIP graph and replay it (as the "
                         "reference harness replays captured steps, benchmark_serving_trace.py:1439-1452)")
@@ -144,6 +145,9 @@ def main():
     def step(k):
         i = k % n_trace
         kp, vp = pools[k % len(pools)]
+        if args.append == "fused":
+            wl.run_step(ext, w, metas[i], i, q_pool, kp, vp, ws, new_kv=appends[i])
+            return
         if appends is not None:
             wl.append_step_kv_native(w, i, kp, vp, metas[i], ext, appends[i])
         wl.run_step(ext, w, metas[i], i, q_pool, kp, vp, ws)
@@ -272,7 +276,7 @@ def main():
                    "splits": "auto (mi355x planner)" if w.auto_splits else w.splits,
                    "fused_merge": bool(args.fused_merge),
                    "launch": "hip graph replay" if args.graph else "eager",
-                   "append_kv": bool(args.append),
+                   "append_kv": args.append or False,
                    "mean_kv_mb_per_step": round(sum(m.kv_bytes for m in metas) / n_trace / 1e6, 2),
                    "cache_basis": f"HBM-cold ({len(pools)} rotated KV pool replicas)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS,
