@@ -349,8 +349,8 @@ int pkv_append_kv_fp8(const void* k_new, const void* v_new, void* k_pages, void*
  * pkv_append_kv(k_new, v_new, ...) followed by the op without the suffix, in one decode
  * launch.  The newest token of each row (position seq_lens[b] - 1) is read from k_new /
  * v_new ([batch, num_kv_heads, 128], `dtype`) by the one wave whose tiles hold it, which
- * also writes it into the pools.  2-byte pools only; page sizes that are not multiples
- * of 16 run pkv_append_kv first on the same stream.  A row's tail slot must not be read
+ * also writes it into the pools.  Page sizes that are not multiples of 16 run
+ * pkv_append_kv first on the same stream.  (fp8 pools: the *_fp8_append entries below.)  A row's tail slot must not be read
  * through another (row, position) of the same step (no two rows share a tail page, as
  * in any copy-on-write cache).  No counterpart in the reference (see pkv_append_kv). */
 int pkv_paged_attention_indexed_append(
@@ -379,6 +379,37 @@ int pkv_paged_attention_workqueue_append(
     int32_t num_pages, int32_t page_size, int32_t max_pages,
     int32_t bucket_context, int32_t total_partial_slots, int32_t fused_merge,
     const void* k_new, const void* v_new, int32_t dtype, void* stream);
+
+/* The fp8-K/V ops with the append: k_new / v_new are in `dtype` and stored as
+ * pkv_append_kv_fp8 stores them, e4m3(clamp(x / k_scale)) and e4m3(clamp(x / v_scale)).
+ * Same result as pkv_append_kv_fp8 followed by the fp8 op, which is what they run (two
+ * launches; an in-decode fp8 append measured slower).  v_scale must be positive. */
+int pkv_paged_attention_indexed_fp8_append(
+    const void* q_source, int32_t q_rows,
+    const void* k_pages, const void* v_pages,
+    const int32_t* block_table, const int32_t* seq_lens,
+    const int32_t* q_indices, const int32_t* out_indices,
+    void* output, int32_t out_rows,
+    void* workspace, size_t workspace_bytes,
+    int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t num_pages, int32_t page_size, int32_t max_pages,
+    int32_t bucket_context, int32_t num_splits, float k_scale, float v_scale,
+    const void* k_new, const void* v_new, int32_t dtype, void* stream);
+
+int pkv_paged_attention_workqueue_fp8_append(
+    const void* q_source, int32_t q_rows,
+    const void* k_pages, const void* v_pages,
+    const int32_t* block_table, const int32_t* seq_lens,
+    const int32_t* work_items, int32_t num_tasks,
+    const int32_t* split_offsets, int32_t* merge_counters,
+    const int32_t* q_indices, const int32_t* out_indices,
+    void* output, int32_t out_rows,
+    void* workspace, size_t workspace_bytes,
+    int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t num_pages, int32_t page_size, int32_t max_pages,
+    int32_t bucket_context, int32_t total_partial_slots, int32_t fused_merge,
+    float k_scale, float v_scale, const void* k_new, const void* v_new,
+    int32_t dtype, void* stream);
 
 /* ---------------------------------------------------------------------------------
  * HBM calibration probes (counterparts of the reference's

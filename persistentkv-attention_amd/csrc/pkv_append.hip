@@ -16,6 +16,7 @@
 #include <stdint.h>
 
 #include "pkv.h"
+#include "pkv_e4m3.h"
 
 namespace pkv {
 int fail(int status, const char* fmt, ...);  // pkv_decode.hip: sets pkv_last_error()
@@ -37,32 +38,6 @@ struct AppendArgs {
   float k_scale, v_scale;      // fp8 pools: stored value = e4m3(x / scale)
 };
 
-// OCP e4m3 byte of y: |y| clamped to 448, rounded to the nearest value with ties to the
-// even code; NaN keeps its sign (0x7f / 0xff).
-__device__ inline uint32_t e4m3_encode(float y) {
-  const uint32_t sign = (__float_as_uint(y) >> 24) & 0x80u;
-  if (y != y) return sign | 0x7Fu;
-  const float a = fminf(fabsf(y), 448.0f);
-  if (a < 0.015625f)  // below 2^-6: subnormal steps of 2^-9 (8 steps is the smallest normal)
-    return sign | (uint32_t)__builtin_rintf(a * 512.0f);
-  const uint32_t bits = __float_as_uint(a);
-  int exponent = (int)(bits >> 23) - 127;  // -6 .. 8
-  uint32_t mantissa = (bits >> 20) & 7u;
-  const uint32_t rest = bits & 0xFFFFFu;   // the 20 mantissa bits below the kept 3
-  if (rest > 0x80000u || (rest == 0x80000u && (mantissa & 1u))) ++mantissa;
-  if (mantissa == 8u) {
-    mantissa = 0;
-    ++exponent;
-  }
-  return sign | ((uint32_t)(exponent + 7) << 3) | mantissa;
-}
-
-template <bool BF16_IN>
-__device__ inline float half_to_float(uint32_t h) {
-  if constexpr (BF16_IN) return __uint_as_float(h << 16);
-  return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
-}
-
 // One wave per (row, kv head); lane l writes dims 2l and 2l + 1 of K and of V.
 template <bool FP8, bool BF16_IN>
 __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
@@ -81,13 +56,8 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
   const uint32_t k2 = *(const uint32_t*)(a.k_new + src * 2);
   const uint32_t v2 = *(const uint32_t*)(a.v_new + src * 2);
   if constexpr (FP8) {
-    auto pack = [&](uint32_t x2, float scale) {
-      const uint32_t lo = e4m3_encode(half_to_float<BF16_IN>(x2 & 0xFFFFu) / scale);
-      const uint32_t hi = e4m3_encode(half_to_float<BF16_IN>(x2 >> 16) / scale);
-      return (uint16_t)(lo | (hi << 8));
-    };
-    *(uint16_t*)(a.k_pages + dst) = pack(k2, a.k_scale);
-    *(uint16_t*)(a.v_pages + dst) = pack(v2, a.v_scale);
+    *(uint16_t*)(a.k_pages + dst) = (uint16_t)pkv::e4m3_pack2<BF16_IN>(k2, a.k_scale);
+    *(uint16_t*)(a.v_pages + dst) = (uint16_t)pkv::e4m3_pack2<BF16_IN>(v2, a.v_scale);
   } else {
     *(uint32_t*)(a.k_pages + dst * 2) = k2;
     *(uint32_t*)(a.v_pages + dst * 2) = v2;

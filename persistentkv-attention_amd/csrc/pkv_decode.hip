@@ -1364,7 +1364,7 @@ void decode_kernel(DecodeArgs a) {
   int first_tile = -1;
   Unit u;
   int q_loaded = 0;  // q_indices[row] when q_indices is set, left in a VGPR (see load_q)
-  if constexpr (MODE == kQueue && (PG == kPgFast || PG == kPgFp8 || PG == kPgAppend)) {
+  if constexpr (MODE == kQueue && PG != kPgGeneric && PG != kPgContig) {
     const int32_t* w = a.work_items + (long)blockIdx.x * 5;
     const int row = load_scalar(w + 0), kvh = load_scalar(w + 1), split = load_scalar(w + 2);
     const int tb = load_scalar(w + 3), te = load_scalar(w + 4);
@@ -1626,7 +1626,7 @@ bool use_async_combine(int units) {
 template <class Elem, int HB, int PG, int MODE>
 hipError_t launch_decode(const DecodeArgs& a, int grid, hipStream_t stream) {
   if (HB == 1 && decode_waves(HB) == 8) {
-    if constexpr (HB == 1 && (PG == kPgFast || PG == kPgFp8 || PG == kPgAppend) && MODE != kDirect) {
+    if constexpr (HB == 1 && PG != kPgGeneric && PG != kPgContig && MODE != kDirect) {
       if (use_async_combine(grid)) {
         decode_kernel<Elem, HB, PG, MODE, 8, true>
             <<<dim3(grid), dim3(8 * 64), lds_bytes(a.group, 8, true), stream>>>(a);
@@ -1850,16 +1850,21 @@ struct NewToken {
   const void* v = nullptr;
 };
 
-// The fused append of the *_append ops.  Pages that are multiples of 16 take the new
-// token inside the decode (AppendPager); other page sizes run pkv_append_kv first, on the
-// same stream.  Call after apply_quant.
-int apply_new_token(const Geometry& g, DecodeArgs& a, const NewToken& nt, hipStream_t stream) {
+// The fused append of the *_append ops.  2-byte pools with pages that are multiples of
+// 16 take the new token inside the decode (AppendPager).  Other page sizes, and fp8
+// pools, run the append kernel first on the same stream: an in-decode fp8 variant (the
+// e4m3 encode on the reloaded lanes) measured slower than the two launches.  Call after
+// apply_quant.
+int apply_new_token(const Geometry& g, DecodeArgs& a, const NewToken& nt, const KvQuant& kq,
+                    hipStream_t stream) {
   if (!nt.k && !nt.v) return PKV_OK;
   if (!nt.k || !nt.v) return fail(PKV_ERR_INVALID_ARGUMENT, "k_new and v_new must both be set");
-  if (a.kv_fp8)
-    return fail(PKV_ERR_UNSUPPORTED,
-                "the fused append takes fp16 / bf16 pools (append to fp8 pools with pkv_append_kv_fp8)");
   if (!a.seq_lens) return fail(PKV_ERR_INVALID_ARGUMENT, "the fused append needs seq_lens");
+  if (a.kv_fp8)
+    return pkv_append_kv_fp8(nt.k, nt.v, const_cast<uint8_t*>(a.k_pages),
+                             const_cast<uint8_t*>(a.v_pages), a.block_table, a.seq_lens, g.batch,
+                             g.hkv, kD, g.num_pages, g.page_size, g.max_pages, kq.k_scale,
+                             kq.v_scale, g.dtype, stream);
   if (g.page_size % 16 == 0) {
     a.k_new = (const uint8_t*)nt.k;
     a.v_new = (const uint8_t*)nt.v;
@@ -1897,7 +1902,7 @@ int run_grid(const Geometry& g, const void* q, int q_rows, const void* k, const 
   a.out_indices = out_idx;
   a.context = context;
   apply_quant(a, kq);
-  st = apply_new_token(g, a, nt, (hipStream_t)stream_ptr);
+  st = apply_new_token(g, a, nt, kq, (hipStream_t)stream_ptr);
   if (st != PKV_OK) return st;
   return launch_grid(g, a, ws, ws_bytes, num_splits, true, (hipStream_t)stream_ptr);
 }
@@ -2022,7 +2027,7 @@ int run_workqueue(const QueueCall& c, int32_t fused_merge, hipStream_t stream, c
   if (c.g.batch == 0) return ok();
   DecodeArgs a = queue_args(c);
   apply_quant(a, kq);
-  st = apply_new_token(c.g, a, nt, stream);
+  st = apply_new_token(c.g, a, nt, kq, stream);
   if (st != PKV_OK) return st;
   a.merge_counters = fused_merge ? c.counters : nullptr;
   st = dispatch_decode<kQueue>(a, c.g.dtype, c.num_tasks, stream);
@@ -2196,6 +2201,40 @@ int pkv_paged_attention_workqueue_append(
                     workspace, workspace_bytes, bucket_context, num_tasks, total_partial_slots};
   if (batch > 0 && (!k_new || !v_new)) return fail(PKV_ERR_INVALID_ARGUMENT, "k_new or v_new is null");
   return run_workqueue(c, fused_merge, (hipStream_t)stream, KvQuant{}, NewToken{k_new, v_new});
+}
+
+int pkv_paged_attention_indexed_fp8_append(
+    const void* q_source, int32_t q_rows, const void* k_pages, const void* v_pages,
+    const int32_t* block_table, const int32_t* seq_lens, const int32_t* q_indices,
+    const int32_t* out_indices, void* output, int32_t out_rows, void* workspace,
+    size_t workspace_bytes, int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+    int32_t head_dim, int32_t num_pages, int32_t page_size, int32_t max_pages,
+    int32_t bucket_context, int32_t num_splits, float k_scale, float v_scale,
+    const void* k_new, const void* v_new, int32_t dtype, void* stream) {
+  const Geometry g{batch, num_q_heads, num_kv_heads, head_dim, num_pages, page_size, max_pages, dtype};
+  if (batch > 0 && (!k_new || !v_new)) return fail(PKV_ERR_INVALID_ARGUMENT, "k_new or v_new is null");
+  return run_indexed(g, q_source, q_rows, k_pages, v_pages, block_table, seq_lens, q_indices,
+                     out_indices, output, out_rows, workspace, workspace_bytes, bucket_context,
+                     num_splits, stream, KvQuant{true, k_scale, v_scale}, NewToken{k_new, v_new});
+}
+
+int pkv_paged_attention_workqueue_fp8_append(
+    const void* q_source, int32_t q_rows, const void* k_pages, const void* v_pages,
+    const int32_t* block_table, const int32_t* seq_lens, const int32_t* work_items,
+    int32_t num_tasks, const int32_t* split_offsets, int32_t* merge_counters,
+    const int32_t* q_indices, const int32_t* out_indices, void* output, int32_t out_rows,
+    void* workspace, size_t workspace_bytes, int32_t batch, int32_t num_q_heads,
+    int32_t num_kv_heads, int32_t head_dim, int32_t num_pages, int32_t page_size,
+    int32_t max_pages, int32_t bucket_context, int32_t total_partial_slots,
+    int32_t fused_merge, float k_scale, float v_scale, const void* k_new, const void* v_new,
+    int32_t dtype, void* stream) {
+  const QueueCall c{{batch, num_q_heads, num_kv_heads, head_dim, num_pages, page_size, max_pages, dtype},
+                    q_source, k_pages, v_pages, q_rows, block_table, seq_lens, work_items,
+                    split_offsets, q_indices, out_indices, merge_counters, output, out_rows,
+                    workspace, workspace_bytes, bucket_context, num_tasks, total_partial_slots};
+  if (batch > 0 && (!k_new || !v_new)) return fail(PKV_ERR_INVALID_ARGUMENT, "k_new or v_new is null");
+  return run_workqueue(c, fused_merge, (hipStream_t)stream, KvQuant{true, k_scale, v_scale},
+                       NewToken{k_new, v_new});
 }
 
 int pkv_paged_attention_workqueue_fp8(

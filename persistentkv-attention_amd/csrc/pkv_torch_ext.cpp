@@ -191,7 +191,16 @@ void indexed_op(torch::Tensor q_source, torch::Tensor k_pages, torch::Tensor v_p
   const int32_t no = i32(output.size(0), "output.size(0)");
   const int32_t np = i32(k_pages.size(0), "k_pages.size(0)");
   const int32_t mp = i32(block_table.size(1), "block_table.size(1)");
-  if (k_new) {
+  if (k_new && kv_fp8) {
+    check_new_token(*k_new, *v_new, dt, B, Hkv);
+    raise_on(pkv_paged_attention_indexed_fp8_append(
+        q_source.data_ptr(), nq, k_pages.data_ptr(), v_pages.data_ptr(), block_table.data_ptr<int>(),
+        seq_lens.data_ptr<int>(), q_indices.data_ptr<int>(), out_indices.data_ptr<int>(),
+        output.data_ptr(), no, ws_ptr(workspace), ws_bytes(workspace), B, Hq, Hkv, d, np,
+        i32(page_size, "page_size"), mp, i32(bucket_context, "bucket_context"),
+        i32(num_splits, "num_splits"), (float)k_scale, (float)v_scale, k_new->data_ptr(),
+        v_new->data_ptr(), pkv_dtype_of(dt), stream_of(q_source)));
+  } else if (k_new) {
     check_new_token(*k_new, *v_new, dt, B, Hkv);
     raise_on(pkv_paged_attention_indexed_append(
         q_source.data_ptr(), nq, k_pages.data_ptr(), v_pages.data_ptr(), block_table.data_ptr<int>(),
@@ -329,7 +338,18 @@ void workqueue_op(torch::Tensor q_source, torch::Tensor k_pages, torch::Tensor v
   const int32_t np = i32(k_pages.size(0), "k_pages.size(0)");
   const int32_t mp = i32(block_table.size(1), "block_table.size(1)");
   int32_t* counters = fused_merge ? merge_counters.data_ptr<int>() : nullptr;
-  if (k_new) {
+  if (k_new && kv_fp8) {
+    check_new_token(*k_new, *v_new, t.dt, t.B, t.Hkv);
+    raise_on(pkv_paged_attention_workqueue_fp8_append(
+        q_source.data_ptr(), nq, k_pages.data_ptr(), v_pages.data_ptr(), block_table.data_ptr<int>(),
+        seq_lens.data_ptr<int>(), work_items.data_ptr<int>(), nt, split_offsets.data_ptr<int>(),
+        counters, q_indices.data_ptr<int>(), out_indices.data_ptr<int>(), output.data_ptr(), no,
+        ws_ptr(workspace), ws_bytes(workspace), t.B, t.Hq, t.Hkv, t.d, np,
+        i32(page_size, "page_size"), mp, i32(bucket_context, "bucket_context"),
+        i32(total_partial_slots, "total_partial_slots"), fused_merge ? 1 : 0, (float)k_scale,
+        (float)v_scale, k_new->data_ptr(), v_new->data_ptr(), pkv_dtype_of(t.dt),
+        stream_of(q_source)));
+  } else if (k_new) {
     check_new_token(*k_new, *v_new, t.dt, t.B, t.Hkv);
     raise_on(pkv_paged_attention_workqueue_append(
         q_source.data_ptr(), nq, k_pages.data_ptr(), v_pages.data_ptr(), block_table.data_ptr<int>(),
@@ -385,6 +405,18 @@ void persistentkv_paged_attention_workqueue_fp8(
                page_size, total_partial_slots, fused_merge, true, k_scale, v_scale);
 }
 
+// The fp8-K/V indexed op with the append fused in: equals append_kv_fp8(k_new, v_new, ...,
+// k_scale, v_scale) followed by paged_attention_indexed_fp8.
+void persistentkv_paged_attention_indexed_fp8_append(
+    torch::Tensor q_source, torch::Tensor k_pages, torch::Tensor v_pages, torch::Tensor block_table,
+    torch::Tensor seq_lens, torch::Tensor q_indices, torch::Tensor out_indices,
+    torch::Tensor output, torch::Tensor workspace, int64_t bucket_context, int64_t page_size,
+    int64_t num_splits, double k_scale, double v_scale, torch::Tensor k_new, torch::Tensor v_new) {
+  indexed_op(q_source, k_pages, v_pages, block_table, seq_lens, q_indices, out_indices, output,
+             workspace, bucket_context, page_size, num_splits, true, k_scale, v_scale, &k_new,
+             &v_new);
+}
+
 // The work-queue op with the KV append fused in (as paged_attention_indexed_append).
 void persistentkv_paged_attention_workqueue_append(
     torch::Tensor q_source, torch::Tensor k_pages, torch::Tensor v_pages, torch::Tensor block_table,
@@ -395,6 +427,19 @@ void persistentkv_paged_attention_workqueue_append(
   workqueue_op(q_source, k_pages, v_pages, block_table, seq_lens, work_items, split_offsets,
                merge_counters, q_indices, out_indices, output, workspace, bucket_context,
                page_size, total_partial_slots, fused_merge, false, 1.0, 1.0, &k_new, &v_new);
+}
+
+// The fp8-K/V work-queue op with the KV append fused in.
+void persistentkv_paged_attention_workqueue_fp8_append(
+    torch::Tensor q_source, torch::Tensor k_pages, torch::Tensor v_pages, torch::Tensor block_table,
+    torch::Tensor seq_lens, torch::Tensor work_items, torch::Tensor split_offsets,
+    torch::Tensor merge_counters, torch::Tensor q_indices, torch::Tensor out_indices,
+    torch::Tensor output, torch::Tensor workspace, int64_t bucket_context, int64_t page_size,
+    int64_t total_partial_slots, bool fused_merge, double k_scale, double v_scale,
+    torch::Tensor k_new, torch::Tensor v_new) {
+  workqueue_op(q_source, k_pages, v_pages, block_table, seq_lens, work_items, split_offsets,
+               merge_counters, q_indices, out_indices, output, workspace, bucket_context,
+               page_size, total_partial_slots, fused_merge, true, k_scale, v_scale, &k_new, &v_new);
 }
 
 namespace {
@@ -604,6 +649,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "paged_attention_indexed with the KV append fused in (k_new, v_new)");
   m.def("paged_attention_workqueue_append", &persistentkv_paged_attention_workqueue_append,
         "paged_attention_workqueue with the KV append fused in (k_new, v_new)");
+  m.def("paged_attention_indexed_fp8_append", &persistentkv_paged_attention_indexed_fp8_append,
+        "paged_attention_indexed_fp8 with the KV append fused in (k_new, v_new)");
+  m.def("paged_attention_workqueue_fp8_append", &persistentkv_paged_attention_workqueue_fp8_append,
+        "paged_attention_workqueue_fp8 with the KV append fused in (k_new, v_new)");
   m.def("append_kv", &persistentkv_append_kv,
         "write each row's newest token's K/V into its tail page (position seq_lens - 1)");
   m.def("append_kv_fp8", &persistentkv_append_kv_fp8,

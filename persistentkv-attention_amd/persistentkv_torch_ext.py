@@ -59,6 +59,10 @@ append_kv_fp8 = _ext.append_kv_fp8
 # arguments followed by k_new, v_new; same result as append_kv then the op.
 paged_attention_indexed_append = _ext.paged_attention_indexed_append
 paged_attention_workqueue_append = _ext.paged_attention_workqueue_append
+# The fp8-K/V ops with the append fused in: (..., k_scale, v_scale, k_new, v_new); the new
+# token is stored as append_kv_fp8 stores it.
+paged_attention_indexed_fp8_append = _ext.paged_attention_indexed_fp8_append
+paged_attention_workqueue_fp8_append = _ext.paged_attention_workqueue_fp8_append
 
 HEAD_DIM = 128
 TILE_TOKENS = 32
@@ -80,6 +84,7 @@ __all__ = [
     "paged_attention_indexed_fp8", "paged_attention_workqueue_fp8", "workqueue_decode_fp8",
     "attention_contiguous",
     "attention_query_head_baseline", "append_kv", "append_kv_fp8",
-    "paged_attention_indexed_append", "paged_attention_workqueue_append", "workspace_floats",
+    "paged_attention_indexed_append", "paged_attention_workqueue_append",
+    "paged_attention_indexed_fp8_append", "paged_attention_workqueue_fp8_append", "workspace_floats",
     "workqueue_workspace_floats", "EXTENSION_PATH", "LIBRARY_PATH",
 ]

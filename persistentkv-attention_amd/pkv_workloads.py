@@ -402,13 +402,24 @@ def run_step(ext, w: Workload, meta: StepMeta, step_index: int, q_pool, k_pages,
              workspace, new_kv=None):
     """One decode step through the op the workload names; returns ``meta.output``.
     ``new_kv`` = (k_new, v_new) of the step's rows runs the op's *_append variant, which
-    also writes them into the pools (2-byte pools, indexed and work-queue ops)."""
+    also writes them into the pools (indexed and work-queue ops)."""
     q_source = q_pool[step_index]
     if new_kv is not None:
-        if w.kv_fp8 or meta.op not in ("paged_attention_workqueue", "paged_attention_indexed"):
-            raise ValueError(f"the fused append is provided for the 2-byte work-queue and "
-                             f"indexed ops, not {meta.op}{' with fp8 K/V' if w.kv_fp8 else ''}")
-        if meta.op == "paged_attention_workqueue":
+        if meta.op not in ("paged_attention_workqueue", "paged_attention_indexed"):
+            raise ValueError(f"the fused append is provided for the work-queue and indexed "
+                             f"ops, not {meta.op}")
+        if meta.op == "paged_attention_workqueue" and w.kv_fp8:
+            ext.paged_attention_workqueue_fp8_append(
+                q_source, k_pages, v_pages, meta.block_table, meta.seq_lens, meta.work_items,
+                meta.split_offsets, meta.merge_counters, meta.q_indices, meta.out_indices,
+                meta.output, workspace, meta.bucket_length, w.page_size, meta.total_partial_slots,
+                w.fused_merge, w.k_scale, w.v_scale, new_kv[0], new_kv[1])
+        elif meta.op == "paged_attention_indexed" and w.kv_fp8:
+            ext.paged_attention_indexed_fp8_append(
+                q_source, k_pages, v_pages, meta.block_table, meta.seq_lens, meta.q_indices,
+                meta.out_indices, meta.output, workspace, meta.bucket_length, w.page_size,
+                meta.splits, w.k_scale, w.v_scale, new_kv[0], new_kv[1])
+        elif meta.op == "paged_attention_workqueue":
             ext.paged_attention_workqueue_append(
                 q_source, k_pages, v_pages, meta.block_table, meta.seq_lens, meta.work_items,
                 meta.split_offsets, meta.merge_counters, meta.q_indices, meta.out_indices,

@@ -292,3 +292,53 @@ def test_fused_append_validation(ext, gpu):
     with pytest.raises(RuntimeError, match="wrong dtype"):
         ext.paged_attention_indexed_append(q, k, v, bt, sl, idx, idx, out, ws, 64, 16, 1,
                                            kn.to(BF16), kn.to(BF16))
+
+
+@pytest.mark.parametrize("op", ["indexed", "workqueue"])
+@pytest.mark.parametrize("dtype,hkv", [(F16, 8), (BF16, 4), (F16, 1)])  # G = 4, 8, 32
+def test_fused_append_fp8_equals_append_then_decode(ext, gpu, op, dtype, hkv):
+    """The fp8-K/V ops with the append fused in store the e4m3 bytes of append_kv_fp8 and
+    give the output of append_kv_fp8 followed by the fp8 op, bit for bit (G = 32 takes the
+    separate append kernel inside the op)."""
+    lengths, hq, ps, ks, vs = [700, 33, 1, 129], 32, 16, 0.05, 0.03
+    b = len(lengths)
+    case = make_case(lengths, hq, hkv, ps, F16, seed=hkv + 40)
+    k8 = (case.k_pages.float() / ks).clamp(-448, 448).to(F8)
+    v8 = (case.v_pages.float() / vs).clamp(-448, 448).to(F8)
+    q = case.q.to(dtype).to(gpu)
+    kn, vn = (t.to(gpu) for t in _new_tokens(b, hkv, dtype, seed=hkv))
+    bt, sl = case.block_table.to(gpu), case.seq_lens.to(gpu)
+    results = []
+    for fused in (False, True):
+        k, v = k8.to(gpu), v8.to(gpu)
+        out = torch.full((b, hq, 128), float("nan"), dtype=dtype, device=gpu)
+        if op == "indexed":
+            idx = torch.arange(b, dtype=torch.int32, device=gpu)
+            ws = torch.empty(b * hq * 3 * 130, dtype=torch.float32, device=gpu)
+            args = (q, k, v, bt, sl, idx, idx, out, ws, max(lengths), ps, 3, ks, vs)
+            if fused:
+                ext.paged_attention_indexed_fp8_append(*args, kn, vn)
+            else:
+                ext.append_kv_fp8(kn, vn, k, v, bt, sl, ks, vs)
+                ext.paged_attention_indexed_fp8(*args)
+        else:
+            meta = pkv_native.build_workqueue(lengths, list(range(b)), case.page_lists, ps, 5,
+                                              False, hkv)
+            t = lambda a: torch.as_tensor(a, dtype=torch.int32, device=gpu)
+            slots = meta["total_partial_slots"]
+            ws = torch.empty(slots * hq * 130, dtype=torch.float32, device=gpu)
+            counters = torch.zeros(b, hkv, dtype=torch.int32, device=gpu)
+            args = (q, k, v, t(meta["block_table"]), t(meta["seq_lens"]), t(meta["work_items"]),
+                    t(meta["split_offsets"]), counters, t(meta["q_indices"]),
+                    t(meta["out_indices"]), out, ws, meta["bucket_length"], ps, slots, False, ks, vs)
+            if fused:
+                ext.paged_attention_workqueue_fp8_append(*args, kn, vn)
+            else:
+                ext.append_kv_fp8(kn, vn, k, v, t(meta["block_table"]), t(meta["seq_lens"]), ks, vs)
+                ext.paged_attention_workqueue_fp8(*args)
+        torch.cuda.synchronize()
+        results.append((out.cpu(), k.cpu().view(torch.uint8), v.cpu().view(torch.uint8)))
+    (o1, k1, v1), (o2, k2, v2) = results
+    assert torch.equal(k2, k1) and torch.equal(v2, v1)
+    assert not torch.equal(k2, k8.view(torch.uint8))  # the append wrote
+    assert torch.equal(o2, o1)
