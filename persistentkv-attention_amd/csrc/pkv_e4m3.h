@@ -1,5 +1,5 @@
-// pkv_e4m3.h — the OCP fp8 e4m3 encode shared by the KV append kernel and the decode's
-// fused append, so both store the same bytes.
+// pkv_e4m3.h — the OCP fp8 e4m3 encode of the KV append into fp8 pools (the bytes of
+// torch's float8_e4m3fn cast), kept in one place for any kernel that stores fp8 K/V.
 #pragma once
 
 #include <hip/hip_runtime.h>
