@@ -26,6 +26,15 @@ int ok();
 namespace {
 
 constexpr int kD = 128;
+constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit data format (gfx9 family)
+
+// A pointer that is the same in every lane of the wave, as buffer descriptors need.
+__device__ inline void* wave_ptr(const void* p) {
+  const uint64_t v = (uint64_t)p;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+  return (void*)(((uint64_t)hi << 32) | lo);
+}
 
 struct AppendArgs {
   const uint8_t* k_new;   // [B, Hkv, 128], 2-byte elements
@@ -45,22 +54,32 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
   const int lane = threadIdx.x & 63;
   if (wave_id >= a.batch * a.hkv) return;
   const int row = wave_id / a.hkv, h = wave_id - row * a.hkv;
-  const int pos = a.seq_lens[row] - 1;
-  if (pos < 0) return;
-  const int logical = pos / a.page_size;
-  if (logical >= a.max_pages) return;
-  const int page = a.block_table[(long)row * a.max_pages + logical];
-  if (page < 0 || page >= a.num_pages) return;
+  // Straight-line code with no early return, so that the new token's loads stay ahead of
+  // (and overlap) the dependent seq_lens -> block_table reads that place it.  A skipped
+  // row stores through a descriptor of 0 bytes, which the hardware drops.
   const long src = ((long)row * a.hkv + h) * kD + 2 * lane;  // element index
-  const long dst = (((long)page * a.hkv + h) * a.page_size + pos % a.page_size) * kD + 2 * lane;
   const uint32_t k2 = *(const uint32_t*)(a.k_new + src * 2);
   const uint32_t v2 = *(const uint32_t*)(a.v_new + src * 2);
+  const int pos = a.seq_lens[row] - 1;
+  const int logical = pos < 0 ? 0 : pos / a.page_size;
+  const bool in_table = pos >= 0 && logical < a.max_pages;
+  const int page = a.block_table[(long)row * a.max_pages + (in_table ? logical : 0)];
+  const bool valid = in_table && page >= 0 && page < a.num_pages;
+  constexpr int kElem = FP8 ? 1 : 2;
+  const long slot = valid ? (((long)page * a.hkv + h) * a.page_size + pos % a.page_size) * kD : 0;
+  const int nrec = __builtin_amdgcn_readfirstlane(valid ? kD * kElem : 0);
+  const __amdgpu_buffer_rsrc_t rk =
+      __builtin_amdgcn_make_buffer_rsrc(wave_ptr(a.k_pages + slot * kElem), (short)0, nrec, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rv =
+      __builtin_amdgcn_make_buffer_rsrc(wave_ptr(a.v_pages + slot * kElem), (short)0, nrec, kRsrcWord3);
   if constexpr (FP8) {
-    *(uint16_t*)(a.k_pages + dst) = (uint16_t)pkv::e4m3_pack2<BF16_IN>(k2, a.k_scale);
-    *(uint16_t*)(a.v_pages + dst) = (uint16_t)pkv::e4m3_pack2<BF16_IN>(v2, a.v_scale);
+    __builtin_amdgcn_raw_buffer_store_b16((uint16_t)pkv::e4m3_pack2<BF16_IN>(k2, a.k_scale), rk,
+                                          lane * 2, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b16((uint16_t)pkv::e4m3_pack2<BF16_IN>(v2, a.v_scale), rv,
+                                          lane * 2, 0, 0);
   } else {
-    *(uint32_t*)(a.k_pages + dst * 2) = k2;
-    *(uint32_t*)(a.v_pages + dst * 2) = v2;
+    __builtin_amdgcn_raw_buffer_store_b32(k2, rk, lane * 4, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(v2, rv, lane * 4, 0, 0);
   }
 }
 
