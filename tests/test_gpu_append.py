@@ -146,10 +146,11 @@ def test_append_validation(ext, gpu):
         ext.append_kv_fp8(kn, kn, k, v, bt, sl, 1.0, 1.0)
 
 
-def test_append_then_decode_in_a_hip_graph(ext, gpu):
-    """append_kv + the masked op captured in one HIP graph and replayed several times,
-    with eager work (pool reset, output clear) between replays: every replay gives the
-    eager result."""
+@pytest.mark.parametrize("fused", [False, True])
+def test_append_then_decode_in_a_hip_graph(ext, gpu, fused):
+    """append_kv + the masked op (or the fused paged_attention_indexed_append) captured in
+    one HIP graph and replayed several times, with eager work (pool reset, output clear)
+    between replays: every replay gives the eager result."""
     lengths = [700, 33, 129]
     case = make_case(lengths, 32, 8, 16, F16, seed=21)
     gen = torch.Generator().manual_seed(22)
@@ -161,9 +162,15 @@ def test_append_then_decode_in_a_hip_graph(ext, gpu):
     out = torch.zeros(3, 32, 128, dtype=F16, device=gpu)
     ws = torch.empty(3 * 32 * 4 * 130, dtype=torch.float32, device=gpu)
 
+    idx = torch.arange(3, dtype=torch.int32, device=gpu)
+
     def step():
-        ext.append_kv(kn, vn, k, v, bt, sl)
-        ext.paged_attention_masked(q, k, v, bt, sl, out, ws, max(lengths), 16, 4)
+        if fused:
+            ext.paged_attention_indexed_append(q, k, v, bt, sl, idx, idx, out, ws, max(lengths),
+                                               16, 4, kn, vn)
+        else:
+            ext.append_kv(kn, vn, k, v, bt, sl)
+            ext.paged_attention_masked(q, k, v, bt, sl, out, ws, max(lengths), 16, 4)
 
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
