@@ -57,7 +57,7 @@ def parse_args():
                    help="minimum KV pool replicas (cold-cache basis; raised for small steps)")
     p.add_argument("--workload", default="c4", choices=sorted(WORKLOAD_NAMES),
                    help="configuration (default c4, the headline; the others are reported "
-                        "for DESIGN.md and are not the metric)")
+                        "for the design notes and are not the metric)")
     p.add_argument("--fused-merge", action="store_true", help="single-launch fused merge variant")
     p.add_argument("--kv-fp8", action="store_true",
                    help="K/V pages in fp8 (OCP e4m3) with per-tensor scales (work-queue and "
@@ -107,7 +107,7 @@ def main():
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the engine has no multi-GPU path in this build "
-              "(see DESIGN.md for how it would shard); run with --gpus 1", file=sys.stderr)
+              "(units are independent and would shard by KV head or row); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     import torch
