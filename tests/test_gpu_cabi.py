@@ -1,9 +1,9 @@
 """Parity through the bare C ABI (libpkv.so via ctypes), without the torch extension.
 
-Binds the entry points with the ctypes argument lists a non-torch caller uses and checks the work-queue
-and grid ops against the repack + fp32 SDPA oracle (max-abs 2e-3, mean-abs 3e-4), and
-that an inconsistent argument returns PKV_ERR_INVALID_ARGUMENT with a message instead of
-launching.
+Binds the entry points with the ctypes argument lists a non-torch caller uses, and checks
+the work-queue and grid ops against the repack + fp32 SDPA oracle (max-abs 2e-3, mean-abs
+3e-4) and that an inconsistent argument returns PKV_ERR_INVALID_ARGUMENT with a message
+instead of launching.
 """
 import ctypes
 
