@@ -245,11 +245,13 @@ def test_fused_append_indexed_equals_append_then_decode(ext, gpu, lengths, hq, h
 
 
 @pytest.mark.parametrize("fused_merge", [False, True])
-@pytest.mark.parametrize("lengths,hkv,dtype", [([40, 700, 1500, 33], 8, F16),
-                                               ([3000, 65, 900], 1, BF16)])
-def test_fused_append_workqueue_equals_append_then_decode(ext, gpu, lengths, hkv, dtype,
+@pytest.mark.parametrize("lengths,hkv,dtype,ps", [([40, 700, 1500, 33], 8, F16, 16),
+                                                  ([3000, 65, 900], 1, BF16, 16),
+                                                  ([500, 2100, 64, 97], 4, BF16, 32),
+                                                  ([300, 41], 8, F16, 8)])  # page 8: two launches
+def test_fused_append_workqueue_equals_append_then_decode(ext, gpu, lengths, hkv, dtype, ps,
                                                           fused_merge):
-    hq, ps = 32, 16
+    hq = 32
     case = make_case(lengths, hq, hkv, ps, dtype, seed=len(lengths) + hkv)
     meta = pkv_native.build_workqueue(lengths, list(range(len(lengths))), case.page_lists, ps, 6,
                                       False, hkv)
