@@ -353,6 +353,15 @@ int pkv_append_kv_fp8(const void* k_new, const void* v_new, void* k_pages, void*
  * pkv_append_kv first on the same stream.  (fp8 pools: the *_fp8_append entries below.)  A row's tail slot must not be read
  * through another (row, position) of the same step (no two rows share a tail page, as
  * in any copy-on-write cache).  No counterpart in the reference (see pkv_append_kv). */
+int pkv_paged_attention_masked_append(
+    const void* q, const void* k_pages, const void* v_pages,
+    const int32_t* block_table, const int32_t* seq_lens, void* output,
+    void* workspace, size_t workspace_bytes,
+    int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t num_pages, int32_t page_size, int32_t max_pages,
+    int32_t bucket_context, int32_t num_splits, const void* k_new, const void* v_new,
+    int32_t dtype, void* stream);
+
 int pkv_paged_attention_indexed_append(
     const void* q_source, int32_t q_rows,
     const void* k_pages, const void* v_pages,

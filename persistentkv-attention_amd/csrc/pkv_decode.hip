@@ -2175,6 +2175,20 @@ int pkv_paged_attention_workqueue(
   return run_workqueue(c, fused_merge, (hipStream_t)stream, KvQuant{});
 }
 
+int pkv_paged_attention_masked_append(
+    const void* q, const void* k_pages, const void* v_pages, const int32_t* block_table,
+    const int32_t* seq_lens, void* output, void* workspace, size_t workspace_bytes,
+    int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t num_pages, int32_t page_size, int32_t max_pages, int32_t bucket_context,
+    int32_t num_splits, const void* k_new, const void* v_new, int32_t dtype, void* stream) {
+  if (batch > 0 && !seq_lens) return fail(PKV_ERR_INVALID_ARGUMENT, "seq_lens is null");
+  if (batch > 0 && (!k_new || !v_new)) return fail(PKV_ERR_INVALID_ARGUMENT, "k_new or v_new is null");
+  const Geometry g{batch, num_q_heads, num_kv_heads, head_dim, num_pages, page_size, max_pages, dtype};
+  return run_grid(g, q, batch, k_pages, v_pages, block_table, seq_lens, nullptr, nullptr, output,
+                  batch, workspace, workspace_bytes, bucket_context, num_splits, stream, KvQuant{},
+                  NewToken{k_new, v_new});
+}
+
 int pkv_paged_attention_indexed_append(
     const void* q_source, int32_t q_rows, const void* k_pages, const void* v_pages,
     const int32_t* block_table, const int32_t* seq_lens, const int32_t* q_indices,

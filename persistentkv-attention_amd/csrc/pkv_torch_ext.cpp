@@ -106,12 +106,41 @@ void persistentkv_paged_attention(torch::Tensor q, torch::Tensor k_pages, torch:
       i32(num_splits, "num_splits"), pkv_dtype_of(dt), stream_of(q)));
 }
 
+namespace {
+void masked_op(torch::Tensor q, torch::Tensor k_pages, torch::Tensor v_pages,
+               torch::Tensor block_table, torch::Tensor seq_lens, torch::Tensor output,
+               torch::Tensor workspace, int64_t bucket_context, int64_t page_size,
+               int64_t num_splits, const torch::Tensor* k_new, const torch::Tensor* v_new);
+}  // namespace
+
 // tests/persistentkv_torch_extension.cu:95-157
 void persistentkv_paged_attention_masked(torch::Tensor q, torch::Tensor k_pages,
                                          torch::Tensor v_pages, torch::Tensor block_table,
                                          torch::Tensor seq_lens, torch::Tensor output,
                                          torch::Tensor workspace, int64_t bucket_context,
                                          int64_t page_size, int64_t num_splits) {
+  masked_op(q, k_pages, v_pages, block_table, seq_lens, output, workspace, bucket_context,
+            page_size, num_splits, nullptr, nullptr);
+}
+
+// The masked op with the KV append fused in (as paged_attention_indexed_append).
+void persistentkv_paged_attention_masked_append(
+    torch::Tensor q, torch::Tensor k_pages, torch::Tensor v_pages, torch::Tensor block_table,
+    torch::Tensor seq_lens, torch::Tensor output, torch::Tensor workspace,
+    int64_t bucket_context, int64_t page_size, int64_t num_splits, torch::Tensor k_new,
+    torch::Tensor v_new) {
+  masked_op(q, k_pages, v_pages, block_table, seq_lens, output, workspace, bucket_context,
+            page_size, num_splits, &k_new, &v_new);
+}
+
+namespace {
+void check_new_token(const torch::Tensor& k_new, const torch::Tensor& v_new, at::ScalarType dt,
+                     int64_t B, int64_t Hkv);
+
+void masked_op(torch::Tensor q, torch::Tensor k_pages, torch::Tensor v_pages,
+               torch::Tensor block_table, torch::Tensor seq_lens, torch::Tensor output,
+               torch::Tensor workspace, int64_t bucket_context, int64_t page_size,
+               int64_t num_splits, const torch::Tensor* k_new, const torch::Tensor* v_new) {
   const auto dt = activation_dtype(q, "q");
   check_tensor(q, "q", dt, 3);
   check_tensor(k_pages, "k_pages", dt, 4);
@@ -133,6 +162,17 @@ void persistentkv_paged_attention_masked(torch::Tensor q, torch::Tensor k_pages,
   TORCH_CHECK(page_size > 0, "page_size must be positive");
   TORCH_CHECK(num_splits > 0, "num_splits must be positive");
   const c10::DeviceGuard guard(q.device());
+  if (k_new) {
+    check_new_token(*k_new, *v_new, dt, B, Hkv);
+    raise_on(pkv_paged_attention_masked_append(
+        q.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(), block_table.data_ptr<int>(),
+        seq_lens.data_ptr<int>(), output.data_ptr(), ws_ptr(workspace), ws_bytes(workspace), B,
+        Hq, Hkv, d, i32(k_pages.size(0), "k_pages.size(0)"), i32(page_size, "page_size"),
+        i32(block_table.size(1), "block_table.size(1)"), i32(bucket_context, "bucket_context"),
+        i32(num_splits, "num_splits"), k_new->data_ptr(), v_new->data_ptr(), pkv_dtype_of(dt),
+        stream_of(q)));
+    return;
+  }
   raise_on(pkv_paged_attention_masked(
       q.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(), block_table.data_ptr<int>(),
       seq_lens.data_ptr<int>(), output.data_ptr(), ws_ptr(workspace), ws_bytes(workspace), B, Hq,
@@ -140,6 +180,7 @@ void persistentkv_paged_attention_masked(torch::Tensor q, torch::Tensor k_pages,
       i32(block_table.size(1), "block_table.size(1)"), i32(bucket_context, "bucket_context"),
       i32(num_splits, "num_splits"), pkv_dtype_of(dt), stream_of(q)));
 }
+}  // namespace
 
 namespace {
 
@@ -645,6 +686,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "Work-queue decode stage over fp8 (e4m3) K/V pages");
   m.def("attention_contiguous", &persistentkv_attention_contiguous,
         "GQA decode over contiguous K/V [B, Hkv, N, 128]");
+  m.def("paged_attention_masked_append", &persistentkv_paged_attention_masked_append,
+        "paged_attention_masked with the KV append fused in (k_new, v_new)");
   m.def("paged_attention_indexed_append", &persistentkv_paged_attention_indexed_append,
         "paged_attention_indexed with the KV append fused in (k_new, v_new)");
   m.def("paged_attention_workqueue_append", &persistentkv_paged_attention_workqueue_append,

@@ -55,8 +55,9 @@ attention_query_head_baseline = _ext.attention_query_head_baseline
 # (fp8 pools store e4m3(x / scale), rounded to nearest even).
 append_kv = _ext.append_kv
 append_kv_fp8 = _ext.append_kv_fp8
-# The indexed and work-queue ops with that append fused in (2-byte pools): the op's
+# The masked, indexed and work-queue ops with that append fused in (2-byte pools): the op's
 # arguments followed by k_new, v_new; same result as append_kv then the op.
+paged_attention_masked_append = _ext.paged_attention_masked_append
 paged_attention_indexed_append = _ext.paged_attention_indexed_append
 paged_attention_workqueue_append = _ext.paged_attention_workqueue_append
 # The fp8-K/V ops with the append fused in: (..., k_scale, v_scale, k_new, v_new); the new
@@ -84,7 +85,8 @@ __all__ = [
     "paged_attention_indexed_fp8", "paged_attention_workqueue_fp8", "workqueue_decode_fp8",
     "attention_contiguous",
     "attention_query_head_baseline", "append_kv", "append_kv_fp8",
-    "paged_attention_indexed_append", "paged_attention_workqueue_append",
+    "paged_attention_masked_append", "paged_attention_indexed_append",
+    "paged_attention_workqueue_append",
     "paged_attention_indexed_fp8_append", "paged_attention_workqueue_fp8_append", "workspace_floats",
     "workqueue_workspace_floats", "EXTENSION_PATH", "LIBRARY_PATH",
 ]

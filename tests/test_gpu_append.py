@@ -214,8 +214,9 @@ FUSED_INDEXED = [
 @pytest.mark.parametrize("lengths,hq,hkv,ps,splits,dtype", FUSED_INDEXED)
 def test_fused_append_indexed_equals_append_then_decode(ext, gpu, lengths, hq, hkv, ps, splits,
                                                         dtype):
-    """paged_attention_indexed_append gives bit for bit the output and the pools of
-    append_kv followed by paged_attention_indexed, and matches the oracle."""
+    """paged_attention_indexed_append (and paged_attention_masked_append) give bit for bit
+    the output and the pools of append_kv followed by paged_attention_indexed, and match
+    the oracle."""
     b = len(lengths)
     case = make_case(lengths, hq, hkv, ps, dtype, seed=sum(lengths) + ps, q_rows=b + 1)
     kn, vn = _new_tokens(b, hkv, dtype, seed=len(lengths))
@@ -242,6 +243,15 @@ def test_fused_append_indexed_equals_append_then_decode(ext, gpu, lengths, hq, h
     ref = oracle.paged_decode(case.q, k_ref, v_ref, case.block_table, case.seq_lens,
                               qi.cpu(), oi.cpu())
     assert_parity(out2, ref)
+    # The masked op with the append: query row b, output row b.
+    k3, v3 = case.k_pages.to(gpu), case.v_pages.to(gpu)
+    out3 = torch.full((b, hq, 128), float("nan"), dtype=dtype, device=gpu)
+    qm = q.index_select(0, qi.long()).contiguous()
+    ext.paged_attention_masked_append(qm, k3, v3, bt, sl, out3, ws, bucket, ps, splits,
+                                      kn.to(gpu), vn.to(gpu))
+    torch.cuda.synchronize()
+    assert torch.equal(k3, k1) and torch.equal(v3, v1)
+    assert torch.equal(out3, out1)
 
 
 @pytest.mark.parametrize("fused_merge", [False, True])
