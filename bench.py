@@ -4,7 +4,10 @@ Workload: bimodal continuous-batching trace, 24 request
 max-active 8, 48 decode steps, Hq 32 / Hkv 8 (G=4), D 128, fp16, page 16, 20 fixed
 work-queue splits with metadata precomputed by the host builder.  One "step" is one
 ``paged_attention_workqueue`` call (decode kernel + LSE merge) over one decode step of
-the trace; timed step k replays trace step k mod 48.
+the trace.  The K timed steps are one sample of the trace: whole passes when K is a
+multiple of its 48 steps (the default K = 96 is two), otherwise K evenly spaced trace
+steps (timed step k replays trace step k * 48 // K).  Every figure of the line (value,
+roofline, traffic, mean_kv_mb_per_step) is taken over that same sample.
 
 Cache basis: the KV pool is replicated ``--rotations`` times and consecutive timed steps
 read different replicas, so a step's pages have been evicted from the 256 MB Infinity
@@ -15,7 +18,12 @@ Reported (one JSON line):
                bytes: sum of active lengths * Hkv * 128 * 2 (K,V) * 2 bytes per step,
                the reference's useful_kv_mb_for_state, tests/benchmark_serving_trace.py:511-513)
   ms_per_step  mean wall time per step between the synchronised bracket points
-  roofline     decode kernel alone, timed with HIP events on its launch stream
+  roofline     decode kernel alone over the same sample, timed with HIP events on its
+               launch stream; traffic = the rocprofv3 FETCH_SIZE + WRITE_SIZE ratio to
+               algorithmic bytes (profiles/c4_decode_traffic.json) x the sample's bytes
+  gate         one sampled step of the timed op checked against a torch fp32 SDPA of the
+               same inputs on the GPU, outside the timed region (max-abs 2e-3, mean-abs
+               3e-4; the run fails otherwise)
   cpu_baseline repack + fp32 SDPA (the reference's CPU path, restated in oracle/) on a
                bounded sample of the same steps on the host cores
 """
@@ -81,7 +89,10 @@ def cpu_baseline(w, q_pool_cpu, k_cpu, v_cpu, metas, budget_s):
 
     from oracle import attention as oracle
 
-    threads = max(1, min(16, os.cpu_count() or 1))
+    host_cores = os.cpu_count() or 1
+    # The GPU box allots 16 host cores to a one-GPU job (OMP_NUM_THREADS is set to that
+    # share there); use them all, and no more than the host has.
+    threads = max(1, min(host_cores, int(os.environ.get("OMP_NUM_THREADS", host_cores))))
     torch.set_num_threads(threads)
     done_bytes, elapsed, steps = 0, 0.0, 0
     for i, meta in enumerate(metas):
@@ -98,9 +109,29 @@ def cpu_baseline(w, q_pool_cpu, k_cpu, v_cpu, metas, budget_s):
         if elapsed >= budget_s:
             break
     return {"value": round(done_bytes / elapsed / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": "port",
+            "kind": "port", "host_cores": host_cores, "cpu_model": cpu_model(),
             "sample": f"trace steps 0..{steps - 1} of {w.name} ({done_bytes / 1e6:.0f} MB of KV), "
-                      f"{elapsed / steps * 1e3:.1f} ms/step, torch CPU SDPA fp32"}
+                      f"{elapsed / steps * 1e3:.1f} ms/step, torch CPU SDPA fp32 on {threads} "
+                      f"threads"}
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def trace_sample(steps, n_trace):
+    """Trace step replayed by each timed step: whole passes when ``steps`` is a multiple
+    of the trace length, else ``steps`` evenly spaced trace steps."""
+    if steps % n_trace == 0:
+        return [k % n_trace for k in range(steps)]
+    return [(k * n_trace) // steps for k in range(steps)]
 
 
 def main():
@@ -109,10 +140,14 @@ def main():
         print("bench.py measures one GPU: the engine has no multi-GPU path in this build "
               "(units are independent and would shard by KV head or row); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.steps <= 0:
+        print("--steps must be positive", file=sys.stderr)
+        sys.exit(2)
 
     import torch
 
     import persistentkv_torch_ext as ext
+    import pkv_serving as serving
     import pkv_workloads as wl
 
     dev = torch.device("cuda:0")
@@ -128,22 +163,24 @@ def main():
     q_pool = wl.make_q_pool(w, dev)
     wl.bind_queries(metas, q_pool)
     k0, v0 = wl.make_kv_pool(w, dev)
+    n_trace = len(w.steps)
+    sample = trace_sample(args.steps, n_trace)
+    sample_bytes = [metas[i].kv_bytes for i in sample]
     # Enough replicas that the bytes read between two uses of one replica exceed twice the
     # 256 MB Infinity Cache (at most 48 GB of replicas).
-    mean_bytes = sum(m.kv_bytes for m in metas) / len(metas)
+    mean_bytes = sum(sample_bytes) / len(sample_bytes)
     pool_bytes = 2 * k0.numel() * k0.element_size()
     rotations = max(args.rotations, -(-2 * MALL_BYTES // int(mean_bytes)) + 1)
     rotations = max(2, min(rotations, int(48e9 // pool_bytes)))
     pools = [(k0, v0)] + [(k0.clone(), v0.clone()) for _ in range(rotations - 1)]
     torch.cuda.synchronize()
-    n_trace = len(w.steps)
 
     # New-token K/V of every trace step, drawn once and kept on the GPU.
     appends = ([tuple(t.to(dev) for t in wl.new_token_kv(w, i)) for i in range(n_trace)]
                if args.append else None)
 
-    def step(k):
-        i = k % n_trace
+    def step(k, i):
+        """Timed step k, replaying trace step i."""
         kp, vp = pools[k % len(pools)]
         if args.append == "fused":
             wl.run_step(ext, w, metas[i], i, q_pool, kp, vp, ws, new_kv=appends[i])
@@ -152,26 +189,47 @@ def main():
             wl.append_step_kv_native(w, i, kp, vp, metas[i], ext, appends[i])
         wl.run_step(ext, w, metas[i], i, q_pool, kp, vp, ws)
 
+    # Correctness gate (reference: benchmark_serving_trace.py:1432-1437), before timing and
+    # on a pool nothing has appended to: the middle trace step of the op as timed, against
+    # a torch fp32 SDPA over the same pages on the GPU.
+    gate_i = n_trace // 2
+    if w.kv_fp8:
+        gate_k, gate_v = serving.dequantize_pool(k0, w.k_scale), serving.dequantize_pool(v0, w.v_scale)
+    elif args.append == "fused":  # the op writes the new token into k0 / v0
+        gate_k, gate_v = k0.clone(), v0.clone()
+    else:
+        gate_k, gate_v = k0, v0
+    fused_kv = appends[gate_i] if args.append == "fused" else None
+    gate_out = wl.run_step(ext, w, metas[gate_i], gate_i, q_pool, k0, v0, ws, new_kv=fused_kv).clone()
+    if fused_kv is not None:  # the reference attends to the appended token too
+        serving.append_reference(w, metas[gate_i], gate_k, gate_v, fused_kv)
+    torch.cuda.synchronize()
+    gate = serving.gate_step(gate_out, metas[gate_i], q_pool[gate_i], gate_k, gate_v, w.page_size)
+    gate["step"] = gate_i
+    if not gate["pass"]:
+        print(f"correctness gate failed at trace step {gate_i}: {gate}", file=sys.stderr)
+        sys.exit(1)
+    del gate_k, gate_v
+
     graph = None
     if args.graph:
-        # Warm up on the capture stream (per-stream scratch is allocated outside capture),
-        # then capture exactly args.steps steps into one graph.
+        # Warm up on the capture stream, then capture exactly args.steps steps into one graph.
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
             for k in range(args.warmup):
-                step(k)
+                step(k, sample[k % len(sample)])
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.stream(side):
             with torch.cuda.graph(graph, stream=side):
                 for k in range(args.steps):
-                    step(k)
+                    step(k, sample[k])
         torch.cuda.synchronize()
         graph.replay()
     else:
         for k in range(args.warmup):
-            step(k)
+            step(k, sample[k % len(sample)])
     torch.cuda.synchronize()
 
     # Timed region: exactly args.steps steps, synchronised on both sides.
@@ -183,12 +241,12 @@ def main():
         graph.replay()
     else:
         for k in range(args.steps):
-            step(k)
+            step(k, sample[k])
     stop.record()
     torch.cuda.synchronize()
     wall_s = time.perf_counter() - t0
     gpu_ms = start.elapsed_time(stop)
-    total_bytes = sum(metas[k % n_trace].kv_bytes for k in range(args.steps))
+    total_bytes = sum(sample_bytes)
 
     def decode_stage(i, m, kp, vp):
         if w.kv_fp8:
@@ -200,47 +258,50 @@ def main():
                                  m.split_offsets, m.q_indices, ws, m.bucket_length, w.page_size,
                                  m.total_partial_slots)
 
-    # Decode kernel alone (stage 1 of the work-queue op), one event pair per launch on its
-    # stream.  The grid ops have no separate stage entry point: their whole op is timed.
-    dec_ms, dec_bytes = [], []
+    # Decode kernel alone (stage 1 of the work-queue op) over the same sample, one event
+    # pair per launch on its stream.  The grid ops have no separate stage entry point:
+    # their whole op is timed.
+    queue = w.op == "paged_attention_workqueue"
+
+    def launch(k):
+        i = sample[k]
+        kp, vp = pools[k % len(pools)]
+        if queue:
+            decode_stage(i, metas[i], kp, vp)
+        else:
+            step(k, i)
+
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(args.steps)]
-    queue = w.op == "paged_attention_workqueue"
     for k in range(args.steps):
-        i = k % n_trace
-        m = metas[i]
-        kp, vp = pools[k % len(pools)]
         evs[k][0].record()
-        if queue:
-            decode_stage(i, m, kp, vp)
-        else:
-            step(k)
+        launch(k)
         evs[k][1].record()
-        dec_bytes.append(m.kv_bytes)
     torch.cuda.synchronize()
     dec_ms = [a.elapsed_time(b) for a, b in evs]
     # The same launches back to back under one event pair (no event packets between them).
     b0, b1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     b0.record()
     for k in range(args.steps):
-        i = k % n_trace
-        m = metas[i]
-        kp, vp = pools[k % len(pools)]
-        if queue:
-            decode_stage(i, m, kp, vp)
-        else:
-            step(k)
+        launch(k)
     b1.record()
     torch.cuda.synchronize()
     batched_us = b0.elapsed_time(b1) * 1e3 / args.steps
     # Roofline numerator over the back-to-back launches: event packets between launches
     # add a few microseconds that are not kernel time (rocprofv3's kernel-trace average
     # duration matches the back-to-back figure to about 1 %).
-    achieved = sum(dec_bytes) / (batched_us * 1e-6 * args.steps) / 1e9
-    traffic = None
-    if os.path.exists(TRAFFIC_FILE):
+    alg_per_launch = total_bytes / args.steps
+    achieved = total_bytes / (batched_us * 1e-6 * args.steps) / 1e9
+    traffic, traffic_note = None, None
+    if args.workload == "c4" and queue and not w.kv_fp8 and os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as fh:
-            traffic = json.load(fh).get("hbm_bytes_per_launch")
+            prof = json.load(fh)
+        ratio = prof["hbm_bytes_per_launch"] / prof["algorithmic_bytes_per_launch"]
+        traffic = int(round(ratio * alg_per_launch))
+        traffic_note = (f"rocprofv3 FETCH_SIZE x {prof['fetch_scale']:.2f} + WRITE_SIZE x "
+                        f"{prof['write_scale']:.2f} = {ratio:.4f} x algorithmic bytes "
+                        f"(profiles/c4_decode_traffic.json, {prof['launches']} launches), "
+                        f"scaled to this sample")
 
     value = total_bytes / (gpu_ms / 1e3) / 1e9
     kernel = {"paged_attention_workqueue": "decode_kernel<*,kQueue> (stage 1 only)",
@@ -252,6 +313,10 @@ def main():
                                       "decode_kernel<*,kSplit> + merge_kernel when few units)"}[w.op]
     if w.op in ("paged_attention", "attention_contiguous") and w.splits > 1:
         kernel = "decode_kernel<*,kSplit> + merge_kernel (whole op)"
+    if args.steps % n_trace == 0:
+        sample_text = f"{args.steps // n_trace} whole pass(es) of the {n_trace}-step trace"
+    else:
+        sample_text = f"{args.steps} evenly spaced steps of the {n_trace}-step trace (k * {n_trace} // {args.steps})"
     result = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -277,15 +342,19 @@ def main():
                    "fused_merge": bool(args.fused_merge),
                    "launch": "hip graph replay" if args.graph else "eager",
                    "append_kv": args.append or False,
-                   "mean_kv_mb_per_step": round(sum(m.kv_bytes for m in metas) / n_trace / 1e6, 2),
+                   "sample": sample_text,
+                   "mean_kv_mb_per_step": round(mean_bytes / 1e6, 2),
+                   "trace_mean_kv_mb_per_step": round(sum(m.kv_bytes for m in metas) / n_trace / 1e6, 2),
                    "cache_basis": f"HBM-cold ({len(pools)} rotated KV pool replicas)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": traffic if args.workload == "c4" and not w.kv_fp8 else None,
+                     "traffic": traffic,
+                     "traffic_source": traffic_note,
                      "kernel": kernel,
                      "mean_launch_us": round(batched_us, 2),
                      "mean_launch_us_event_bracketed": round(sum(dec_ms) / len(dec_ms) * 1e3, 2),
-                     "algorithmic_bytes_per_launch": int(sum(dec_bytes) / len(dec_bytes))},
+                     "algorithmic_bytes_per_launch": int(alg_per_launch)},
+        "gate": gate,
     }
     if w.op == "attention_contiguous":
         # The reference's query-head baseline on the same inputs (smoke_test.cu:342-374

@@ -1,7 +1,10 @@
 """Achievable-HBM-bandwidth probes and rocprof byte-counter calibration.
 
 The MI355X counterpart of the reference's micro_benchmarks/01_hbm_bandwidth.cu:20-51
-(hbm_read / hbm_copy), driving ``pkv_probe_read`` / ``pkv_probe_copy`` of libpkv.so:
+(hbm_read / hbm_copy), driving ``pkv_probe_read`` / ``pkv_probe_copy`` of
+``persistentkv-attention_amd/libpkv_probe.so`` (include/pkv_probe.h; built by
+``make -C persistentkv-attention_amd/csrc``), a measurement library kept apart from the
+engine's libpkv.so:
 
   python hbm_probe.py read            # read bandwidth for the decode kernel's access patterns
   python hbm_probe.py copy --mib 1024 # one known-size copy per launch, for rocprofv3 --pmc
@@ -19,11 +22,35 @@ import argparse
 import os
 import sys
 
-_HERE = os.path.dirname(os.path.abspath(__file__))
-if _HERE not in sys.path:
-    sys.path.insert(0, _HERE)
+import ctypes
 
-PATTERNS = {0: "contiguous", 1: "K operand (16 rows x 64 B)", 2: "V operand (4 rows x 256 B)"}
+_HERE = os.path.dirname(os.path.abspath(__file__))
+PROBE_LIBRARY = os.path.join(_HERE, "persistentkv-attention_amd", "libpkv_probe.so")
+
+PATTERNS = {0: "contiguous", 1: "K operand (16 rows x 64 B)", 2: "V operand (4 rows x 256 B)",
+            3: "K whole lines via LDS (4 rows x 256 B)"}
+_lib = None
+
+
+def _probe_lib():
+    """libpkv_probe.so with argument types declared (torch is imported first, so the
+    library binds to torch's HIP runtime)."""
+    global _lib
+    if _lib is None:
+        import torch  # noqa: F401
+        if not os.path.exists(PROBE_LIBRARY):
+            raise ImportError(f"{PROBE_LIBRARY} is not built; run `make -C persistentkv-attention_amd/csrc`")
+        so = ctypes.CDLL(PROBE_LIBRARY)
+        vp, sz, i32 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int32
+        so.pkv_probe_read.argtypes = [vp, sz, i32, vp, vp]
+        so.pkv_probe_copy.argtypes = [vp, vp, sz, vp]
+        so.pkv_probe_read_cus.argtypes = [vp, sz, i32, i32, vp, vp]
+        so.pkv_probe_read_inflight.argtypes = [vp, sz, i32, i32, i32, i32, vp, vp]
+        for f in (so.pkv_probe_read, so.pkv_probe_copy, so.pkv_probe_read_cus,
+                  so.pkv_probe_read_inflight):
+            f.restype = ctypes.c_int
+        _lib = so
+    return _lib
 
 
 def _time_ms(torch, fn, iters):
@@ -40,15 +67,13 @@ def _time_ms(torch, fn, iters):
 
 def _check(lib, status):
     if status != 0:
-        raise RuntimeError(f"probe launch failed: {lib.pkv_status_string(status).decode()}")
+        raise RuntimeError(f"probe launch failed with status {status}")
 
 
 def run_read(sizes_mib, iters):
     import torch
 
-    import pkv_native
-
-    lib = pkv_native.lib()
+    lib = _probe_lib()
     dev = torch.device("cuda:0")
     buf = torch.empty(max(sizes_mib) << 20, dtype=torch.uint8, device=dev).random_(0, 256)
     sink = torch.zeros(4096, dtype=torch.int32, device=dev)
@@ -70,9 +95,7 @@ def run_cus(counts, mib, iters):
     per CU: the per-CU ceiling when n is below the CU count."""
     import torch
 
-    import pkv_native
-
-    lib = pkv_native.lib()
+    lib = _probe_lib()
     dev = torch.device("cuda:0")
     nbytes = mib << 20
     buf = torch.empty(nbytes, dtype=torch.uint8, device=dev).random_(0, 256)
@@ -92,9 +115,7 @@ def run_inflight(counts, mib, iters, patterns):
     bytes in flight per CU / bandwidth per CU."""
     import torch
 
-    import pkv_native
-
-    lib = pkv_native.lib()
+    lib = _probe_lib()
     dev = torch.device("cuda:0")
     nbytes = mib << 20
     buf = torch.empty(nbytes, dtype=torch.uint8, device=dev).random_(0, 256)
@@ -118,9 +139,7 @@ def run_inflight(counts, mib, iters, patterns):
 def run_copy(mib, iters):
     import torch
 
-    import pkv_native
-
-    lib = pkv_native.lib()
+    lib = _probe_lib()
     dev = torch.device("cuda:0")
     nbytes = mib << 20
     src = torch.empty(nbytes, dtype=torch.uint8, device=dev).random_(0, 256)
@@ -148,7 +167,7 @@ def main(argv=None):
     f.add_argument("--workgroups", type=int, nargs="+", default=[8, 128, 256])
     f.add_argument("--mib", type=int, default=4096)
     f.add_argument("--iters", type=int, default=2)
-    f.add_argument("--patterns", type=int, nargs="+", default=[1, 2])
+    f.add_argument("--patterns", type=int, nargs="+", default=[1, 2, 3])
     c = sub.add_parser("copy")
     c.add_argument("--mib", type=int, default=1024)
     c.add_argument("--iters", type=int, default=4)

@@ -3,13 +3,13 @@
  *
  * Every entry point takes plain device pointers, sizes and a HIP stream passed as
  * `void*` (a hipStream_t; NULL selects the null stream).  Outputs, the split workspace
- * and the merge counters are owned by the caller, exactly as in the reference op surface.
- * One exception to "the library allocates nothing": a direct launch (num_splits == 1) of
- * fewer than 128 (row, kv head) pairs is split internally, and its partial states go to a
- * scratch buffer that the library allocates on the first such launch on a stream (4 MiB
- * or more, never during graph capture, kept until the process ends; PKV_DIRECT_SPLIT=0 in
- * the environment turns this off).  Calls enqueue work asynchronously and never
- * synchronise the host (a scratch buffer that must grow waits for its stream once).
+ * and the merge counters are owned by the caller, exactly as in the reference op surface,
+ * and the library allocates no device memory.  A direct launch (num_splits == 1) of fewer
+ * than 128 (row, kv head) pairs splits itself internally when the caller's workspace can
+ * hold the partial states (pkv_direct_workspace_bytes gives the size for the full split;
+ * a smaller or empty workspace gives a smaller split or the single launch, with the same
+ * result to fp32 rounding; PKV_DIRECT_SPLIT=0 in the environment turns this off).  Calls
+ * enqueue work asynchronously and never synchronise the host.
  * Errors are reported as a pkv_status code; a one-line message describing the last
  * failure on the calling thread is available from pkv_last_error().
  *
@@ -74,6 +74,14 @@ size_t pkv_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t num_split
 /* Bytes of workspace for the work-queue op (total_partial_slots partial states per head).
  * Replaces persistentkv_partition_workqueue_workspace sizing, cuh:915-927. */
 size_t pkv_workqueue_workspace_bytes(int32_t total_partial_slots, int32_t num_q_heads);
+
+/* Bytes of workspace with which a direct launch (num_splits == 1) of the grid ops and of
+ * pkv_attention_contiguous runs its full internal split: about 256 units of work for a
+ * batch of few (row, kv head) pairs, whose partial states are merged by a second launch.
+ * 0 when that launch is not split.  The reference's direct path takes no workspace
+ * (cuh:929-946); this entry has no counterpart there. */
+size_t pkv_direct_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                                  int32_t context);
 
 /* ---------------------------------------------------------------------------------
  * The four ops.  Argument order follows the torch op surface of
@@ -241,8 +249,10 @@ int pkv_attention_query_head_baseline(
 typedef enum pkv_policy { PKV_POLICY_REFERENCE = 0, PKV_POLICY_MI355X = 1 } pkv_policy;
 
 typedef enum pkv_route {
-  PKV_ROUTE_FLASHINFER = 0,   /* the reference's fallback route (not provided here) */
-  PKV_ROUTE_BUCKET = 1,       /* length-bucket split grid (paged_attention_indexed) */
+  PKV_ROUTE_FLASHINFER = 0,   /* the reference's fallback route (reference policy only;
+                                 this engine has no such route) */
+  PKV_ROUTE_BUCKET = 1,       /* length-bucket split grid (paged_attention_indexed); with
+                                 1 split, the direct launch */
   PKV_ROUTE_WORKQUEUE = 2     /* compact work queue (paged_attention_workqueue) */
 } pkv_route;
 
@@ -286,7 +296,11 @@ double pkv_estimate_route_ms(
     const pkv_cost_model* model);
 
 /* choose_adaptive_route_cost_model, benchmark_serving_trace.py:445-488.  Returns the
- * chosen pkv_route and writes its split count and estimate. */
+ * chosen pkv_route and writes its split count and estimate.  With model->policy ==
+ * PKV_POLICY_MI355X it never returns PKV_ROUTE_FLASHINFER: every step, for any G, length
+ * and active count, goes to the cheaper of PKV_ROUTE_BUCKET (splits from
+ * pkv_model_bucket_splits, priced as one ragged grid launch plus its merge) and
+ * PKV_ROUTE_WORKQUEUE (splits from pkv_model_workqueue_splits). */
 int32_t pkv_choose_adaptive_route(
     const int32_t* lengths, int32_t count, const pkv_cost_model* model,
     int32_t* out_splits, double* out_estimated_ms);
@@ -318,6 +332,40 @@ int pkv_build_workqueue(
     int32_t* seq_lens, int32_t* q_indices, int32_t* out_indices,
     int32_t* work_items, int32_t work_capacity, int32_t* out_num_tasks,
     int32_t* split_offsets, int32_t* out_total_partial_slots);
+
+/* round_bucket_length, benchmark_serving_trace.py:316-321: `length` rounded up to a
+ * multiple of bucket_tokens, then to a multiple of page_size (at least one page), capped
+ * at the row's allocated_pages * page_size; `length` itself when bucket_tokens <= 0. */
+int32_t pkv_round_bucket_length(int32_t length, int32_t bucket_tokens, int32_t allocated_pages,
+                                int32_t page_size);
+
+/* use_single_bucket_for_state, benchmark_serving_trace.py:491-504: 1 when the step's rows
+ * go through one ragged bucket (requested, or adaptive with at least max(3, count - 1)
+ * distinct lengths among count > 1 rows). */
+int32_t pkv_use_single_bucket(const int32_t* lengths, int32_t count,
+                              int32_t requested_single_bucket, int32_t adaptive_route);
+
+/* Builds one decode step's length-bucket metadata, bit-exact with the bucket branch of
+ * compile_persistentkv_metadata (benchmark_serving_trace.py:731-780): rows grouped by
+ * pkv_round_bucket_length of their length (one bucket of max(lengths) when
+ * pkv_use_single_bucket), buckets in order of first appearance, rows of a bucket in step
+ * order.  Bucket j (j < *out_bucket_count <= count) holds bucket_rows[j] rows, which are
+ * entries [sum of earlier bucket_rows, + bucket_rows[j]) of seq_lens (the row's length),
+ * q_indices (its request id) and out_indices (its position in the step), and one
+ * [bucket_rows[j], bucket_table_cols[j] = ceil(bucket_lengths[j] / page_size)] block
+ * table, stored after the earlier buckets' tables in `tables`, each row its first
+ * reserved pages padded with its last one.  bucket_splits[j] is choose_splits over the
+ * bucket's lengths (pkv_choose_splits with `policy`).  Every bucket is one
+ * pkv_paged_attention_indexed launch with bucket_context = bucket_lengths[j] (:986-1000).
+ * Returns PKV_ERR_CAPACITY with *out_table_elems set when `tables` is too small. */
+int pkv_build_buckets(const int32_t* lengths, const int32_t* request_ids, int32_t count,
+                      const int32_t* page_indptr, const int32_t* page_ids, int32_t page_size,
+                      int32_t requested_splits, int32_t auto_splits, int32_t bucket_tokens,
+                      int32_t single_bucket, int32_t adaptive_route, int32_t num_kv_heads,
+                      int32_t policy, int32_t* out_bucket_count, int32_t* bucket_lengths,
+                      int32_t* bucket_rows, int32_t* bucket_splits, int32_t* bucket_table_cols,
+                      int32_t* seq_lens, int32_t* q_indices, int32_t* out_indices,
+                      int32_t* tables, int64_t table_capacity, int64_t* out_table_elems);
 
 /* ---------------------------------------------------------------------------------
  * KV-cache append: the write of each row's newest token before its decode step.
@@ -419,34 +467,6 @@ int pkv_paged_attention_workqueue_fp8_append(
     int32_t bucket_context, int32_t total_partial_slots, int32_t fused_merge,
     float k_scale, float v_scale, const void* k_new, const void* v_new,
     int32_t dtype, void* stream);
-
-/* ---------------------------------------------------------------------------------
- * HBM calibration probes (counterparts of the reference's
- * micro_benchmarks/01_hbm_bandwidth.cu:20-51 read/copy kernels).
- * ------------------------------------------------------------------------------- */
-
-/* Reads `bytes` (a multiple of 4096, < 8 TiB) of `src` once, visiting its 4 KB chunks in
- * a permuted order with access pattern 0 (contiguous 1 KB per load instruction),
- * 1 (the decode kernel's K-operand loads: 16 rows x 64 B) or 2 (its V-operand loads:
- * 4 rows x 256 B).  `sink` receives at most one word per workgroup (2048 words). */
-int pkv_probe_read(const void* src, size_t bytes, int32_t pattern, void* sink, void* stream);
-
-/* Copies `bytes` (a multiple of 16) from src to dst with a plain grid-stride kernel. */
-int pkv_probe_copy(const void* src, void* dst, size_t bytes, void* stream);
-
-/* pkv_probe_read over `workgroups` workgroups of 8 waves, at most one per CU (each holds
- * 96 KB of LDS): with fewer workgroups than CUs it measures the read bandwidth of that
- * many CUs (sink holds `workgroups` words).  No counterpart in the reference. */
-int pkv_probe_read_cus(const void* src, size_t bytes, int32_t pattern, int32_t workgroups,
-                       void* sink, void* stream);
-
-/* pkv_probe_read_cus with `waves` (4, 8 or 16) waves per workgroup, each keeping
- * `chunks_per_wave` (1, 2 or 4) 4 KB chunks in flight: read bandwidth and loaded latency
- * (bytes in flight / bandwidth) against how the bytes in flight are spread over waves.
- * No counterpart in the reference. */
-int pkv_probe_read_inflight(const void* src, size_t bytes, int32_t pattern, int32_t waves,
-                            int32_t chunks_per_wave, int32_t workgroups, void* sink,
-                            void* stream);
 
 #ifdef __cplusplus
 }  /* extern "C" */

@@ -8,7 +8,10 @@ Restates tests/benchmark_serving_trace.py of ahmed123hds/persistentkv-attention:
   model_workqueue_splits       :405-415
   estimate_route_ms            :418-442 (useful_kv_mb_for_state :511-513)
   choose_adaptive_route        :445-488
+  round_bucket_length          :316-321 (rounded_length :159-160)
+  use_single_bucket            :491-504 (use_single_bucket_for_state)
   build_workqueue              :668-729 (work-queue branch of compile_persistentkv_metadata)
+  build_buckets                :731-780 (length-bucket branch of compile_persistentkv_metadata)
 
 The reference reads HQ/HKV/DIM and the cost constants from module globals (:33-43);
 here they are keyword arguments with the reference's values as defaults.  Integer
@@ -181,3 +184,54 @@ def build_workqueue(lengths, request_ids, page_lists, page_size, requested_split
                 q_indices=q_indices, out_indices=out_indices, work_items=work_items,
                 split_offsets=split_offsets, total_partial_slots=split_offsets[-1],
                 splits=max(1, max(row_splits_all)))
+
+
+def round_bucket_length(length, bucket_tokens, allocated_pages, page_size=16):
+    """benchmark_serving_trace.py:316-321 with rounded_length (:159-160) at ``page_size``."""
+    if bucket_tokens <= 0:
+        return length
+    bucket = ((length + bucket_tokens - 1) // bucket_tokens) * bucket_tokens
+    bucket = max(page_size, ((bucket + page_size - 1) // page_size) * page_size)
+    return min(bucket, allocated_pages * page_size)
+
+
+def use_single_bucket(lengths, requested_single_bucket, adaptive_route):
+    """use_single_bucket_for_state, benchmark_serving_trace.py:491-504."""
+    if requested_single_bucket:
+        return True
+    if not adaptive_route:
+        return False
+    active = len(lengths)
+    if active <= 1:
+        return False
+    return len(set(lengths)) >= max(3, active - 1)
+
+
+def build_buckets(lengths, request_ids, page_lists, page_size, requested_splits, auto_splits,
+                  bucket_tokens=0, single_bucket=False, adaptive_route=False, hkv=8):
+    """One decode step's length buckets (benchmark_serving_trace.py:731-780): a list of
+    dicts with bucket_length, block_table (rows), seq_lens, q_indices, out_indices, splits,
+    in the dict order the reference builds them."""
+    state_single = use_single_bucket(lengths, single_bucket, adaptive_route)
+    buckets = {}
+    if state_single:
+        buckets[max(lengths)] = list(range(len(lengths)))
+    else:
+        for offset, length in enumerate(lengths):
+            key = round_bucket_length(length, bucket_tokens, len(page_lists[offset]), page_size)
+            buckets.setdefault(key, []).append(offset)
+    result = []
+    for bucket_length, offsets in buckets.items():
+        page_count = math.ceil(bucket_length / page_size)
+        rows, seq_lens = [], []
+        for offset in offsets:
+            pages = list(page_lists[offset][:page_count])
+            if len(pages) < page_count:
+                pages = pages + [page_lists[offset][-1]] * (page_count - len(pages))
+            rows.append(pages)
+            seq_lens.append(lengths[offset])
+        result.append(dict(bucket_length=int(bucket_length), block_table=rows, seq_lens=seq_lens,
+                           q_indices=[request_ids[o] for o in offsets], out_indices=list(offsets),
+                           splits=choose_splits(seq_lens, requested_splits, auto_splits,
+                                                state_single, hkv)))
+    return result

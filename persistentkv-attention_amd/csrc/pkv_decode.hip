@@ -1685,74 +1685,33 @@ int dispatch_merge(const MergeArgs& m, bool queue, int dtype, hipStream_t stream
   return PKV_OK;
 }
 
-// Per-stream scratch for the partial states of the direct op's internal split: one device
-// buffer per (device, stream).  Launches on one stream run in order, so a buffer is only
-// ever used by one op at a time.  It is allocated, or grown, on a launch that needs it,
-// never while the stream is being captured into a graph, and kept until the process ends.
-// A launch that gets no buffer (more than kMaxScratchStreams streams, capture before the
-// first launch, allocation failure) runs the single-launch direct kernel instead.
-struct StreamScratch {
-  int device;
-  hipStream_t stream;
-  void* ptr;
-  size_t bytes;
-};
-constexpr size_t kMinScratchBytes = 4u << 20;
-constexpr int kMaxScratchStreams = 64;
-
-StreamScratch* stream_scratch(hipStream_t stream, size_t need) {
-  static std::mutex mu;
-  static StreamScratch table[kMaxScratchStreams];
-  static int used = 0;
-  int device = 0;
-  if (hipGetDevice(&device) != hipSuccess) return nullptr;
-  std::lock_guard<std::mutex> lock(mu);
-  StreamScratch* e = nullptr;
-  for (int i = 0; i < used; ++i)
-    if (table[i].device == device && table[i].stream == stream) e = &table[i];
-  if (e && e->bytes >= need) return e;
-  if (!e && used >= kMaxScratchStreams) return nullptr;
-  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(stream, &capture) != hipSuccess || capture != hipStreamCaptureStatusNone)
-    return nullptr;
-  const size_t bytes = need > kMinScratchBytes ? need : kMinScratchBytes;
-  void* p = nullptr;
-  if (hipMalloc(&p, bytes) != hipSuccess) {
-    (void)hipGetLastError();
-    return nullptr;
-  }
-  if (e) {  // grow: the old buffer may still be read by work queued on this stream
-    if (hipStreamSynchronize(stream) != hipSuccess || hipFree(e->ptr) != hipSuccess) {
-      (void)hipFree(p);
-      (void)hipGetLastError();
-      return nullptr;
-    }
-    e->ptr = p;
-    e->bytes = bytes;
-    return e;
-  }
-  table[used] = StreamScratch{device, stream, p, bytes};
-  return &table[used++];
-}
-
-// Internal split count for a direct (num_splits == 1) launch.  One decode workgroup per
-// (row, kv head) streams at most ~37 GB/s (one MI355X CU with 8 waves of one tile each), so with
-// few rows the op is split into about 256 units of at least 2 tiles, merged by the merge
-// kernel from scratch partial states.  (2-tile units are streamed by one wave each;
-// measured on C1: 10.0 us against 10.5 us for 4-tile units and 11.5 us for 8-tile ones.)
-// PKV_DIRECT_SPLIT=0 keeps the single launch.
-int direct_splits(const Geometry& g, int context) {
+// Internal split count wanted by a direct (num_splits == 1) launch.  One decode workgroup
+// per (row, kv head) streams at most ~37 GB/s (one MI355X CU with 8 waves of one tile
+// each), so with few rows the op is split into about 256 units of at least 2 tiles, merged
+// by the merge kernel from partial states kept in the caller's workspace.  (2-tile units
+// are streamed by one wave each; measured on C1: 10.0 us against 10.5 us for 4-tile units
+// and 11.5 us for 8-tile ones.)  PKV_DIRECT_SPLIT=0 keeps the single launch.
+int direct_splits_wanted(int batch, int hkv, int context) {
   static const bool on = [] {
     const char* e = getenv("PKV_DIRECT_SPLIT");
     return !(e && e[0] == '0');
   }();
-  const long units = (long)g.batch * g.hkv;
-  if (!on || units >= 128) return 1;
+  const long units = (long)batch * hkv;
+  if (!on || units <= 0 || units >= 128) return 1;
   const int tiles = (context + kTile - 1) / kTile;
   long s = (256 + units - 1) / units;
   if (s > tiles / 2) s = tiles / 2;
-  const long per_split = (long)g.batch * g.hq * (kD + 2) * (long)sizeof(float);
-  if (s * per_split > (long)kMinScratchBytes) s = (long)kMinScratchBytes / per_split;
+  return s >= 2 ? (int)s : 1;
+}
+
+// The internal split a direct launch runs with: the wanted one, reduced to what the
+// caller's workspace holds (no split when it holds fewer than two partial states per
+// head).  The library allocates nothing for it.
+int direct_splits(const Geometry& g, int context, size_t ws_bytes) {
+  long s = direct_splits_wanted(g.batch, g.hkv, context);
+  const size_t per_split = (size_t)g.batch * g.hq * (kD + 2) * sizeof(float);
+  if (per_split == 0) return 1;
+  if ((size_t)s * per_split > ws_bytes) s = (long)(ws_bytes / per_split);
   return s >= 2 ? (int)s : 1;
 }
 
@@ -1780,33 +1739,43 @@ DecodeArgs base_args(const Geometry& g, const void* q, int q_rows, const void* k
   return a;
 }
 
-// Launches of the grid ops once arguments are checked: one direct launch, or split decode
-// plus merge (cuh:929-974 persistentkv_launch).  `internal_split` lets a direct launch of
-// few units split itself into the per-stream scratch.
-int launch_grid(const Geometry& g, DecodeArgs a, void* ws, size_t ws_bytes, int num_splits,
-                bool internal_split, hipStream_t stream) {
-  int st;
-  const int units = (int)((long)a.batch * a.hkv);
-  a.num_splits = num_splits;
+// How a grid op runs: one direct launch (splits == 1) or a split decode over `splits`
+// sequence splits plus the merge, with partial states in `ws`.
+struct GridPlan {
+  int splits;
+  void* ws;
+};
+
+// Chooses the launches of a grid op and checks the workspace, before anything is launched
+// (cuh:929-974 persistentkv_launch).  `internal_split` lets a direct launch of few units
+// split itself into the caller's workspace when it is large enough.
+int plan_grid(const Geometry& g, const DecodeArgs& a, void* ws, size_t ws_bytes, int num_splits,
+              bool internal_split, GridPlan& plan) {
+  plan.splits = num_splits;
+  plan.ws = ws;
   if (num_splits == 1) {
-    const int internal = internal_split ? direct_splits(g, a.context) : 1;
-    StreamScratch* scratch =
-        internal > 1 ? stream_scratch(stream, pkv_workspace_bytes(g.batch, g.hq, internal)) : nullptr;
-    if (!scratch) {
-      st = dispatch_decode<kDirect>(a, g.dtype, units, stream);
-      return st == PKV_OK ? ok() : st;
-    }
-    num_splits = internal;
-    ws = scratch->ptr;
-    ws_bytes = scratch->bytes;
-    a.num_splits = num_splits;
+    plan.splits = internal_split && ws ? direct_splits(g, a.context, ws_bytes) : 1;
+    return PKV_OK;
   }
   const size_t need = pkv_workspace_bytes(g.batch, g.hq, num_splits);
   if (!ws || ws_bytes < need)
     return fail(PKV_ERR_WORKSPACE_TOO_SMALL, "split dispatch requires a workspace of %zu bytes (got %zu)",
                 need, ws ? ws_bytes : (size_t)0);
+  return PKV_OK;
+}
+
+// Launches a planned grid op.
+int launch_grid(const Geometry& g, DecodeArgs a, const GridPlan& plan, hipStream_t stream) {
+  int st;
+  const int units = (int)((long)a.batch * a.hkv);
+  const int num_splits = plan.splits;
+  a.num_splits = num_splits;
+  if (num_splits == 1) {
+    st = dispatch_decode<kDirect>(a, g.dtype, units, stream);
+    return st == PKV_OK ? ok() : st;
+  }
   const long states = (long)g.batch * g.hq * num_splits;
-  a.part_m = (float*)ws;
+  a.part_m = (float*)plan.ws;
   a.part_l = a.part_m + states;
   a.part_acc = a.part_l + states;
   st = dispatch_decode<kSplit>(a, g.dtype, units * num_splits, stream);
@@ -1857,13 +1826,19 @@ struct NewToken {
 // The fused append of the *_append ops.  2-byte pools with pages that are multiples of
 // 16 take the new token inside the decode (AppendPager).  Other page sizes, and fp8
 // pools, run the append kernel first on the same stream: an in-decode fp8 variant (the
-// e4m3 encode on the reloaded lanes) measured slower than the two launches.  Call after
-// apply_quant.
-int apply_new_token(const Geometry& g, DecodeArgs& a, const NewToken& nt, const KvQuant& kq,
-                    hipStream_t stream) {
+// e4m3 encode on the reloaded lanes) measured slower than the two launches.
+// check_new_token validates the arguments without launching anything; apply_new_token
+// (after apply_quant and after every other check of the op) launches or wires the append.
+int check_new_token(const DecodeArgs& a, const NewToken& nt) {
   if (!nt.k && !nt.v) return PKV_OK;
   if (!nt.k || !nt.v) return fail(PKV_ERR_INVALID_ARGUMENT, "k_new and v_new must both be set");
   if (!a.seq_lens) return fail(PKV_ERR_INVALID_ARGUMENT, "the fused append needs seq_lens");
+  return PKV_OK;
+}
+
+int apply_new_token(const Geometry& g, DecodeArgs& a, const NewToken& nt, const KvQuant& kq,
+                    hipStream_t stream) {
+  if (!nt.k && !nt.v) return PKV_OK;
   if (a.kv_fp8)
     return pkv_append_kv_fp8(nt.k, nt.v, const_cast<uint8_t*>(a.k_pages),
                              const_cast<uint8_t*>(a.v_pages), a.block_table, a.seq_lens, g.batch,
@@ -1906,9 +1881,15 @@ int run_grid(const Geometry& g, const void* q, int q_rows, const void* k, const 
   a.out_indices = out_idx;
   a.context = context;
   apply_quant(a, kq);
+  st = check_new_token(a, nt);
+  if (st != PKV_OK) return st;
+  GridPlan plan;
+  st = plan_grid(g, a, ws, ws_bytes, num_splits, true, plan);
+  if (st != PKV_OK) return st;
+  // Every argument is checked: only now may the append write the pools.
   st = apply_new_token(g, a, nt, kq, (hipStream_t)stream_ptr);
   if (st != PKV_OK) return st;
-  return launch_grid(g, a, ws, ws_bytes, num_splits, true, (hipStream_t)stream_ptr);
+  return launch_grid(g, a, plan, (hipStream_t)stream_ptr);
 }
 
 // Contiguous K/V [B, Hkv, N, 128] (cuh:128-178).  `baseline` runs one unit per query
@@ -1938,7 +1919,10 @@ int run_contiguous(const Geometry& g, const void* q, const void* k, const void* 
     a.hkv = g.hq;
     a.group = 1;
   }
-  return launch_grid(g, a, ws, ws_bytes, num_splits, !baseline, (hipStream_t)stream_ptr);
+  GridPlan plan;
+  st = plan_grid(g, a, ws, ws_bytes, num_splits, !baseline, plan);
+  if (st != PKV_OK) return st;
+  return launch_grid(g, a, plan, (hipStream_t)stream_ptr);
 }
 
 struct QueueCall {
@@ -2031,6 +2015,9 @@ int run_workqueue(const QueueCall& c, int32_t fused_merge, hipStream_t stream, c
   if (c.g.batch == 0) return ok();
   DecodeArgs a = queue_args(c);
   apply_quant(a, kq);
+  st = check_new_token(a, nt);
+  if (st != PKV_OK) return st;
+  // Every argument is checked (the workspace by check_queue): the append may now run.
   st = apply_new_token(c.g, a, nt, kq, stream);
   if (st != PKV_OK) return st;
   a.merge_counters = fused_merge ? c.counters : nullptr;
@@ -2086,6 +2073,13 @@ size_t pkv_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t num_split
 size_t pkv_workqueue_workspace_bytes(int32_t total_partial_slots, int32_t num_q_heads) {
   if (total_partial_slots <= 0 || num_q_heads <= 0) return 0;
   return (size_t)total_partial_slots * num_q_heads * (kD + 2) * sizeof(float);
+}
+
+size_t pkv_direct_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                                  int32_t context) {
+  if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || context <= 0) return 0;
+  const int s = direct_splits_wanted(batch, num_kv_heads, context);
+  return s > 1 ? pkv_workspace_bytes(batch, num_q_heads, s) : 0;
 }
 
 int pkv_paged_attention(const void* q, const void* k_pages, const void* v_pages,

@@ -9,12 +9,17 @@
 //   0  contiguous: each 16-byte load instruction covers 1 KB of consecutive bytes
 //   1  K operand:  each instruction reads 16 rows x 64 B (the decode kernel's K loads)
 //   2  V operand:  each instruction reads 4 rows x 256 B (the decode kernel's V loads)
+//   3  K through LDS: the loads of pattern 2 (whole 128-byte lines), then each chunk is
+//      written to a per-wave LDS slab and read back in the K-operand layout (16 rows x
+//      64 B per read), with the 16-byte column index XORed with the row so that neither
+//      the writes nor the reads conflict on LDS banks (pkv_probe_read_inflight only)
 // Chunks are visited in a pseudo-random order (as random page ids would be).
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "pkv.h"
+#include "pkv.h"  // status codes
+#include "pkv_probe.h"
 
 namespace {
 
@@ -24,8 +29,25 @@ constexpr uint32_t kRsrcWord3 = 0x00020000u;
 __device__ inline uint32_t lane_offset(int pattern, int lane, int k) {
   const int c = lane & 15, g = lane >> 4;
   if (pattern == 1) return c * 256 + k * 64 + g * 16;       // K operand (k = 0..3)
-  if (pattern == 2) return (4 * g + k) * 256 + c * 16;      // V operand (k = 0..3)
+  if (pattern >= 2) return (4 * g + k) * 256 + c * 16;      // V operand / whole lines
   return k * 1024 + lane * 16;                              // contiguous
+}
+
+// Swizzled LDS byte offset of 16-byte column `col` of row `row` in a 16 x 256 B slab.
+__device__ inline uint32_t slab_offset(int row, int col) {
+  return row * 256 + ((col ^ (row & 7)) * 16);
+}
+
+// Pattern 3: a chunk loaded as whole lines (lane (c, g) holds rows 4g + k, column c) goes
+// through the wave's LDS slab and comes back as K operands (row c, columns 4k + g).
+__device__ inline void through_lds(u32x4 (&v)[4], uint8_t* slab, int lane) {
+  const int c = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) *(u32x4*)(slab + slab_offset(4 * g + k, c)) = v[k];
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int k = 0; k < 4; ++k) v[k] = *(const u32x4*)(slab + slab_offset(c, 4 * k + g));
+  __builtin_amdgcn_wave_barrier();
 }
 
 // One wave reads whole 4 KB chunks (4 loads of 1 KB); 4 chunks in flight per iteration.
@@ -65,6 +87,8 @@ template <int U>
 __global__ __launch_bounds__(1024) void probe_inflight_kernel(const uint8_t* src, uint64_t chunks,
                                                               uint64_t stride, int pattern,
                                                               uint32_t* sink) {
+  extern __shared__ uint8_t lds[];  // 96 KB: one workgroup per CU; 4 KB slab per wave
+  uint8_t* slab = lds + (threadIdx.x >> 6) * 4096;
   const int lane = threadIdx.x & 63;
   const int waves_per_group = blockDim.x >> 6;
   const uint64_t wave = (uint64_t)blockIdx.x * waves_per_group + (threadIdx.x >> 6);
@@ -84,9 +108,11 @@ __global__ __launch_bounds__(1024) void probe_inflight_kernel(const uint8_t* src
         v[u][k] = __builtin_amdgcn_raw_buffer_load_b128(r, lane_offset(pattern, lane, k), 0, 0);
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u)
+    for (int u = 0; u < U; ++u) {
+      if (pattern == 3) through_lds(v[u], slab, lane);
 #pragma unroll
       for (int k = 0; k < 4; ++k) acc ^= v[u][k];
+    }
   }
   const uint32_t x = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
   if (x == 0x9e3779b9u) sink[blockIdx.x] = x;
@@ -133,11 +159,12 @@ int pkv_probe_read_cus(const void* src, size_t bytes, int32_t pattern, int32_t w
 }
 
 // pkv_probe_read_cus with `waves` (4, 8 or 16) waves per workgroup, each keeping
-// `chunks_per_wave` (1, 2 or 4) chunks of 4 KB in flight.
+// `chunks_per_wave` (1, 2 or 4) chunks of 4 KB in flight; pattern 3 also moves every
+// chunk through LDS (at most 16 waves x 4 KB of the workgroup's 96 KB).
 int pkv_probe_read_inflight(const void* src, size_t bytes, int32_t pattern, int32_t waves,
                             int32_t chunks_per_wave, int32_t workgroups, void* sink, void* stream) {
   if (!src || !sink || bytes < 4096 || bytes % 4096 || bytes / 4096 >= 2147483647ull ||
-      pattern < 0 || pattern > 2 || workgroups <= 0 || workgroups > 65536 ||
+      pattern < 0 || pattern > 3 || workgroups <= 0 || workgroups > 65536 ||
       (waves != 4 && waves != 8 && waves != 16) ||
       (chunks_per_wave != 1 && chunks_per_wave != 2 && chunks_per_wave != 4))
     return PKV_ERR_INVALID_ARGUMENT;

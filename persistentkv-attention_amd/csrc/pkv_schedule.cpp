@@ -196,7 +196,10 @@ double pkv_estimate_route_ms(const int32_t* lengths, int32_t count, int32_t rout
     merge_mb = 0.0;
   } else if (route == PKV_ROUTE_BUCKET) {
     ctas_per_cu = (double)(active * m->num_kv_heads * splits) / (double)m->compute_units;
-    launch_count = 2 * (int64_t)unique.size();
+    // The reference launches decode + merge per exact-length bucket.  The MI355X harness
+    // runs the step as one ragged grid (row-local split bounds): decode plus a merge, or
+    // one direct launch that splits itself into the caller's workspace.
+    launch_count = m->policy == PKV_POLICY_MI355X ? 2 : 2 * (int64_t)unique.size();
     merge_mb = (double)merge_bytes / (1024.0 * 1024.0);
   } else if (route == PKV_ROUTE_WORKQUEUE) {
     ctas_per_cu = (double)(active * m->num_kv_heads * splits) / (double)m->compute_units;
@@ -212,11 +215,23 @@ double pkv_estimate_route_ms(const int32_t* lengths, int32_t count, int32_t rout
 }
 
 // choose_adaptive_route_cost_model, benchmark_serving_trace.py:445-488.  The reference
-// falls back to FlashInfer for unsupported G and short contexts; with supported_group
-// == 0 every G stays on the native routes.
+// falls back to FlashInfer for unsupported G and short contexts.  The MI355X policy has
+// no such route: every step goes to one of this engine's own routes, the split grid
+// (PKV_ROUTE_BUCKET, with splits == 1 meaning the direct launch) or the compact work
+// queue, whichever the cost model prices lower, for every G, length and active count.
 int32_t pkv_choose_adaptive_route(const int32_t* lengths, int32_t count, const pkv_cost_model* m,
                                   int32_t* out_splits, double* out_ms) {
   if (!m || !lengths || count <= 0) return -1;
+  if (m->policy == PKV_POLICY_MI355X) {
+    const int32_t bs = pkv_model_bucket_splits(lengths, count, m->num_kv_heads, m->policy);
+    const int32_t ws = pkv_model_workqueue_splits(lengths, count, m->num_kv_heads, m->policy);
+    const double be = pkv_estimate_route_ms(lengths, count, PKV_ROUTE_BUCKET, bs, m);
+    const double we = pkv_estimate_route_ms(lengths, count, PKV_ROUTE_WORKQUEUE, ws, m);
+    const bool queue = we < be;  // ties keep the grid: one fewer metadata tensor per step
+    if (out_splits) *out_splits = queue ? ws : bs;
+    if (out_ms) *out_ms = queue ? we : be;
+    return queue ? PKV_ROUTE_WORKQUEUE : PKV_ROUTE_BUCKET;
+  }
   const int32_t g = m->num_kv_heads > 0 ? m->num_q_heads / m->num_kv_heads : 0;
   int32_t route = PKV_ROUTE_FLASHINFER, splits = 1;
   double best = pkv_estimate_route_ms(lengths, count, PKV_ROUTE_FLASHINFER, 1, m);
@@ -360,6 +375,99 @@ int pkv_build_workqueue(const int32_t* lengths, const int32_t* request_ids, int3
       }
     }
     split_offsets[r + 1] = split_offsets[r] + (int32_t)s;  // :703 counts empty splits too
+  }
+  return PKV_OK;
+}
+
+// round_bucket_length, benchmark_serving_trace.py:316-321 (rounded_length :159-160 with
+// the harness's PAGE_SIZE).
+int32_t pkv_round_bucket_length(int32_t length, int32_t bucket_tokens, int32_t allocated_pages,
+                                int32_t page_size) {
+  if (bucket_tokens <= 0) return length;
+  int64_t bucket = floordiv((int64_t)length + bucket_tokens - 1, bucket_tokens) * bucket_tokens;
+  bucket = std::max<int64_t>(page_size, floordiv(bucket + page_size - 1, page_size) * page_size);
+  return (int32_t)std::min<int64_t>(bucket, (int64_t)allocated_pages * page_size);
+}
+
+// use_single_bucket_for_state, benchmark_serving_trace.py:491-504.
+int32_t pkv_use_single_bucket(const int32_t* lengths, int32_t count,
+                              int32_t requested_single_bucket, int32_t adaptive_route) {
+  if (requested_single_bucket) return 1;
+  if (!adaptive_route) return 0;
+  if (count <= 1 || !lengths) return 0;
+  const int64_t unique = (int64_t)std::set<int32_t>(lengths, lengths + count).size();
+  return unique >= std::max<int64_t>(3, (int64_t)count - 1) ? 1 : 0;
+}
+
+// Length-bucket route of compile_persistentkv_metadata (benchmark_serving_trace.py:731-780):
+// active rows grouped by rounded length, buckets in order of first appearance (Python
+// dict order), rows of a bucket in step order, one block table per bucket of
+// ceil(bucket_length / page_size) columns padded with the row's last reserved page, and
+// the bucket's split count from choose_splits over its rows' lengths.
+int pkv_build_buckets(const int32_t* lengths, const int32_t* request_ids, int32_t count,
+                      const int32_t* page_indptr, const int32_t* page_ids, int32_t page_size,
+                      int32_t requested_splits, int32_t auto_splits, int32_t bucket_tokens,
+                      int32_t single_bucket, int32_t adaptive_route, int32_t num_kv_heads,
+                      int32_t policy, int32_t* out_bucket_count, int32_t* bucket_lengths,
+                      int32_t* bucket_rows, int32_t* bucket_splits, int32_t* bucket_table_cols,
+                      int32_t* seq_lens, int32_t* q_indices, int32_t* out_indices,
+                      int32_t* tables, int64_t table_capacity, int64_t* out_table_elems) {
+  if (count <= 0 || !lengths || !request_ids || !page_indptr || !page_ids || page_size <= 0 ||
+      num_kv_heads <= 0)
+    return PKV_ERR_INVALID_ARGUMENT;
+  for (int32_t r = 0; r < count; ++r)
+    if (page_indptr[r + 1] <= page_indptr[r]) return PKV_ERR_INVALID_ARGUMENT;  // :756 reads [-1]
+  const int32_t single = pkv_use_single_bucket(lengths, count, single_bucket, adaptive_route);
+  // Group rows (:734-745).
+  std::vector<int32_t> keys;                 // bucket lengths, first-appearance order
+  std::vector<std::vector<int32_t>> rows;    // offsets per bucket
+  if (single) {
+    keys.push_back(*std::max_element(lengths, lengths + count));
+    rows.emplace_back();
+    for (int32_t r = 0; r < count; ++r) rows[0].push_back(r);
+  } else {
+    for (int32_t r = 0; r < count; ++r) {
+      const int32_t allocated = page_indptr[r + 1] - page_indptr[r];
+      const int32_t key = pkv_round_bucket_length(lengths[r], bucket_tokens, allocated, page_size);
+      size_t j = 0;
+      while (j < keys.size() && keys[j] != key) ++j;
+      if (j == keys.size()) {
+        keys.push_back(key);
+        rows.emplace_back();
+      }
+      rows[j].push_back(r);
+    }
+  }
+  int64_t elems = 0;
+  for (size_t j = 0; j < keys.size(); ++j)
+    elems += (int64_t)rows[j].size() * (keys[j] > 0 ? ceil_div_pos(keys[j], page_size) : 0);
+  if (out_bucket_count) *out_bucket_count = (int32_t)keys.size();
+  if (out_table_elems) *out_table_elems = elems;
+  if (elems > table_capacity) return PKV_ERR_CAPACITY;
+  if (!bucket_lengths || !bucket_rows || !bucket_splits || !bucket_table_cols || !seq_lens ||
+      !q_indices || !out_indices || (elems > 0 && !tables))
+    return PKV_ERR_INVALID_ARGUMENT;
+  int64_t t = 0;
+  int32_t n = 0;
+  std::vector<int32_t> lens;
+  for (size_t j = 0; j < keys.size(); ++j) {
+    const int64_t cols = keys[j] > 0 ? ceil_div_pos(keys[j], page_size) : 0;  // :748
+    lens.clear();
+    for (const int32_t r : rows[j]) {
+      const int32_t p0 = page_indptr[r], p1 = page_indptr[r + 1];
+      for (int64_t c = 0; c < cols; ++c)  // :752-757
+        tables[t++] = c < p1 - p0 ? page_ids[p0 + c] : page_ids[p1 - 1];
+      seq_lens[n] = lengths[r];
+      q_indices[n] = request_ids[r];
+      out_indices[n] = r;
+      lens.push_back(lengths[r]);
+      ++n;
+    }
+    bucket_lengths[j] = keys[j];
+    bucket_rows[j] = (int32_t)rows[j].size();
+    bucket_table_cols[j] = (int32_t)cols;
+    bucket_splits[j] = pkv_choose_splits(lens.data(), (int32_t)lens.size(), requested_splits,
+                                         auto_splits, single, num_kv_heads, policy);  // :759-761
   }
   return PKV_OK;
 }

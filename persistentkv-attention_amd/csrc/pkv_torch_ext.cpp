@@ -666,7 +666,16 @@ void persistentkv_append_kv_fp8(torch::Tensor k_new, torch::Tensor v_new, torch:
   append_op(k_new, v_new, k_pages, v_pages, block_table, seq_lens, true, k_scale, v_scale);
 }
 
+int64_t persistentkv_direct_workspace_floats(int64_t batch, int64_t num_q_heads,
+                                             int64_t num_kv_heads, int64_t context) {
+  return (int64_t)(pkv_direct_workspace_bytes(i32(batch, "batch"), i32(num_q_heads, "Hq"),
+                                              i32(num_kv_heads, "Hkv"), i32(context, "context")) /
+                   sizeof(float));
+}
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("direct_workspace_floats", &persistentkv_direct_workspace_floats,
+        "fp32 workspace elements with which a num_splits == 1 launch runs its full internal split");
   m.def("paged_attention", &persistentkv_paged_attention, "PersistentKV native paged attention");
   m.def("paged_attention_masked", &persistentkv_paged_attention_masked,
         "PersistentKV native paged attention with per-request sequence lengths");

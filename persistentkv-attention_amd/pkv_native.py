@@ -66,6 +66,8 @@ def lib():
     so.pkv_workspace_bytes.argtypes = [_I32, _I32, _I32]
     so.pkv_workqueue_workspace_bytes.restype = ctypes.c_size_t
     so.pkv_workqueue_workspace_bytes.argtypes = [_I32, _I32]
+    so.pkv_direct_workspace_bytes.restype = ctypes.c_size_t
+    so.pkv_direct_workspace_bytes.argtypes = [_I32, _I32, _I32, _I32]
     so.pkv_cost_model_preset.argtypes = [_I32, ctypes.POINTER(CostModel)]
     so.pkv_cost_model_preset.restype = None
     so.pkv_choose_workqueue_row_splits.argtypes = [_I32] * 6
@@ -87,24 +89,27 @@ def lib():
         _PI32, _PI32, _I32, _PI32, _PI32, _I32, _I32, _I32, _I32, _I32, _I32,
         _PI32, _I32, _PI32, _PI32, _PI32, _PI32, _PI32, _I32, _PI32, _PI32, _PI32]
     so.pkv_build_workqueue.restype = ctypes.c_int
-    so.pkv_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, _I32, ctypes.c_void_p,
-                                  ctypes.c_void_p]
-    so.pkv_probe_read.restype = ctypes.c_int
-    so.pkv_probe_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
-                                  ctypes.c_void_p]
-    so.pkv_probe_copy.restype = ctypes.c_int
-    so.pkv_probe_read_cus.argtypes = [ctypes.c_void_p, ctypes.c_size_t, _I32, _I32,
-                                      ctypes.c_void_p, ctypes.c_void_p]
-    so.pkv_probe_read_cus.restype = ctypes.c_int
-    so.pkv_probe_read_inflight.argtypes = [ctypes.c_void_p, ctypes.c_size_t, _I32, _I32, _I32,
-                                           _I32, ctypes.c_void_p, ctypes.c_void_p]
-    so.pkv_probe_read_inflight.restype = ctypes.c_int
+    so.pkv_round_bucket_length.argtypes = [_I32] * 4
+    so.pkv_round_bucket_length.restype = _I32
+    so.pkv_use_single_bucket.argtypes = [_PI32, _I32, _I32, _I32]
+    so.pkv_use_single_bucket.restype = _I32
+    _PI64 = ctypes.POINTER(ctypes.c_int64)
+    so.pkv_build_buckets.argtypes = [
+        _PI32, _PI32, _I32, _PI32, _PI32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32,
+        _PI32, _PI32, _PI32, _PI32, _PI32, _PI32, _PI32, _PI32, _PI32, ctypes.c_int64, _PI64]
+    so.pkv_build_buckets.restype = ctypes.c_int
     _lib = so
     return so
 
 
 def last_error() -> str:
     return lib().pkv_last_error().decode()
+
+
+def direct_workspace_bytes(batch, hq, hkv, context) -> int:
+    """Workspace bytes with which a direct (num_splits == 1) launch runs its full internal
+    split (pkv_direct_workspace_bytes)."""
+    return int(lib().pkv_direct_workspace_bytes(batch, hq, hkv, context))
 
 
 def _arr(values):
@@ -199,6 +204,55 @@ def build_workqueue(lengths, request_ids, page_lists, page_size, requested_split
                 q_indices=qi, out_indices=oi, work_items=items[:out_tasks.value],
                 split_offsets=offs, total_partial_slots=int(out_slots.value),
                 splits=int(max(1, row_splits.max())) if count else 1)
+
+
+def round_bucket_length(length, bucket_tokens, allocated_pages, page_size=16) -> int:
+    return lib().pkv_round_bucket_length(length, bucket_tokens, allocated_pages, page_size)
+
+
+def use_single_bucket(lengths, requested_single_bucket, adaptive_route) -> bool:
+    a, p = _arr(lengths)
+    return bool(lib().pkv_use_single_bucket(p, len(a), int(bool(requested_single_bucket)),
+                                            int(bool(adaptive_route))))
+
+
+def build_buckets(lengths, request_ids, page_lists, page_size, requested_splits, auto_splits,
+                  bucket_tokens=0, single_bucket=False, adaptive_route=False, hkv=8,
+                  policy=POLICY_REFERENCE):
+    """One step's length-bucket metadata (pkv_build_buckets): a list of dicts with
+    bucket_length, block_table [rows, cols], seq_lens, q_indices, out_indices, splits."""
+    count = len(lengths)
+    la, lp = _arr(lengths)
+    ra, rp = _arr(request_ids)
+    indptr = np.zeros(count + 1, dtype=np.int32)
+    for r, pages in enumerate(page_lists):
+        indptr[r + 1] = indptr[r] + len(pages)
+    ids = np.ascontiguousarray(np.concatenate([np.asarray(p, dtype=np.int32) for p in page_lists])
+                               if count else np.zeros(0, dtype=np.int32))
+    n_buckets, elems = _I32(), ctypes.c_int64()
+    per = [np.zeros(max(count, 1), dtype=np.int32) for _ in range(7)]
+    blen, brows, bsplit, bcols, seq, qi, oi = per
+    args = lambda tables, cap: (
+        lp, rp, count, indptr.ctypes.data_as(_PI32), ids.ctypes.data_as(_PI32), page_size,
+        requested_splits, int(bool(auto_splits)), bucket_tokens, int(bool(single_bucket)),
+        int(bool(adaptive_route)), hkv, policy, ctypes.byref(n_buckets),
+        *(x.ctypes.data_as(_PI32) for x in per), tables, cap, ctypes.byref(elems))
+    st = lib().pkv_build_buckets(*args(None, 0))
+    if st not in (PKV_OK, PKV_ERR_CAPACITY):
+        raise ValueError(f"pkv_build_buckets failed with status {st}")
+    tables = np.zeros(max(int(elems.value), 1), dtype=np.int32)
+    st = lib().pkv_build_buckets(*args(tables.ctypes.data_as(_PI32), tables.size))
+    if st != PKV_OK:
+        raise ValueError(f"pkv_build_buckets failed with status {st}")
+    out, r0, t0 = [], 0, 0
+    for j in range(n_buckets.value):
+        n, c = int(brows[j]), int(bcols[j])
+        out.append(dict(bucket_length=int(blen[j]), block_table=tables[t0:t0 + n * c].reshape(n, c),
+                        seq_lens=seq[r0:r0 + n].copy(), q_indices=qi[r0:r0 + n].copy(),
+                        out_indices=oi[r0:r0 + n].copy(), splits=int(bsplit[j])))
+        r0 += n
+        t0 += n * c
+    return out
 
 
 def header_functions(path: str = HEADER_PATH):

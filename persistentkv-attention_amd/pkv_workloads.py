@@ -379,12 +379,18 @@ def compile_step(w: Workload, step_index: int, device) -> StepMeta:
 
 
 def workspace_for(w: Workload, metas, device):
+    """One fp32 workspace for every step of ``metas``: the work queue's partial states,
+    a split grid's, or for a direct (num_splits == 1) launch the size at which the op
+    runs its full internal split (pkv_direct_workspace_bytes)."""
     floats = 1
     for m in metas:
         if m.op == "paged_attention_workqueue":
             floats = max(floats, m.total_partial_slots * w.hq * (2 + HEAD_DIM))
         elif m.splits > 1:
             floats = max(floats, len(m.seq_lens) * w.hq * m.splits * (2 + HEAD_DIM))
+        else:
+            floats = max(floats, pkv_native.direct_workspace_bytes(
+                len(m.seq_lens), w.hq, w.hkv, m.bucket_length) // 4)
     return torch.empty(floats, device=device, dtype=torch.float32)
 
 
@@ -405,9 +411,12 @@ def run_step(ext, w: Workload, meta: StepMeta, step_index: int, q_pool, k_pages,
     also writes them into the pools (indexed and work-queue ops)."""
     q_source = q_pool[step_index]
     if new_kv is not None:
-        if meta.op not in ("paged_attention_workqueue", "paged_attention_indexed"):
-            raise ValueError(f"the fused append is provided for the work-queue and indexed "
-                             f"ops, not {meta.op}")
+        if meta.op not in ("paged_attention_workqueue", "paged_attention_indexed",
+                           "paged_attention_masked"):
+            raise ValueError(f"the fused append is provided for the work-queue, indexed and "
+                             f"masked ops, not {meta.op}")
+        if meta.op == "paged_attention_masked" and w.kv_fp8:
+            raise ValueError("the masked op has no fp8 variant")
         if meta.op == "paged_attention_workqueue" and w.kv_fp8:
             ext.paged_attention_workqueue_fp8_append(
                 q_source, k_pages, v_pages, meta.block_table, meta.seq_lens, meta.work_items,
@@ -425,6 +434,11 @@ def run_step(ext, w: Workload, meta: StepMeta, step_index: int, q_pool, k_pages,
                 meta.split_offsets, meta.merge_counters, meta.q_indices, meta.out_indices,
                 meta.output, workspace, meta.bucket_length, w.page_size, meta.total_partial_slots,
                 w.fused_merge, new_kv[0], new_kv[1])
+        elif meta.op == "paged_attention_masked":
+            q = meta.q if meta.q is not None else q_source.index_select(0, meta.q_indices.long()).contiguous()
+            ext.paged_attention_masked_append(
+                q, k_pages, v_pages, meta.block_table, meta.seq_lens, meta.output, workspace,
+                meta.bucket_length, w.page_size, meta.splits, new_kv[0], new_kv[1])
         else:
             ext.paged_attention_indexed_append(
                 q_source, k_pages, v_pages, meta.block_table, meta.seq_lens, meta.q_indices,

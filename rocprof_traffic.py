@@ -2,7 +2,8 @@
 
 FETCH_SIZE and WRITE_SIZE (KiB per dispatch) are each scaled by what the same counter
 reads for ``pkv_probe_copy`` of a known byte count (``hbm_probe.py copy``), then averaged
-over the last ``--launches`` dispatches of the decode kernel (bench.py's decode-only pass):
+over the last ``--launches`` dispatches of the decode kernel (bench.py's decode-only pass
+with ``--steps`` equal to ``--launches``, which replays the same trace sample):
 
   python rocprof_traffic.py --fetch F.csv --write W.csv --copy-fetch CF.csv \
       --copy-write CW.csv --copy-mib 1024 --launches 96 --workload c4 -o traffic.json
@@ -20,8 +21,9 @@ import os
 import sys
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-if _HERE not in sys.path:
-    sys.path.insert(0, _HERE)
+for _p in (os.path.join(_HERE, "persistentkv-attention_amd"), _HERE):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
 
 
 def counter_values(path, counter, kernel_substring):
@@ -65,7 +67,9 @@ def main(argv=None):
     work = wl.CONFIGS[a.workload](seed=a.seed)
     elem = 2
     step_bytes = [sum(s.lengths) * work.hkv * 128 * 2 * elem for s in work.steps]
-    alg = sum(step_bytes[k % len(step_bytes)] for k in range(a.launches)) / a.launches
+    from bench import trace_sample  # the trace steps bench.py's decode-only pass replays
+
+    alg = sum(step_bytes[i] for i in trace_sample(a.launches, len(step_bytes))) / a.launches
     out = {
         "kernel": a.kernel, "workload": a.workload, "launches": len(f),
         "fetch_kib_per_launch": round(sum(f) / len(f), 3),

@@ -10,8 +10,11 @@ records input/output pairs of its CPU-only functions, which no closed form pins:
                     model_bucket_splits :396-402, model_workqueue_splits :405-415
   * cost model      estimate_route_ms :418-442, choose_adaptive_route_cost_model :445-488
   * trace RNG       make_lengths :163-195, build_requests :232-282, build_steps :285-298
+  * length buckets  round_bucket_length :316-321, use_single_bucket_for_state :491-504
 The module globals HKV and PAGE_SIZE are set the way the reference's main() sets them
-(:1215-1217).  Functions that touch the GPU are not called.
+(:1215-1217).  Functions that touch the GPU are not called.  The draws of each section
+come after those of the sections above it, so adding a section leaves the earlier
+vectors unchanged.
 """
 from __future__ import annotations
 
@@ -39,7 +42,8 @@ def main(root):
     ref = load_reference(root)
     rng = random.Random(1234)
     out = {"source": "tests/benchmark_serving_trace.py", "row_splits": [], "choose_splits": [],
-           "model_splits": [], "routes": [], "traces": []}
+           "model_splits": [], "routes": [], "traces": [], "round_bucket": [],
+           "single_bucket": []}
 
     lengths_grid = [0, 1, 31, 32, 33, 100, 255, 256, 511, 512, 1023, 1024, 2047, 2048, 4096,
                     6000, 8192, 12288, 16383, 16384, 16385, 24576, 32768, 49152, 65536, 131072]
@@ -106,6 +110,29 @@ def main(root):
                 "steps": [[s.step, list(s.active_ids), list(s.lengths)] for s in steps],
             })
     ref.PAGE_SIZE = 16
+
+    # round_bucket_length(length, bucket_tokens, allocated_pages) at each page size.
+    for page in (8, 16, 32, 64, 128):
+        ref.PAGE_SIZE = page
+        for length in (1, 7, 8, 15, 16, 17, 100, 1000, 1024, 4095, 4096, 4097, 16384, 20000,
+                       32768, 65535, 65536):
+            for bucket_tokens in (-1, 0, 1, 16, 100, 512, 1024, 4096, 8192):
+                for pages in (0, 1, 3, 64, 512, 5000):
+                    out["round_bucket"].append(
+                        [page, length, bucket_tokens, pages,
+                         ref.round_bucket_length(length, bucket_tokens, pages)])
+    ref.PAGE_SIZE = 16
+    # use_single_bucket_for_state(state, requested_single_bucket, adaptive_route).
+    for _ in range(400):
+        n = rng.choice([1, 2, 3, 4, 5, 6, 8, 9, 16])
+        pool = rng.choice([[1024], [1024, 2048], [100, 200, 300, 400], list(range(1, 40))])
+        lens = [rng.choice(pool) for _ in range(n)]
+        state = ref.StepState(0, tuple(range(n)), tuple(lens))
+        for single in (False, True):
+            for adaptive in (False, True):
+                out["single_bucket"].append(
+                    [lens, int(single), int(adaptive),
+                     int(ref.use_single_bucket_for_state(state, single, adaptive))])
 
     path = os.path.join(HERE, "policy_vectors.json")
     with open(path, "w") as fh:

@@ -297,6 +297,101 @@ def test_fused_append_workqueue_equals_append_then_decode(ext, gpu, lengths, hkv
     assert_parity(o2, ref)
 
 
+@pytest.mark.parametrize("op", ["indexed", "masked", "workqueue"])
+def test_fused_append_skipped_rows_equal_append_then_decode(ext, gpu, op):
+    """The fused append on the rows the append kernel skips (ROWS: no tokens, a position
+    past the 3-column table, a page id of -1, a page id outside the 12-page pool) next to
+    ordinary rows: pools and output equal append_kv followed by the op, bit for bit (the
+    decode clamps those lengths and page ids the same way in both)."""
+    ps, hkv, hq, pages, dtype = 16, 4, 16, 12, F16
+    table = torch.tensor([r for _, r in ROWS], dtype=torch.int32)
+    lens = [n for n, _ in ROWS]
+    b = len(ROWS)
+    k0, v0 = _pools(pages, hkv, ps, dtype, seed=5)
+    kn, vn = (t.to(gpu) for t in _new_tokens(b, hkv, dtype, seed=6))
+    gen = torch.Generator().manual_seed(7)
+    q = torch.randn(b, hq, 128, generator=gen).to(dtype).to(gpu)
+    bt, sl = table.to(gpu), torch.tensor(lens, dtype=torch.int32, device=gpu)
+    idx = torch.arange(b, dtype=torch.int32, device=gpu)
+    if op == "workqueue":
+        meta = pkv_native.build_workqueue(lens, list(range(b)), [r for _, r in ROWS], ps, 2,
+                                          False, hkv)
+        t = lambda a: torch.as_tensor(a, dtype=torch.int32, device=gpu)
+        slots = meta["total_partial_slots"]
+        wi, so = t(meta["work_items"]), t(meta["split_offsets"])
+        ws = torch.empty(slots * hq * 130, dtype=torch.float32, device=gpu)
+    else:
+        ws = torch.empty(b * hq * 2 * 130, dtype=torch.float32, device=gpu)
+    results = []
+    for fused in (False, True):
+        k, v = k0.to(gpu), v0.to(gpu)
+        out = torch.full((b, hq, 128), float("nan"), dtype=dtype, device=gpu)
+        if op == "workqueue":
+            counters = torch.zeros(b, hkv, dtype=torch.int32, device=gpu)
+            args = (q, k, v, bt, sl, wi, so, counters, idx, idx, out, ws, max(lens), ps, slots,
+                    False)
+            call = ext.paged_attention_workqueue_append if fused else ext.paged_attention_workqueue
+        elif op == "indexed":
+            args = (q, k, v, bt, sl, idx, idx, out, ws, 48, ps, 2)  # 3 columns of 16 tokens
+            call = ext.paged_attention_indexed_append if fused else ext.paged_attention_indexed
+        else:
+            args = (q, k, v, bt, sl, out, ws, 48, ps, 2)
+            call = ext.paged_attention_masked_append if fused else ext.paged_attention_masked
+        if fused:
+            call(*args, kn, vn)
+        else:
+            ext.append_kv(kn, vn, k, v, bt, sl)
+            call(*args)
+        torch.cuda.synchronize()
+        results.append((out.cpu(), k.cpu(), v.cpu()))
+    (o1, k1, v1), (o2, k2, v2) = results
+    assert torch.equal(k2, k1) and torch.equal(v2, v1)
+    assert torch.equal(o2, o1)
+    k_ref, v_ref = oracle.append_kv(k0, v0, table, torch.tensor(lens, dtype=torch.int32),
+                                    kn.cpu(), vn.cpu())
+    assert torch.equal(k2, k_ref) and torch.equal(v2, v_ref)
+
+
+@pytest.mark.parametrize("op", ["indexed", "workqueue", "indexed_fp8"])
+def test_fused_append_rejected_before_any_write(ext, gpu, op):
+    """A fused-append op whose workspace is too small raises before the append runs: the
+    pools stay bit-identical (page 5 and fp8 pools run the append kernel inside the op)."""
+    lengths, hq, hkv = [90, 41], 32, 8
+    ps = 5 if op == "indexed" else 16
+    case = make_case(lengths, hq, hkv, ps, F16, seed=3)
+    b = len(lengths)
+    kn, vn = (t.to(gpu) for t in _new_tokens(b, hkv, F16, seed=4))
+    q, bt, sl = case.q.to(gpu), case.block_table.to(gpu), case.seq_lens.to(gpu)
+    idx = torch.arange(b, dtype=torch.int32, device=gpu)
+    out = torch.zeros(b, hq, 128, dtype=F16, device=gpu)
+    small = torch.empty(16, dtype=torch.float32, device=gpu)
+    if op == "indexed_fp8":
+        k = (case.k_pages.float() / 0.05).clamp(-448, 448).to(F8).to(gpu)
+        v = (case.v_pages.float() / 0.05).clamp(-448, 448).to(F8).to(gpu)
+    else:
+        k, v = case.k_pages.to(gpu), case.v_pages.to(gpu)
+    k_before, v_before = k.clone(), v.clone()
+    with pytest.raises(RuntimeError, match="workspace"):
+        if op == "indexed":
+            ext.paged_attention_indexed_append(q, k, v, bt, sl, idx, idx, out, small, 90, ps, 2,
+                                               kn, vn)
+        elif op == "indexed_fp8":
+            ext.paged_attention_indexed_fp8_append(q, k, v, bt, sl, idx, idx, out, small, 90, ps,
+                                                   2, 0.05, 0.05, kn, vn)
+        else:
+            meta = pkv_native.build_workqueue(lengths, list(range(b)), case.page_lists, ps, 2,
+                                              False, hkv)
+            t = lambda a: torch.as_tensor(a, dtype=torch.int32, device=gpu)
+            counters = torch.zeros(b, hkv, dtype=torch.int32, device=gpu)
+            ext.paged_attention_workqueue_append(
+                q, k, v, t(meta["block_table"]), t(meta["seq_lens"]), t(meta["work_items"]),
+                t(meta["split_offsets"]), counters, t(meta["q_indices"]), t(meta["out_indices"]),
+                out, small, meta["bucket_length"], ps, meta["total_partial_slots"], False, kn, vn)
+    torch.cuda.synchronize()
+    view = (lambda x: x.view(torch.uint8)) if op == "indexed_fp8" else (lambda x: x)
+    assert torch.equal(view(k), view(k_before)) and torch.equal(view(v), view(v_before))
+
+
 def test_fused_append_validation(ext, gpu):
     case = make_case([64], 32, 8, 16, F16)
     q, k, v = case.q.to(gpu), case.k_pages.to(gpu), case.v_pages.to(gpu)

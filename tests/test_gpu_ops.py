@@ -22,9 +22,17 @@ def _dev(case, dev):
             case.seq_lens.to(dev))
 
 
-def _ws(batch, hq, splits, dev):
-    return torch.empty(max(1, batch * hq * splits * 130) if splits > 1 else 0,
-                       dtype=torch.float32, device=dev)
+def _ws(batch, hq, splits, dev, direct=None):
+    """Workspace of a split launch; for splits == 1, ``direct = (ext, hkv, context)`` sizes
+    it for the op's full internal split (empty otherwise: the single launch)."""
+    if splits > 1:
+        floats = max(1, batch * hq * splits * 130)
+    elif direct is not None:
+        ext, hkv, ctx = direct
+        floats = ext.direct_workspace_floats(batch, hq, hkv, ctx)
+    else:
+        floats = 0
+    return torch.empty(floats, dtype=torch.float32, device=dev)
 
 
 # (B, Hq, Hkv, context, page_size, splits, dtype, table)
@@ -60,7 +68,7 @@ def test_paged_attention(ext, gpu, b, hq, hkv, ctx, ps, splits, dtype, table):
     case = make_case([ctx] * b, hq, hkv, ps, dtype, seed=ctx + splits, table=table)
     q, k, v, bt, _ = _dev(case, gpu)
     out = torch.full((b, hq, 128), float("nan"), dtype=dtype, device=gpu)
-    ext.paged_attention(q, k, v, bt, out, _ws(b, hq, splits, gpu), ctx, ps, splits)
+    ext.paged_attention(q, k, v, bt, out, _ws(b, hq, splits, gpu, (ext, hkv, ctx)), ctx, ps, splits)
     torch.cuda.synchronize()
     ref = oracle.paged_decode(case.q, case.k_pages, case.v_pages, case.block_table, case.seq_lens)
     assert_parity(out, ref)
@@ -152,7 +160,7 @@ def test_attention_contiguous_and_query_head_baseline(ext, gpu, b, hq, hkv, n, s
     ref = torch.stack([oracle.sdpa_row(q[i], k[i], v[i]) for i in range(b)])
     qd, kd, vd = q.to(gpu), k.to(gpu), v.to(gpu)
     out = torch.full((b, hq, 128), float("nan"), dtype=dtype, device=gpu)
-    ext.attention_contiguous(qd, kd, vd, out, _ws(b, hq, splits, gpu), splits)
+    ext.attention_contiguous(qd, kd, vd, out, _ws(b, hq, splits, gpu, (ext, hkv, n)), splits)
     base = torch.full_like(out, float("nan"))
     ext.attention_query_head_baseline(qd, kd, vd, base)
     torch.cuda.synchronize()
@@ -354,7 +362,7 @@ def test_hip_graph_replay(ext, gpu):
     tail = [meta["bucket_length"], 16, meta["total_partial_slots"], False]
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):  # eager run on the capture stream (allocates its scratch)
+    with torch.cuda.stream(s):  # eager run on the capture stream
         ext.paged_attention_workqueue(*args, out, ws, *tail)
     torch.cuda.synchronize()
     eager = out.clone()

@@ -1,0 +1,81 @@
+"""The serving harness on the GPU: multi-bucket steps through per-bucket
+paged_attention_indexed launches (the reference's length-bucket route,
+benchmark_serving_trace.py:731-780, :986-1000) and the adaptive engine's routed steps,
+each against the repack + fp32 SDPA oracle; and the harness's own gate."""
+import pytest
+import torch
+
+import pkv_serving as serving
+import pkv_workloads as wl
+from oracle import attention as oracle
+from paged_cases import assert_parity
+
+pytestmark = pytest.mark.gpu
+
+
+def _oracle(w, meta, q_source, k_pages, v_pages):
+    """Oracle output [rows, Hq, 128] (rows in output order); only each row's pages leave
+    the GPU."""
+    out = torch.zeros(meta.output.shape[0], w.hq, 128)
+    for b, n in enumerate(meta.seq_lens.tolist()):
+        pages = meta.block_table[b, : -(-n // w.page_size)].long()
+        k = k_pages.index_select(0, pages).cpu()
+        v = v_pages.index_select(0, pages).cpu()
+        kk, vv = oracle.gather_row(k, v, torch.arange(len(pages), dtype=torch.int32), n)
+        out[int(meta.out_indices[b])] = oracle.sdpa_row(q_source[int(meta.q_indices[b])].cpu(), kk, vv)
+    return out
+
+
+@pytest.mark.parametrize("bucket_tokens,single,splits", [(0, False, 4), (4096, False, 8),
+                                                         (0, True, 20), (0, False, 1)])
+def test_multi_bucket_step_matches_oracle(ext, gpu, bucket_tokens, single, splits):
+    w = wl.config_c4()
+    q_pool = wl.make_q_pool(w, gpu)
+    k, v = wl.make_kv_pool(w, gpu)
+    for i in (5, 30):
+        step = serving.compile_bucket_step(w, i, gpu, splits, bucket_tokens=bucket_tokens,
+                                           single_bucket=single)
+        if not single:
+            assert len(step.buckets) >= 2
+        ws = serving.bucket_workspace(w, [step], gpu)
+        out = serving.run_bucket_step(ext, w, step, i, q_pool, k, v, ws)
+        torch.cuda.synchronize()
+        eng_meta = serving.Engine.gate_meta(_Holder(step), 0)
+        assert_parity(out, _oracle(w, eng_meta, q_pool[i], k, v))
+
+
+class _Holder:
+    """Engine.gate_meta reads .meta[i]; this holds one bucket step."""
+    def __init__(self, step):
+        self.meta = [("bucket", step)]
+
+
+@pytest.mark.parametrize("name", ["c4", "c5_g8"])
+def test_adaptive_engine_matches_oracle(ext, gpu, name):
+    w = wl.CONFIGS[name]()
+    eng = serving.Engine("adaptive", w, gpu)
+    routes = {r for r, _ in eng.routes}
+    assert routes <= {"persistentkv_bucket", "persistentkv_workqueue"}
+    q_pool = wl.make_q_pool(w, gpu)
+    k, v = wl.make_kv_pool(w, gpu)
+    for i in (0, len(w.steps) // 2, len(w.steps) - 1):
+        out = eng.run(ext, i, q_pool, k, v)
+        torch.cuda.synchronize()
+        assert_parity(out, _oracle(w, eng.gate_meta(i), q_pool[i], k, v))
+        gate = serving.gate_step(out, eng.gate_meta(i), q_pool[i], k, v, w.page_size)
+        assert gate["pass"], gate
+
+
+def test_harness_run_reports_every_engine(ext, gpu):
+    """One repeat of C3 at 32k through the three engines: the gate passes, timing and
+    profiles are filled in, and the bucket engine launches one bucket per step."""
+    rep = serving.run_workload(ext, "c3_32k", ["bucket", "workqueue", "adaptive"], 1, 2, 2, gpu,
+                               wl.DEFAULT_SEED)
+    assert set(rep["engines"]) == {"bucket", "workqueue", "adaptive"}
+    for e in rep["engines"].values():
+        assert e["gate"]["pass"]
+        s = e["stats"]
+        assert s["steps"] == rep["trace_steps"] and s["event_mean_ms"] > 0
+        assert s["event_p50_ms"] <= s["event_p95_ms"] <= s["event_p99_ms"]
+    assert rep["engines"]["bucket"]["profile"]["launches_per_step"] == 2.0
+    assert "persistentkv_workqueue" in rep["engines"]["workqueue"]["profile"]["route_counts"]

@@ -22,6 +22,20 @@ def test_library_exports_every_header_function():
     assert not missing, missing
 
 
+def test_probe_library_is_separate():
+    """The HBM probes (include/pkv_probe.h) live in libpkv_probe.so, not in the engine."""
+    import os
+    probe_header = os.path.join(os.path.dirname(pkv_native.HEADER_PATH), "pkv_probe.h")
+    names = pkv_native.header_functions(probe_header)
+    assert set(names) == {"pkv_probe_read", "pkv_probe_copy", "pkv_probe_read_cus",
+                          "pkv_probe_read_inflight"}
+    probe = ctypes.CDLL(os.path.join(os.path.dirname(pkv_native.LIBRARY_PATH), "libpkv_probe.so"))
+    assert all(hasattr(probe, n) for n in names)
+    engine = pkv_native.lib()
+    assert not any(hasattr(engine, n) for n in names)
+    assert not any(n.startswith("pkv_probe") for n in pkv_native.header_functions())
+
+
 def test_op_module_surface():
     import persistentkv_torch_ext as ext
     for name in ("paged_attention", "paged_attention_masked", "paged_attention_indexed",
@@ -49,6 +63,11 @@ def test_workspace_sizes():
     assert lib.pkv_workspace_bytes(8, 32, 1) == 0                      # cuh:894-895
     assert lib.pkv_workspace_bytes(8, 32, 20) == 8 * 32 * 20 * 130 * 4  # cuh:896-897
     assert lib.pkv_workqueue_workspace_bytes(160, 32) == 160 * 32 * 130 * 4
+    # direct launches: ~256 units of >= 2 tiles from the caller's workspace
+    assert pkv_native.direct_workspace_bytes(1, 32, 8, 2048) == 1 * 32 * 32 * 130 * 4
+    assert pkv_native.direct_workspace_bytes(1, 32, 8, 200) == 1 * 32 * 3 * 130 * 4  # 7 tiles
+    assert pkv_native.direct_workspace_bytes(1, 32, 8, 64) == 0    # 2 tiles: not split
+    assert pkv_native.direct_workspace_bytes(16, 32, 8, 8192) == 0  # 128 units: not split
 
 
 def _call_paged(**overrides):

@@ -103,3 +103,91 @@ def test_builder_invariants_random():
         auto = rng.random() < 0.5
         meta = wq.build_workqueue(lengths, list(range(n)), page_lists, ps, rng.randint(1, 40), auto, hkv)
         check_builder_invariants(meta, lengths, hkv, page_lists, ps)
+
+
+def test_round_bucket_length_matches_reference(golden):
+    for page, length, bucket_tokens, pages, expected in golden["round_bucket"]:
+        assert wq.round_bucket_length(length, bucket_tokens, pages, page) == expected
+
+
+def test_round_bucket_length_hand_worked():
+    """Worked by hand (page 16): 1000 tokens in 512-token buckets -> 1024; capped by the
+    row's 40 allocated pages -> 640; bucket 100 -> 1000 rounds to 1000, then to the page
+    multiple 1008; 7 tokens with 1-token buckets -> one page, 16; no bucketing -> 1000."""
+    assert wq.round_bucket_length(1000, 512, 1000) == 1024
+    assert wq.round_bucket_length(1000, 512, 40) == 640
+    assert wq.round_bucket_length(1000, 100, 1000) == 1008
+    assert wq.round_bucket_length(7, 1, 10) == 16
+    assert wq.round_bucket_length(1000, 0, 1) == 1000
+
+
+def test_planted_bucket_rounding_mistake_fails(golden):
+    """A restatement that forgets the page rounding after the bucket rounding disagrees
+    with the reference's vectors."""
+    def wrong(length, bucket_tokens, pages, page):
+        if bucket_tokens <= 0:
+            return length
+        return min(((length + bucket_tokens - 1) // bucket_tokens) * bucket_tokens, pages * page)
+    assert any(wrong(length, b, pages, page) != expected
+               for page, length, b, pages, expected in golden["round_bucket"])
+
+
+def test_use_single_bucket_matches_reference(golden):
+    for lens, single, adaptive, expected in golden["single_bucket"]:
+        assert int(wq.use_single_bucket(lens, bool(single), bool(adaptive))) == expected
+
+
+def test_bucket_builder_hand_worked_example():
+    """Rows with lengths 300, 1000, 310, 1000 (page 16, 2 KV heads, 4 splits requested),
+    exact buckets: 300 -> [row 0], 1000 -> [rows 1, 3], 310 -> [row 2], in that (first
+    appearance) order; tables of ceil(300/16) = 19, 63 and 20 columns."""
+    pages = [list(range(100, 119)), list(range(200, 263)), list(range(300, 320)),
+             list(range(400, 463))]
+    got = wq.build_buckets([300, 1000, 310, 1000], [7, 8, 9, 10], pages, 16, 4, False, hkv=2)
+    assert [b["bucket_length"] for b in got] == [300, 1000, 310]
+    assert [b["out_indices"] for b in got] == [[0], [1, 3], [2]]
+    assert [b["q_indices"] for b in got] == [[7], [8, 10], [9]]
+    assert [b["seq_lens"] for b in got] == [[300], [1000, 1000], [310]]
+    assert [len(b["block_table"][0]) for b in got] == [19, 63, 20]
+    assert got[1]["block_table"][1] == list(range(400, 463))
+    assert all(b["splits"] == 4 for b in got)
+    # 512-token buckets: 300, 310 and 1000 round up to 512 and 1024, then are capped at
+    # each row's allocated pages (19, 20, 63 x 16 tokens), so the rows stay apart.
+    got = wq.build_buckets([300, 1000, 310, 1000], [7, 8, 9, 10], pages, 16, 4, False,
+                           bucket_tokens=512, hkv=2)
+    assert [b["bucket_length"] for b in got] == [304, 1008, 320]
+    # A single ragged bucket of max length; rows padded with their last page.
+    got = wq.build_buckets([300, 1000, 310, 1000], [7, 8, 9, 10], pages, 16, 4, False,
+                           single_bucket=True, hkv=2)
+    assert len(got) == 1 and got[0]["bucket_length"] == 1000
+    assert got[0]["block_table"][0] == list(range(100, 119)) + [118] * (63 - 19)
+
+
+def check_bucket_invariants(buckets, lengths, request_ids, page_lists, page_size):
+    seen = sorted(o for b in buckets for o in b["out_indices"])
+    assert seen == list(range(len(lengths)))
+    firsts = [b["out_indices"][0] for b in buckets]
+    assert firsts == sorted(firsts)  # buckets in order of first appearance
+    for b in buckets:
+        cols = -(-b["bucket_length"] // page_size)
+        assert b["out_indices"] == sorted(b["out_indices"])
+        for row, o, n, q in zip(b["block_table"], b["out_indices"], b["seq_lens"], b["q_indices"]):
+            assert n == lengths[o] and q == request_ids[o] and len(row) == cols
+            p = page_lists[o]
+            assert list(row[:len(p)]) == list(p[:cols]) and all(x == p[-1] for x in row[len(p):])
+
+
+def test_bucket_builder_invariants_random():
+    rng = random.Random(11)
+    for _ in range(300):
+        n = rng.randint(1, 9)
+        ps = rng.choice([8, 16, 32])
+        lengths = [rng.choice([rng.randint(1, 3000), 1024, 2048]) for _ in range(n)]
+        page_lists = [list(range(1000 * r, 1000 * r + -(-lengths[r] // ps) + rng.randint(0, 5)))
+                      for r in range(n)]
+        b = rng.choice([0, 0, 256, 1000])
+        got = wq.build_buckets(lengths, list(range(50, 50 + n)), page_lists, ps,
+                               rng.randint(1, 40), rng.random() < 0.5, bucket_tokens=b,
+                               single_bucket=rng.random() < 0.2, adaptive_route=rng.random() < 0.5,
+                               hkv=rng.choice([1, 8]))
+        check_bucket_invariants(got, lengths, list(range(50, 50 + n)), page_lists, ps)

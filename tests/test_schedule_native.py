@@ -91,3 +91,55 @@ def test_c4_step_uses_twenty_splits():
                                16, 20, False, 8)
     assert meta["total_partial_slots"] == 160
     assert np.all(np.diff(meta["split_offsets"]) == 20)
+
+
+def test_bucket_functions_match_reference(golden):
+    for page, length, bucket_tokens, pages, expected in golden["round_bucket"]:
+        assert nat.round_bucket_length(length, bucket_tokens, pages, page) == expected
+    for lens, single, adaptive, expected in golden["single_bucket"]:
+        assert int(nat.use_single_bucket(lens, single, adaptive)) == expected
+
+
+@settings(max_examples=300, deadline=None)
+@given(st.lists(st.integers(1, 40000), min_size=1, max_size=10), st.integers(1, 48),
+       st.booleans(), st.sampled_from([0, 0, 256, 1000, 4096]), st.booleans(), st.booleans(),
+       st.sampled_from([1, 2, 8, 32]), st.sampled_from([8, 16, 32, 64]), st.integers(0, 1 << 30))
+def test_bucket_builder_matches_python_restatement(lengths, requested, auto, bucket_tokens, single,
+                                                   adaptive, hkv, ps, seed):
+    rng = np.random.default_rng(seed)
+    n = len(lengths)
+    # repeated lengths so that rows share buckets
+    lengths = [lengths[int(rng.integers(0, n))] if rng.random() < 0.4 else x for x in lengths]
+    page_lists = [list(rng.integers(0, 1 << 20, size=int(rng.integers(1, 3000 // ps + 2)))) for _ in range(n)]
+    ids = [int(x) for x in rng.permutation(n + 3)[:n]]
+    py = wq.build_buckets(lengths, ids, page_lists, ps, requested, auto, bucket_tokens, single,
+                          adaptive, hkv)
+    cc = nat.build_buckets(lengths, ids, page_lists, ps, requested, auto, bucket_tokens, single,
+                           adaptive, hkv)
+    assert len(cc) == len(py)
+    for c, p in zip(cc, py):
+        assert c["bucket_length"] == p["bucket_length"] and c["splits"] == p["splits"]
+        assert c["block_table"].tolist() == p["block_table"]
+        assert c["seq_lens"].tolist() == p["seq_lens"]
+        assert c["q_indices"].tolist() == p["q_indices"]
+        assert c["out_indices"].tolist() == p["out_indices"]
+
+
+def test_mi355x_router_never_leaves_the_engine(golden):
+    """The MI355X policy routes every step to one of the engine's own routes (split grid or
+    work queue), for every G, length and active count; the reference policy keeps its
+    FlashInfer fallback (pinned by test_cost_model_and_router_match_reference)."""
+    lens_grid = [1, 31, 32, 256, 2048, 8192, 16383, 16384, 32768, 65536, 131072]
+    cases = [[x] * n for x in lens_grid for n in (1, 2, 3, 4, 7, 8, 9, 16, 64)]
+    cases += [lens for _, lens, _, _ in golden["routes"]]
+    cases += [lens for _, lens, _, _ in golden["model_splits"]]
+    cases += [[2048], [20000, 30000, 300], [20000] * 4]
+    routes = set()
+    for hq, hkv in ((32, 8), (32, 1), (32, 4), (32, 32), (48, 2), (27, 1)):
+        m = nat.cost_model(nat.POLICY_MI355X, num_q_heads=hq, num_kv_heads=hkv)
+        for lens in cases:
+            route, splits, ms = nat.choose_adaptive_route(lens, m)
+            assert route in ("persistentkv_bucket", "persistentkv_workqueue"), (hq, hkv, lens)
+            assert splits >= 1 and ms > 0
+            routes.add(route)
+    assert routes == {"persistentkv_bucket", "persistentkv_workqueue"}
