@@ -297,16 +297,31 @@ def test_fused_append_workqueue_equals_append_then_decode(ext, gpu, lengths, hkv
     assert_parity(o2, ref)
 
 
+# rows: (seq_len, block-table row) over a 16-page pool, the skip cases of ROWS arranged so
+# that no row reads a page another row appends to (the fused ops' precondition: a row's
+# tail slot is read by no other row of the step)
+FUSED_ROWS = [
+    (1, [3, 13, 13]),      # first slot of the first page
+    (16, [5, 7, 14]),      # last slot of page 0
+    (17, [1, 2, 15]),      # first slot of the second page
+    (40, [9, 10, 11]),     # last page of the table
+    (0, [4, 4, 4]),        # no tokens: skipped
+    (49, [6, 6, 6]),       # position 48 is past the 3-column table: skipped
+    (20, [8, -1, 0]),      # page id -1: skipped (the decode clamps it to page 0)
+    (33, [0, 12, 16]),     # page id 16 is outside the pool: skipped (decoded as page 15)
+]
+
+
 @pytest.mark.parametrize("op", ["indexed", "masked", "workqueue"])
 def test_fused_append_skipped_rows_equal_append_then_decode(ext, gpu, op):
-    """The fused append on the rows the append kernel skips (ROWS: no tokens, a position
-    past the 3-column table, a page id of -1, a page id outside the 12-page pool) next to
-    ordinary rows: pools and output equal append_kv followed by the op, bit for bit (the
-    decode clamps those lengths and page ids the same way in both)."""
-    ps, hkv, hq, pages, dtype = 16, 4, 16, 12, F16
-    table = torch.tensor([r for _, r in ROWS], dtype=torch.int32)
-    lens = [n for n, _ in ROWS]
-    b = len(ROWS)
+    """The fused append on the rows the append kernel skips (no tokens, a position past
+    the 3-column table, a page id of -1, a page id outside the pool) next to ordinary
+    rows: pools and output equal append_kv followed by the op, bit for bit (the decode
+    clamps those lengths and page ids the same way in both)."""
+    ps, hkv, hq, pages, dtype = 16, 4, 16, 16, F16
+    table = torch.tensor([r for _, r in FUSED_ROWS], dtype=torch.int32)
+    lens = [n for n, _ in FUSED_ROWS]
+    b = len(FUSED_ROWS)
     k0, v0 = _pools(pages, hkv, ps, dtype, seed=5)
     kn, vn = (t.to(gpu) for t in _new_tokens(b, hkv, dtype, seed=6))
     gen = torch.Generator().manual_seed(7)
@@ -314,8 +329,8 @@ def test_fused_append_skipped_rows_equal_append_then_decode(ext, gpu, op):
     bt, sl = table.to(gpu), torch.tensor(lens, dtype=torch.int32, device=gpu)
     idx = torch.arange(b, dtype=torch.int32, device=gpu)
     if op == "workqueue":
-        meta = pkv_native.build_workqueue(lens, list(range(b)), [r for _, r in ROWS], ps, 2,
-                                          False, hkv)
+        meta = pkv_native.build_workqueue(lens, list(range(b)), [r for _, r in FUSED_ROWS], ps,
+                                          2, False, hkv)
         t = lambda a: torch.as_tensor(a, dtype=torch.int32, device=gpu)
         slots = meta["total_partial_slots"]
         wi, so = t(meta["work_items"]), t(meta["split_offsets"])
