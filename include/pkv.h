@@ -142,6 +142,30 @@ int pkv_paged_attention_workqueue(
     int32_t bucket_context, int32_t total_partial_slots, int32_t fused_merge,
     int32_t dtype, void* stream);
 
+/* pkv_paged_attention_workqueue without the workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid allocation).  It has no counterpart in the reference.  The partial states
+ * go to a 16 MiB static scratch array in the library's code object (one per GPU, held
+ * until the process ends); the call allocates nothing.  It returns
+ * PKV_ERR_WORKSPACE_TOO_SMALL when pkv_workqueue_workspace_bytes(total_partial_slots,
+ * num_q_heads) exceeds 16 MiB.  Every call on one GPU shares that GPU's scratch: calls
+ * that overlap on one GPU (on other streams, or graph replays running at the same time)
+ * race and give wrong results.  The scratch's address is taken on the calling thread's
+ * current HIP device, which must be the device of `stream`.  Same results as
+ * pkv_paged_attention_workqueue, bit for bit. */
+int pkv_paged_attention_workqueue_noalloc(
+    const void* q_source, int32_t q_rows,
+    const void* k_pages, const void* v_pages,
+    const int32_t* block_table, const int32_t* seq_lens,
+    const int32_t* work_items, int32_t num_tasks,
+    const int32_t* split_offsets, int32_t* merge_counters,
+    const int32_t* q_indices, const int32_t* out_indices,
+    void* output, int32_t out_rows,
+    int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t num_pages, int32_t page_size, int32_t max_pages,
+    int32_t bucket_context, int32_t total_partial_slots, int32_t fused_merge,
+    int32_t dtype, void* stream);
+
 /* The two stages of pkv_paged_attention_workqueue with fused_merge == 0, callable on
  * their own (for per-kernel timing and for callers that overlap the merge with other
  * work).  Running decode then merge on one stream equals the combined call.  The

@@ -2043,6 +2043,45 @@ int run_queue_decode(const QueueCall& c, hipStream_t stream, const KvQuant& kq) 
   return st == PKV_OK ? ok() : st;
 }
 
+// ---------------------------------------------------------------------------------
+// Static scratch of the allocation-free work-queue entry point: the partial states of
+// one call, in device memory that the code object brings with it (each GPU the library
+// runs on holds its own copy until the process ends).  On the host, `scratch` names a
+// host-side stand-in, never the device array: its device address comes from
+// hipGetSymbolAddress, taken once per device on that device's first call, and only that
+// address is passed to kernels.  Every call on a GPU shares that GPU's array, so calls
+// that overlap on one GPU (other streams, concurrent graph replays) race.  The work-queue
+// op needs no part of it cleared: every partial state it merges is written by the same
+// call first, and the slots of empty splits are skipped, not read.
+// ---------------------------------------------------------------------------------
+constexpr size_t kScratchBytes = 16u << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+// Device address of `scratch` on the current device, or null (with the error set).
+void* scratch_address() {
+  static std::mutex mu;
+  static void* address[64] = {};
+  int device = -1;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) {
+    (void)hipGetLastError();
+    fail(PKV_ERR_LAUNCH, "no current HIP device for the static scratch");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!address[device]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      (void)hipGetLastError();
+      fail(PKV_ERR_LAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", device,
+           hipGetErrorString(e));
+      return nullptr;
+    }
+    address[device] = p;
+  }
+  return address[device];
+}
+
 }  // namespace pkv
 
 using namespace pkv;
@@ -2166,6 +2205,29 @@ int pkv_paged_attention_workqueue(
                     q_source, k_pages, v_pages, q_rows, block_table, seq_lens, work_items,
                     split_offsets, q_indices, out_indices, merge_counters, output, out_rows,
                     workspace, workspace_bytes, bucket_context, num_tasks, total_partial_slots};
+  return run_workqueue(c, fused_merge, (hipStream_t)stream, KvQuant{});
+}
+
+int pkv_paged_attention_workqueue_noalloc(
+    const void* q_source, int32_t q_rows, const void* k_pages, const void* v_pages,
+    const int32_t* block_table, const int32_t* seq_lens, const int32_t* work_items,
+    int32_t num_tasks, const int32_t* split_offsets, int32_t* merge_counters,
+    const int32_t* q_indices, const int32_t* out_indices, void* output, int32_t out_rows,
+    int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t num_pages,
+    int32_t page_size, int32_t max_pages, int32_t bucket_context, int32_t total_partial_slots,
+    int32_t fused_merge, int32_t dtype, void* stream) {
+  const size_t need = pkv_workqueue_workspace_bytes(total_partial_slots, num_q_heads);
+  if (need > kScratchBytes)
+    return fail(PKV_ERR_WORKSPACE_TOO_SMALL,
+                "the partial states of %d slots x %d heads need %zu bytes, more than the %zu-byte "
+                "static scratch of pkv_paged_attention_workqueue_noalloc",
+                total_partial_slots, num_q_heads, need, kScratchBytes);
+  void* ws = scratch_address();
+  if (!ws) return PKV_ERR_LAUNCH;
+  const QueueCall c{{batch, num_q_heads, num_kv_heads, head_dim, num_pages, page_size, max_pages, dtype},
+                    q_source, k_pages, v_pages, q_rows, block_table, seq_lens, work_items,
+                    split_offsets, q_indices, out_indices, merge_counters, output, out_rows,
+                    ws, kScratchBytes, bucket_context, num_tasks, total_partial_slots};
   return run_workqueue(c, fused_merge, (hipStream_t)stream, KvQuant{});
 }
 
