@@ -249,19 +249,22 @@ def main():
     total_bytes = sum(sample_bytes)
 
     def decode_stage(i, m, kp, vp):
-        if w.kv_fp8:
-            ext.workqueue_decode_fp8(q_pool[i], kp, vp, m.block_table, m.seq_lens, m.work_items,
-                                     m.split_offsets, m.q_indices, ws, m.bucket_length,
-                                     w.page_size, m.total_partial_slots, w.k_scale, w.v_scale)
-        else:
-            ext.workqueue_decode(q_pool[i], kp, vp, m.block_table, m.seq_lens, m.work_items,
-                                 m.split_offsets, m.q_indices, ws, m.bucket_length, w.page_size,
-                                 m.total_partial_slots)
+        # Stage 1 of the op as it runs (the balanced or the per-item schedule).
+        ext.paged_attention_workqueue_stage(1, q_pool[i], kp, vp, m.block_table, m.seq_lens,
+                                            m.work_items, m.split_offsets, m.q_indices,
+                                            m.out_indices, m.output, ws, m.bucket_length,
+                                            w.page_size, m.total_partial_slots, w.kv_fp8,
+                                            w.k_scale, w.v_scale)
 
     # Decode kernel alone (stage 1 of the work-queue op) over the same sample, one event
     # pair per launch on its stream.  The grid ops have no separate stage entry point:
-    # their whole op is timed.
-    queue = w.op == "paged_attention_workqueue"
+    # their whole op is timed.  With the fused merge there are no stages: the op is timed.
+    queue = w.op == "paged_attention_workqueue" and not w.fused_merge
+    schedule = None
+    if w.op == "paged_attention_workqueue":
+        schedule = ("balanced" if ext.workqueue_schedule(
+            max(len(m.seq_lens) for m in metas), w.hq, w.hkv, w.page_size, ws.numel(),
+            w.fused_merge) else "per-item")
 
     def launch(k):
         i = sample[k]
@@ -287,6 +290,24 @@ def main():
     b1.record()
     torch.cuda.synchronize()
     batched_us = b0.elapsed_time(b1) * 1e3 / args.steps
+    merge_us = None
+    if queue:  # stage 2 (the merge) alone, back to back over the same sample
+        def merge_stage(k):
+            i = sample[k]
+            m = metas[i]
+            kp, vp = pools[k % len(pools)]
+            ext.paged_attention_workqueue_stage(2, q_pool[i], kp, vp, m.block_table, m.seq_lens,
+                                                m.work_items, m.split_offsets, m.q_indices,
+                                                m.out_indices, m.output, ws, m.bucket_length,
+                                                w.page_size, m.total_partial_slots, w.kv_fp8,
+                                                w.k_scale, w.v_scale)
+        m0, m1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        m0.record()
+        for k in range(args.steps):
+            merge_stage(k)
+        m1.record()
+        torch.cuda.synchronize()
+        merge_us = m0.elapsed_time(m1) * 1e3 / args.steps
     # Roofline numerator over the back-to-back launches: event packets between launches
     # add a few microseconds that are not kernel time (rocprofv3's kernel-trace average
     # duration matches the back-to-back figure to about 1 %).
@@ -304,7 +325,9 @@ def main():
                         f"scaled to this sample")
 
     value = total_bytes / (gpu_ms / 1e3) / 1e9
-    kernel = {"paged_attention_workqueue": "decode_kernel<*,kQueue> (stage 1 only)",
+    kernel = {"paged_attention_workqueue": ("balanced_decode_kernel (stage 1 only)"
+                                            if schedule == "balanced" else
+                                            "decode_kernel<*,kQueue> (stage 1 only)"),
               "paged_attention_indexed": "decode_kernel<*,kSplit> + merge_kernel (whole op)",
               "paged_attention_masked": "decode_kernel<*,kSplit> + merge_kernel (whole op)",
               "paged_attention": "decode_kernel<*,kDirect> (whole op; split internally into "
@@ -340,6 +363,7 @@ def main():
                    "page_size": w.page_size,
                    "splits": "auto (mi355x planner)" if w.auto_splits else w.splits,
                    "fused_merge": bool(args.fused_merge),
+                   "schedule": schedule,
                    "launch": "hip graph replay" if args.graph else "eager",
                    "append_kv": args.append or False,
                    "sample": sample_text,
@@ -352,6 +376,7 @@ def main():
                      "traffic_source": traffic_note,
                      "kernel": kernel,
                      "mean_launch_us": round(batched_us, 2),
+                     "merge_stage_us": None if merge_us is None else round(merge_us, 2),
                      "mean_launch_us_event_bracketed": round(sum(dec_ms) / len(dec_ms) * 1e3, 2),
                      "algorithmic_bytes_per_launch": int(alg_per_launch)},
         "gate": gate,

@@ -151,8 +151,10 @@ int pkv_paged_attention_workqueue(
  * num_q_heads) exceeds 16 MiB.  Every call on one GPU shares that GPU's scratch: calls
  * that overlap on one GPU (on other streams, or graph replays running at the same time)
  * race and give wrong results.  The scratch's address is taken on the calling thread's
- * current HIP device, which must be the device of `stream`.  Same results as
- * pkv_paged_attention_workqueue, bit for bit. */
+ * current HIP device, which must be the device of `stream`.  Same results, bit for bit, as
+ * pkv_paged_attention_workqueue with a workspace of exactly
+ * pkv_workqueue_workspace_bytes(total_partial_slots, num_q_heads) bytes (the same
+ * schedule, see pkv_workqueue_schedule). */
 int pkv_paged_attention_workqueue_noalloc(
     const void* q_source, int32_t q_rows,
     const void* k_pages, const void* v_pages,
@@ -166,11 +168,52 @@ int pkv_paged_attention_workqueue_noalloc(
     int32_t bucket_context, int32_t total_partial_slots, int32_t fused_merge,
     int32_t dtype, void* stream);
 
-/* The two stages of pkv_paged_attention_workqueue with fused_merge == 0, callable on
- * their own (for per-kernel timing and for callers that overlap the merge with other
- * work).  Running decode then merge on one stream equals the combined call.  The
+/* Which schedule pkv_paged_attention_workqueue (and its fp8 and append variants) runs
+ * for these sizes on the current device: 1 = the balanced schedule, 0 = one workgroup per
+ * work item.  The balanced schedule streams every (row, kv head) pair's tiles with an equal
+ * share per wave (4 waves per CU) and merges the pieces; it applies when fused_merge == 0,
+ * G = num_q_heads / num_kv_heads <= 16, page_size is a multiple of 16, batch <= 256 and
+ * the workspace holds (batch * num_kv_heads + 4 * CUs) * G partial states of 130 floats.
+ * It reads the work items' row set, not their tile ranges: the queue must be complete
+ * (every non-empty split of every kv head of every row, as pkv_build_workqueue builds it),
+ * which is the only input on which the reference's merge reads no unwritten slot.  Both
+ * schedules give the same result to fp32 rounding.  No counterpart in the reference. */
+int pkv_workqueue_schedule(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                           int32_t page_size, size_t workspace_bytes, int32_t fused_merge);
+
+/* Workspace bytes the balanced schedule needs on the current device:
+ * (batch * num_kv_heads + 4 * CUs) * (num_q_heads / num_kv_heads) * 130 * 4.  A complete
+ * queue's reference-sized workspace (pkv_workqueue_workspace_bytes) often holds it already
+ * (C4: 2.66 MB against 2.26 MB).  No counterpart in the reference. */
+size_t pkv_workqueue_balanced_workspace_bytes(int32_t batch, int32_t num_q_heads,
+                                              int32_t num_kv_heads);
+
+/* One stage of pkv_paged_attention_workqueue (fused_merge == 0), in whichever schedule
+ * pkv_workqueue_schedule names: stage 1 = the decode kernel, 2 = the merge.  Stage 1 then
+ * stage 2 on one stream equal the combined call bit for bit; they exist for per-kernel
+ * timing and for callers that overlap the merge with other work.  kv_fp8 != 0 selects the
+ * fp8 K/V pages of pkv_paged_attention_workqueue_fp8 with k_scale / v_scale.  The
  * reference launches both from one host function (cuh:1005-1017); it has no separate
  * entry points. */
+int pkv_paged_attention_workqueue_stage(
+    int32_t stage, const void* q_source, int32_t q_rows,
+    const void* k_pages, const void* v_pages,
+    const int32_t* block_table, const int32_t* seq_lens,
+    const int32_t* work_items, int32_t num_tasks,
+    const int32_t* split_offsets, const int32_t* q_indices, const int32_t* out_indices,
+    void* output, int32_t out_rows,
+    void* workspace, size_t workspace_bytes,
+    int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t num_pages, int32_t page_size, int32_t max_pages,
+    int32_t bucket_context, int32_t total_partial_slots, int32_t kv_fp8, float k_scale,
+    float v_scale, int32_t dtype, void* stream);
+
+/* The two stages of the per-item schedule of pkv_paged_attention_workqueue with
+ * fused_merge == 0 (one workgroup per work item, partial states in the reference's slot
+ * format (split_offsets[b] + s) * Hq + qh), callable on their own.  Running decode then
+ * merge on one stream equals the combined call when it takes the per-item schedule
+ * (pkv_workqueue_schedule == 0).  The reference launches both from one host function
+ * (cuh:1005-1017); it has no separate entry points. */
 int pkv_workqueue_decode(
     const void* q_source, int32_t q_rows,
     const void* k_pages, const void* v_pages,

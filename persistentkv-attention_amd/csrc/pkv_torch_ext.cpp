@@ -666,6 +666,44 @@ void persistentkv_append_kv_fp8(torch::Tensor k_new, torch::Tensor v_new, torch:
   append_op(k_new, v_new, k_pages, v_pages, block_table, seq_lens, true, k_scale, v_scale);
 }
 
+// One stage of the work-queue op (1 = decode, 2 = merge) in the schedule the combined op
+// takes for these tensors; kv_fp8 selects float8_e4m3fn pages with k_scale / v_scale.
+void persistentkv_paged_attention_workqueue_stage(
+    int64_t stage, torch::Tensor q_source, torch::Tensor k_pages, torch::Tensor v_pages,
+    torch::Tensor block_table, torch::Tensor seq_lens, torch::Tensor work_items,
+    torch::Tensor split_offsets, torch::Tensor q_indices, torch::Tensor out_indices,
+    torch::Tensor output, torch::Tensor workspace, int64_t bucket_context, int64_t page_size,
+    int64_t total_partial_slots, bool kv_fp8, double k_scale, double v_scale) {
+  const QueueTensors t = check_queue_tensors(q_source, k_pages, v_pages, block_table, seq_lens,
+                                             work_items, split_offsets, q_indices, workspace,
+                                             bucket_context, page_size, total_partial_slots,
+                                             kv_fp8);
+  check_tensor(out_indices, "out_indices", at::kInt, 1);
+  check_tensor(output, "output", t.dt, 3);
+  TORCH_CHECK(output.size(1) == t.Hq && output.size(2) == t.d,
+              "output shape must match q head dimensions");
+  TORCH_CHECK(out_indices.size(0) == t.B, "out_indices batch mismatch");
+  const c10::DeviceGuard guard(q_source.device());
+  raise_on(pkv_paged_attention_workqueue_stage(
+      i32(stage, "stage"), q_source.data_ptr(), i32(q_source.size(0), "q_source.size(0)"),
+      k_pages.data_ptr(), v_pages.data_ptr(), block_table.data_ptr<int>(), seq_lens.data_ptr<int>(),
+      work_items.data_ptr<int>(), i32(work_items.size(0), "work_items.size(0)"),
+      split_offsets.data_ptr<int>(), q_indices.data_ptr<int>(), out_indices.data_ptr<int>(),
+      output.data_ptr(), i32(output.size(0), "output.size(0)"), ws_ptr(workspace),
+      ws_bytes(workspace), t.B, t.Hq, t.Hkv, t.d, i32(k_pages.size(0), "k_pages.size(0)"),
+      i32(page_size, "page_size"), i32(block_table.size(1), "block_table.size(1)"),
+      i32(bucket_context, "bucket_context"), i32(total_partial_slots, "total_partial_slots"),
+      kv_fp8 ? 1 : 0, (float)k_scale, (float)v_scale, pkv_dtype_of(t.dt), stream_of(q_source)));
+}
+
+int64_t persistentkv_workqueue_schedule(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                                        int64_t page_size, int64_t workspace_floats,
+                                        bool fused_merge) {
+  return pkv_workqueue_schedule(i32(batch, "batch"), i32(num_q_heads, "Hq"),
+                                i32(num_kv_heads, "Hkv"), i32(page_size, "page_size"),
+                                (size_t)workspace_floats * sizeof(float), fused_merge ? 1 : 0);
+}
+
 int64_t persistentkv_direct_workspace_floats(int64_t batch, int64_t num_q_heads,
                                              int64_t num_kv_heads, int64_t context) {
   return (int64_t)(pkv_direct_workspace_bytes(i32(batch, "batch"), i32(num_q_heads, "Hq"),
@@ -674,6 +712,10 @@ int64_t persistentkv_direct_workspace_floats(int64_t batch, int64_t num_q_heads,
 }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("paged_attention_workqueue_stage", &persistentkv_paged_attention_workqueue_stage,
+        "one stage (1 decode, 2 merge) of paged_attention_workqueue in the schedule it takes");
+  m.def("workqueue_schedule", &persistentkv_workqueue_schedule,
+        "1 when paged_attention_workqueue takes the balanced schedule for these sizes, else 0");
   m.def("direct_workspace_floats", &persistentkv_direct_workspace_floats,
         "fp32 workspace elements with which a num_splits == 1 launch runs its full internal split");
   m.def("paged_attention", &persistentkv_paged_attention, "PersistentKV native paged attention");

@@ -44,6 +44,13 @@ paged_attention_indexed = _ext.paged_attention_indexed
 paged_attention_workqueue = _ext.paged_attention_workqueue
 workqueue_decode = _ext.workqueue_decode
 workqueue_merge = _ext.workqueue_merge
+# The schedule of paged_attention_workqueue (1 = balanced: equal tile shares per wave over
+# every (row, kv head) pair of a complete queue; 0 = one workgroup per work item) for
+# (batch, Hq, Hkv, page_size, workspace floats, fused_merge), and one stage of it
+# (stage, then the paged_attention_workqueue tensors without merge_counters, then
+# bucket_context, page_size, total_partial_slots, kv_fp8, k_scale, v_scale).
+workqueue_schedule = _ext.workqueue_schedule
+paged_attention_workqueue_stage = _ext.paged_attention_workqueue_stage
 # fp8 (float8_e4m3fn) K/V pages with per-tensor scales: K = k_scale * k8, V = v_scale * v8.
 paged_attention_indexed_fp8 = _ext.paged_attention_indexed_fp8
 paged_attention_workqueue_fp8 = _ext.paged_attention_workqueue_fp8
@@ -86,7 +93,8 @@ def workqueue_workspace_floats(total_partial_slots: int, num_q_heads: int) -> in
 
 __all__ = [
     "paged_attention", "paged_attention_masked", "paged_attention_indexed",
-    "paged_attention_workqueue", "workqueue_decode", "workqueue_merge",
+    "paged_attention_workqueue", "workqueue_decode", "workqueue_merge", "workqueue_schedule",
+    "paged_attention_workqueue_stage",
     "paged_attention_indexed_fp8", "paged_attention_workqueue_fp8", "workqueue_decode_fp8",
     "attention_contiguous",
     "attention_query_head_baseline", "append_kv", "append_kv_fp8",

@@ -68,6 +68,10 @@ def lib():
     so.pkv_workqueue_workspace_bytes.argtypes = [_I32, _I32]
     so.pkv_direct_workspace_bytes.restype = ctypes.c_size_t
     so.pkv_direct_workspace_bytes.argtypes = [_I32, _I32, _I32, _I32]
+    so.pkv_workqueue_balanced_workspace_bytes.restype = ctypes.c_size_t
+    so.pkv_workqueue_balanced_workspace_bytes.argtypes = [_I32, _I32, _I32]
+    so.pkv_workqueue_schedule.restype = ctypes.c_int
+    so.pkv_workqueue_schedule.argtypes = [_I32, _I32, _I32, _I32, ctypes.c_size_t, _I32]
     so.pkv_cost_model_preset.argtypes = [_I32, ctypes.POINTER(CostModel)]
     so.pkv_cost_model_preset.restype = None
     so.pkv_choose_workqueue_row_splits.argtypes = [_I32] * 6
@@ -110,6 +114,18 @@ def direct_workspace_bytes(batch, hq, hkv, context) -> int:
     """Workspace bytes with which a direct (num_splits == 1) launch runs its full internal
     split (pkv_direct_workspace_bytes)."""
     return int(lib().pkv_direct_workspace_bytes(batch, hq, hkv, context))
+
+
+def workqueue_balanced_workspace_bytes(batch, hq, hkv) -> int:
+    """Workspace bytes with which the work-queue op takes its balanced schedule on the
+    current device (pkv_workqueue_balanced_workspace_bytes)."""
+    return int(lib().pkv_workqueue_balanced_workspace_bytes(batch, hq, hkv))
+
+
+def workqueue_schedule(batch, hq, hkv, page_size, workspace_bytes, fused_merge=False) -> int:
+    """1 when the work-queue op takes the balanced schedule, else 0 (pkv_workqueue_schedule)."""
+    return int(lib().pkv_workqueue_schedule(batch, hq, hkv, page_size, workspace_bytes,
+                                            int(bool(fused_merge))))
 
 
 def _arr(values):

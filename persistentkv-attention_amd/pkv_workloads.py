@@ -378,14 +378,19 @@ def compile_step(w: Workload, step_index: int, device) -> StepMeta:
                     t(np.arange(n)), output, w.splits, kv_bytes=w.kv_bytes(step_index))
 
 
-def workspace_for(w: Workload, metas, device):
-    """One fp32 workspace for every step of ``metas``: the work queue's partial states,
-    a split grid's, or for a direct (num_splits == 1) launch the size at which the op
-    runs its full internal split (pkv_direct_workspace_bytes)."""
+def workspace_for(w: Workload, metas, device, balanced=True):
+    """One fp32 workspace for every step of ``metas``: the work queue's partial states
+    (and, with ``balanced``, at least what its balanced schedule needs,
+    pkv_workqueue_balanced_workspace_bytes), a split grid's, or for a direct
+    (num_splits == 1) launch the size at which the op runs its full internal split
+    (pkv_direct_workspace_bytes)."""
     floats = 1
     for m in metas:
         if m.op == "paged_attention_workqueue":
             floats = max(floats, m.total_partial_slots * w.hq * (2 + HEAD_DIM))
+            if balanced:
+                floats = max(floats, pkv_native.workqueue_balanced_workspace_bytes(
+                    len(m.seq_lens), w.hq, w.hkv) // 4)
         elif m.splits > 1:
             floats = max(floats, len(m.seq_lens) * w.hq * m.splits * (2 + HEAD_DIM))
         else:
