@@ -900,8 +900,10 @@ struct LseAcc {
 };
 
 // Up to 32 slot states as one wave loads them: lane j holds (m, l) of slot c0 + j and
-// v[j] this lane's two dims of that slot's acc.  All loads are issued together; slots
-// past the chunk re-read its last one.
+// v[j] this lane's two dims of that slot's acc.  All loads are issued together; the acc
+// of slots past the chunk (n, uniform) is not loaded (v[j] = 0, and fold gives those
+// slots weight 0), since a merge of many short rows would otherwise spend most of its
+// time re-reading the last state.
 struct SlotChunk {
   float ms, ls;
   f32x2 v[kMergeChunk];
@@ -910,20 +912,21 @@ struct SlotChunk {
 template <bool COHERENT>
 __device__ inline void load_chunk(SlotChunk& c, const float* pm, const float* pl, const float* pacc,
                                   long base, long stride, int c0, int n, int lane) {
+  n = uniform(n);
   const int s_lane = c0 + (lane < n ? lane : n - 1);
   c.ms = get_f32<COHERENT>(pm + base + (long)s_lane * stride);
   c.ls = get_f32<COHERENT>(pl + base + (long)s_lane * stride);
 #pragma unroll
-  for (int j = 0; j < kMergeChunk; ++j) {
-    const int s = c0 + (j < n ? j : n - 1);
-    c.v[j] = get_f32x2<COHERENT>(pacc + (base + (long)s * stride) * kD + 2 * lane);
-  }
+  for (int j = 0; j < kMergeChunk; ++j)
+    c.v[j] = j < n ? get_f32x2<COHERENT>(pacc + (base + (long)(c0 + j) * stride) * kD + 2 * lane)
+                   : f32x2{0.f, 0.f};
 }
 
 // load_chunk through buffer descriptors that cover the chunk's states (n >= 1): when
 // `enable` is false they cover nothing, and the loads return zeros without reading memory.
 __device__ inline void load_chunk_if(SlotChunk& c, const float* pm, const float* pl, const float* pacc,
                                      long base, long stride, int n, int lane, bool enable) {
+  n = uniform(n);
   const int span = enable ? (int)((long)(n - 1) * stride + 1) : 0;  // states from base
   const __amdgpu_buffer_rsrc_t rm =
       __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(pm + base), (short)0, uniform(span * 4), kRsrcWord3);
@@ -935,11 +938,10 @@ __device__ inline void load_chunk_if(SlotChunk& c, const float* pm, const float*
   c.ms = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rm, (int)(s_lane * stride * 4), 0, 0));
   c.ls = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, (int)(s_lane * stride * 4), 0, 0));
 #pragma unroll
-  for (int j = 0; j < kMergeChunk; ++j) {
-    const int s = j < n ? j : n - 1;
-    c.v[j] = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(
-                                           ra, (int)((s * stride * kD + 2 * lane) * 4), 0, 0));
-  }
+  for (int j = 0; j < kMergeChunk; ++j)
+    c.v[j] = j < n ? __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                   ra, (int)((j * stride * kD + 2 * lane) * 4), 0, 0))
+                   : f32x2{0.f, 0.f};
 }
 
 // Whether slot s of a row holds a state: in queue mode the builder leaves splits with no
@@ -1559,25 +1561,31 @@ __global__ __launch_bounds__(64) void merge_kernel(MergeArgs a) {
 // (row, kv head) pair, as the builder emits it) covers each pair's tiles
 // [0, ceil(len / 32)) once, whatever its split counts; the combined work-queue op can
 // therefore stream those tiles with an equal share per wave instead of one workgroup per
-// item.  The pairs' tiles are laid end to end (rows in order, kv heads within a row), T in
-// all; wave v of V takes positions [floor(v T / V), floor((v + 1) T / V)), cutting pairs
-// anywhere, and writes one partial state per pair piece it holds.  The piece of pair p in
-// wave v goes to state group p + v: pieces are intervals of both orderings, so no two
-// pieces share a group, and the pieces of one pair lie in the groups p + va .. p + vb, va
-// and vb the waves of its first and last tile (position x is in wave
-// ceil((x + 1) V / T) - 1).  When T < V some waves hold no position; their groups are
-// skipped by the same rule as the empty splits of a work queue.  A group holds the pair's
-// G query heads; there are at most B * Hkv + V - 1 groups.  Waves run one per SIMD with two
-// tiles in flight, four per CU, with no LDS and no barrier; the merge recomputes the
-// layout from seq_lens.  The per-item schedule ends with a tail: C4 steps put 1.25 long
-// items on some CUs and 2 on others, and the CUs with two finish ~8 us later (per-wave
-// timestamps of the decode kernel).
+// item.  Each (row, kv head) pair with tiles is laid out as kBalPieceCost start-up
+// positions followed by its tiles, pairs end to end (rows in order, kv heads within a
+// row), T positions in all; wave v of V takes positions [floor(v T / V), floor((v + 1) T
+// / V)), cutting pairs anywhere, and writes one partial state per pair piece that holds
+// tiles.  The start-up positions carry no work: they charge each piece its fixed cost
+// (the Q loads, the first page lookups and the pipeline ramp, ~1-1.5 us per piece against
+// ~0.5-0.8 us per tile per wave in per-wave timestamps), so a wave that starts many short
+// rows takes fewer tiles.  The piece of pair p in wave v goes to state group p + v: pieces
+// are intervals of both orderings, so no two pieces share a group, and the pieces of one
+// pair lie in the groups p + va .. p + vb, va and vb the waves of its first and last tile
+// (position x is in wave ceil((x + 1) V / T) - 1).  When T < V some waves hold no
+// position; their groups are skipped by the same rule as the empty splits of a work
+// queue.  A group holds the pair's G query heads; there are at most B * Hkv + V - 1
+// groups.  Waves run one per SIMD with two tiles in flight, four per CU, with no LDS and
+// no barrier; the merge recomputes the layout from seq_lens.  The per-item schedule ends
+// with a tail: C4 steps put 1.25 long items on some CUs and 2 on others, and the CUs with
+// two finish ~8 us later (per-wave timestamps of the decode kernel).
 // ---------------------------------------------------------------------------------
 constexpr int kBalWaves = 4;      // waves per workgroup (one per SIMD) and per CU
 constexpr int kBalRowChunks = 4;  // lane l holds rows l + 64k, k < 4: batches up to 256
+constexpr int kBalPieceCost = 2;  // start-up positions of each (row, kv head) pair
 
 // The rows of a launch as one wave holds them: lane l keeps rows l + 64k (chunk k).  A
-// row weighs tiles * Hkv positions; incl is the inclusive prefix of weights in row order
+// row weighs (kBalPieceCost + tiles) * Hkv positions, 0 without tiles; incl is the
+// inclusive prefix of weights in row order
 // (rows past the batch weigh 0, so their prefix is the total).  The four chunks are
 // separate registers, never an array, so that selecting one by a run-time chunk index
 // does not put the table in scratch memory.
@@ -1608,7 +1616,8 @@ __device__ inline void row_chunk(const DecodeArgs& a, int lane, int k, int raw, 
                                  long& incl, long& carry) {
   const int r = lane + 64 * k;
   len = r < a.batch ? clamp_length(a, raw) : 0;
-  incl = wave_incl_scan((long)ceil_tiles(len) * a.hkv, lane) + carry;
+  const int tiles = ceil_tiles(len);
+  incl = wave_incl_scan(tiles > 0 ? (long)(tiles + kBalPieceCost) * a.hkv : 0, lane) + carry;
   carry = read_lane64(incl, 63);
 }
 
@@ -1670,14 +1679,18 @@ void balanced_decode_kernel(DecodeArgs a) {
   const long x1 = (v + 1) * T / V;
   const int G = a.group;
   while (x < x1) {
-    const int r = uniform(table_row(t, x));
+    const int r = uniform(table_row(t, x));  // a row with tiles: others hold no position
     const int len = uniform(table_len(t, r));
     const int tiles = ceil_tiles(len);
-    const long off = x - (table_incl(t, r) - (long)tiles * a.hkv);
-    const int kvh = uniform((int)(off / tiles));
-    const int t0 = uniform((int)(off - (long)kvh * tiles));
-    const long left = x1 - x;
-    const int t1 = uniform(left < tiles - t0 ? t0 + (int)left : tiles);
+    const long span = tiles + kBalPieceCost;  // positions of each of the row's pairs
+    const long off = x - (table_incl(t, r) - span * a.hkv);
+    const int kvh = uniform((int)(off / span));
+    const long pair0 = x - off + kvh * span;  // first position of pair (r, kvh)
+    const long e = x - pair0;                 // 0 <= e < span
+    const int t0 = uniform((int)(e > kBalPieceCost ? e - kBalPieceCost : 0));
+    const long lim = x1 - pair0 - kBalPieceCost;  // tiles of the pair within this wave
+    const int t1 = uniform(lim < tiles ? (int)(lim > 0 ? lim : 0) : tiles);
+    if (t1 <= t0) break;  // the range ends among the pair's start-up positions
     // The query row is requested first and waited for only at the Q loads; the first two
     // block-table reads go out beside it.
     const int q_loaded = load_vector_lanes(a.q_indices ? a.q_indices + r : nullptr,
@@ -1697,15 +1710,16 @@ void balanced_decode_kernel(DecodeArgs a) {
     const long group = (long)r * a.hkv + kvh + v;
     const Dest d{a.part_m, a.part_l, a.part_acc, group * G, 1, false};
     write_wave_state<Elem, 1, false>(a, st, qh0, 0, d, lane);
-    x += t1 - t0;
+    x = pair0 + kBalPieceCost + t1;
   }
 }
 
-// Merge of the balanced schedule: one workgroup of kBalMergeWaves waves per (row, query
-// head) folds the groups of its pair (the recomputed layout of balanced_decode_kernel over
-// `waves` waves): wave w folds the w-th quarter of the groups, and the partial merges are
-// combined through LDS (a long pair has ~80 groups at C4; one wave folding them chunk
-// after chunk took ~9 us).
+// Merge of the balanced schedule: one workgroup of nw = blockDim.x / 64 waves (1, 2 or
+// kBalMergeWaves) per (row, query head) folds the groups of its pair (the recomputed
+// layout of balanced_decode_kernel over `waves` waves): wave w folds the w-th of nw equal
+// shares of the groups, and the partial merges are combined through LDS.  A few long
+// pairs (~70 groups each at 8 rows) take 4 waves each; many short rows take one wave
+// each, so that the whole grid is resident at once (the kernel needs ~165 VGPRs).
 constexpr int kBalMergeWaves = 4;
 
 template <class Elem>
@@ -1714,6 +1728,7 @@ __global__ __launch_bounds__(kBalMergeWaves * 64) void balanced_merge_kernel(Dec
   __shared__ f32x2 sm_a[kBalMergeWaves][64];
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
+  const int nw = uniform(blockDim.x >> 6);
   const int wg = blockIdx.x;
   if (wg >= a.batch * a.hq) return;  // whole workgroup
   const int row = uniform(wg / a.hq);
@@ -1727,35 +1742,38 @@ __global__ __launch_bounds__(kBalMergeWaves * 64) void balanced_merge_kernel(Dec
   int count = 0, va = 0;
   long base = 0;
   if (tiles > 0) {
-    const long x0 = table_incl(t, row) - tiles * a.hkv + kvh * tiles;  // first position
+    const long span = tiles + kBalPieceCost;
+    const long x0 = table_incl(t, row) - span * a.hkv + kvh * span + kBalPieceCost;  // first tile
     va = (int)(((x0 + 1) * waves + T - 1) / T - 1);                      // wave of x0
     const int vb = (int)(((x0 + tiles) * waves + T - 1) / T - 1);         // wave of the last
     count = vb - va + 1;
     base = ((long)row * a.hkv + kvh + va) * a.group + h;
   }
   // This wave's share of the groups [c0, c1).
-  const int c0 = count * wave / kBalMergeWaves, c1 = count * (wave + 1) / kBalMergeWaves;
+  const int c0 = count * wave / nw, c1 = count * (wave + 1) / nw;
   LseAcc acc;
   // Groups of waves with no position are skipped, as the empty splits of a queue are.
   fold_slots_pipelined<true>(acc, a.part_m, a.part_l, a.part_acc, base + (long)c0 * a.group,
                              a.group, c1 - c0, T, waves, va + c0, lane);
-  if (lane == 0) {
-    sm_ml[wave][0] = acc.M;
-    sm_ml[wave][1] = acc.L;
-  }
-  sm_a[wave][lane] = acc.A;
-  __syncthreads();
-  if (wave != 0) return;
-  float M = -FLT_MAX;
-#pragma unroll
-  for (int w = 0; w < kBalMergeWaves; ++w) M = fmaxf(M, sm_ml[w][0]);
-  float L = 0.f;
-  f32x2 A = {0.f, 0.f};
-#pragma unroll
-  for (int w = 0; w < kBalMergeWaves; ++w) {
-    const float e = __builtin_amdgcn_exp2f((sm_ml[w][0] - M) * kLog2e);
-    L += e * sm_ml[w][1];
-    A += e * sm_a[w][lane];
+  float M = acc.M, L = acc.L;
+  f32x2 A = acc.A;
+  if (nw > 1) {
+    if (lane == 0) {
+      sm_ml[wave][0] = acc.M;
+      sm_ml[wave][1] = acc.L;
+    }
+    sm_a[wave][lane] = acc.A;
+    __syncthreads();
+    if (wave != 0) return;
+    M = -FLT_MAX;
+    for (int w = 0; w < nw; ++w) M = fmaxf(M, sm_ml[w][0]);
+    L = 0.f;
+    A = f32x2{0.f, 0.f};
+    for (int w = 0; w < nw; ++w) {
+      const float e = __builtin_amdgcn_exp2f((sm_ml[w][0] - M) * kLog2e);
+      L += e * sm_ml[w][1];
+      A += e * sm_a[w][lane];
+    }
   }
   const int out_row = a.out_indices ? uniform(out_row_loaded) : row;
   if (out_row < 0 || out_row >= a.out_rows) return;
@@ -2308,7 +2326,10 @@ int run_workqueue(const QueueCall& c, int32_t fused_merge, hipStream_t stream, c
     }
     if (stages & 2) {
       const int grid = c.g.batch * c.g.hq;
-      const int block = kBalMergeWaves * 64;
+      // Waves per (row, query head): the most that keep the grid within ~8 waves per CU.
+      int merge_waves = kBalMergeWaves;
+      while (merge_waves > 1 && (long)grid * merge_waves > 8L * cu_count()) merge_waves >>= 1;
+      const int block = merge_waves * 64;
       if (c.g.dtype == PKV_DTYPE_BF16) balanced_merge_kernel<BFloat><<<grid, block, 0, stream>>>(a, waves);
       else balanced_merge_kernel<Half><<<grid, block, 0, stream>>>(a, waves);
       e = hipGetLastError();

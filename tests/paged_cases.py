@@ -77,7 +77,11 @@ def assert_parity(out, ref):
         half_ulp = torch.exp2(torch.floor(torch.log2(mag)) - 8)
         excess = (diff - half_ulp).max().item()
         mean = (got[mask] - ref[mask].to(torch.bfloat16).float()).abs().mean().item()
+        print(f"parity bf16: raw max-abs {diff.max().item():.3e}, max-abs beyond half an "
+              f"output ulp {excess:.3e}, mean-abs vs bf16-rounded oracle {mean:.3e}, "
+              f"raw mean-abs {diff.mean().item():.3e}")
         assert excess < MAX_ABS and mean < MEAN_ABS, (excess, mean, diff.max().item())
     else:
         mx, mean = diff.max().item(), diff.mean().item()
+        print(f"parity {str(out.dtype).replace('torch.', '')}: max-abs {mx:.3e}, mean-abs {mean:.3e}")
         assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)

@@ -64,6 +64,10 @@ CASES = [
     ([4000, 600, 8100], 32, 2, 16, 3, F16),                              # G = 16
     ([31, 32, 33, 1] * 18, 32, 8, 16, 2, F16),                           # 72 rows: two row chunks
     ([40 + 13 * i for i in range(200)], 16, 8, 16, 2, F16),              # 200 rows, G = 2
+    # 24 rows x 32 heads: two merge waves per (row, query head) on 256 CUs
+    ([25000 if i % 8 == 0 else 200 + 97 * i for i in range(24)], 32, 8, 16, 3, BF16),
+    # 72 rows x 32 heads: one merge wave, two long rows with more than 32 groups per pair
+    ([30000 if i % 36 == 0 else 100 + 7 * i for i in range(72)], 32, 8, 16, 2, F16),
 ]
 
 
