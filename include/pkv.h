@@ -83,6 +83,18 @@ size_t pkv_workqueue_workspace_bytes(int32_t total_partial_slots, int32_t num_q_
 size_t pkv_direct_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
                                   int32_t context);
 
+/* Bytes of workspace with which a split launch (num_splits > 1) of the grid ops and of
+ * pkv_attention_contiguous runs its full internal sub-split: a launch of fewer
+ * batch * num_kv_heads * num_splits units than about 3/4 of the CUs cuts each split into
+ * sub-splits, to about one unit per CU (at least 2 tiles of 32 tokens each), merged
+ * together.  pkv_workspace_bytes(batch, num_q_heads, num_splits) when the launch is not
+ * sub-split; with that size (the reference's) the partial states keep the reference's
+ * layout; sizes in between give fewer sub-splits, with the same result to fp32 rounding
+ * (PKV_SPLIT_SUBDIVIDE=0 in the environment turns this off).  No counterpart in the
+ * reference, whose split launches use exactly the caller's split (cuh:947-974). */
+size_t pkv_split_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                                 int32_t context, int32_t num_splits);
+
 /* ---------------------------------------------------------------------------------
  * The four ops.  Argument order follows the torch op surface of
  * tests/persistentkv_torch_extension.cu, with the tensor shapes spelled out.

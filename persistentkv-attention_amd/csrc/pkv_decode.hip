@@ -1973,6 +1973,26 @@ int direct_splits(const Geometry& g, int context, size_t ws_bytes) {
   return s >= 2 ? (int)s : 1;
 }
 
+// Internal sub-splits per caller split wanted by a split launch of few units.  A launch of
+// B * Hkv * S units fewer than the CUs leaves CUs idle (B = 1, Hkv = 8, S = 16: 128 of 256
+// CUs), so each caller split is cut into k sub-splits, to about one unit per CU with at
+// least 2 tiles each; the merge folds all S * k partial states of a head.  More than one
+// unit per CU is slower (measured on C3 at 32k: 27.8 us with 256 units, 32.2 us with 512;
+// B1 G4 32k with S = 16: 38.4 us with 128 units, 28.3 us with 256, 29.4 us with 512).
+int split_factor_wanted(int batch, int hkv, int context, int num_splits) {
+  static const bool on = [] {
+    const char* e = getenv("PKV_SPLIT_SUBDIVIDE");
+    return !(e && e[0] == '0');
+  }();
+  const long units = (long)batch * hkv * num_splits;
+  const long cus = cu_count();
+  if (!on || units <= 0 || num_splits <= 1 || 4 * units >= 3 * cus) return 1;
+  const long tiles = (context + kTile - 1) / kTile;
+  long k = (cus + units - 1) / units;
+  while (k > 1 && num_splits * k * 2 > tiles) --k;
+  return (int)k;
+}
+
 DecodeArgs base_args(const Geometry& g, const void* q, int q_rows, const void* k, const void* v,
                      const int32_t* table, void* out, int out_rows) {
   DecodeArgs a = {};
@@ -2005,8 +2025,9 @@ struct GridPlan {
 };
 
 // Chooses the launches of a grid op and checks the workspace, before anything is launched
-// (cuh:929-974 persistentkv_launch).  `internal_split` lets a direct launch of few units
-// split itself into the caller's workspace when it is large enough.
+// (cuh:929-974 persistentkv_launch).  `internal_split` lets a launch of few units split
+// itself further into the caller's workspace when it is large enough: a direct launch
+// into about 256 units, a split launch into sub-splits of the caller's.
 int plan_grid(const Geometry& g, const DecodeArgs& a, void* ws, size_t ws_bytes, int num_splits,
               bool internal_split, GridPlan& plan) {
   plan.splits = num_splits;
@@ -2019,6 +2040,11 @@ int plan_grid(const Geometry& g, const DecodeArgs& a, void* ws, size_t ws_bytes,
   if (!ws || ws_bytes < need)
     return fail(PKV_ERR_WORKSPACE_TOO_SMALL, "split dispatch requires a workspace of %zu bytes (got %zu)",
                 need, ws ? ws_bytes : (size_t)0);
+  // Sub-splits of a few-unit launch, as many as the workspace holds (the caller's S alone
+  // with the reference's workspace size, whose partial states then keep its layout).
+  int k = internal_split ? split_factor_wanted(g.batch, g.hkv, a.context, num_splits) : 1;
+  while (k > 1 && pkv_workspace_bytes(g.batch, g.hq, num_splits * k) > ws_bytes) --k;
+  plan.splits = num_splits * k;
   return PKV_OK;
 }
 
@@ -2438,6 +2464,14 @@ size_t pkv_direct_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t nu
   if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || context <= 0) return 0;
   const int s = direct_splits_wanted(batch, num_kv_heads, context);
   return s > 1 ? pkv_workspace_bytes(batch, num_q_heads, s) : 0;
+}
+
+size_t pkv_split_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                                 int32_t context, int32_t num_splits) {
+  if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || context <= 0 || num_splits <= 1)
+    return 0;
+  const int k = split_factor_wanted(batch, num_kv_heads, context, num_splits);
+  return pkv_workspace_bytes(batch, num_q_heads, num_splits * k);
 }
 
 int pkv_paged_attention(const void* q, const void* k_pages, const void* v_pages,

@@ -711,6 +711,14 @@ int64_t persistentkv_direct_workspace_floats(int64_t batch, int64_t num_q_heads,
                    sizeof(float));
 }
 
+int64_t persistentkv_split_workspace_floats(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                                            int64_t context, int64_t num_splits) {
+  return (int64_t)(pkv_split_workspace_bytes(i32(batch, "batch"), i32(num_q_heads, "Hq"),
+                                             i32(num_kv_heads, "Hkv"), i32(context, "context"),
+                                             i32(num_splits, "num_splits")) /
+                   sizeof(float));
+}
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("paged_attention_workqueue_stage", &persistentkv_paged_attention_workqueue_stage,
         "one stage (1 decode, 2 merge) of paged_attention_workqueue in the schedule it takes");
@@ -718,6 +726,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "1 when paged_attention_workqueue takes the balanced schedule for these sizes, else 0");
   m.def("direct_workspace_floats", &persistentkv_direct_workspace_floats,
         "fp32 workspace elements with which a num_splits == 1 launch runs its full internal split");
+  m.def("split_workspace_floats", &persistentkv_split_workspace_floats,
+        "fp32 workspace elements with which a num_splits > 1 launch of few units runs its full "
+        "internal sub-split");
   m.def("paged_attention", &persistentkv_paged_attention, "PersistentKV native paged attention");
   m.def("paged_attention_masked", &persistentkv_paged_attention_masked,
         "PersistentKV native paged attention with per-request sequence lengths");

@@ -76,6 +76,7 @@ paged_attention_workqueue_fp8_append = _ext.paged_attention_workqueue_fp8_append
 # paged_attention_masked / _indexed or attention_contiguous runs its full internal split
 # (0 when it is not split; a smaller workspace gives a smaller split, an empty one none).
 direct_workspace_floats = _ext.direct_workspace_floats
+split_workspace_floats = _ext.split_workspace_floats
 
 HEAD_DIM = 128
 TILE_TOKENS = 32
@@ -101,5 +102,5 @@ __all__ = [
     "paged_attention_masked_append", "paged_attention_indexed_append",
     "paged_attention_workqueue_append",
     "paged_attention_indexed_fp8_append", "paged_attention_workqueue_fp8_append", "workspace_floats",
-    "workqueue_workspace_floats", "direct_workspace_floats", "EXTENSION_PATH", "LIBRARY_PATH",
+    "workqueue_workspace_floats", "direct_workspace_floats", "split_workspace_floats", "EXTENSION_PATH", "LIBRARY_PATH",
 ]

@@ -68,6 +68,8 @@ def lib():
     so.pkv_workqueue_workspace_bytes.argtypes = [_I32, _I32]
     so.pkv_direct_workspace_bytes.restype = ctypes.c_size_t
     so.pkv_direct_workspace_bytes.argtypes = [_I32, _I32, _I32, _I32]
+    so.pkv_split_workspace_bytes.restype = ctypes.c_size_t
+    so.pkv_split_workspace_bytes.argtypes = [_I32, _I32, _I32, _I32, _I32]
     so.pkv_workqueue_balanced_workspace_bytes.restype = ctypes.c_size_t
     so.pkv_workqueue_balanced_workspace_bytes.argtypes = [_I32, _I32, _I32]
     so.pkv_workqueue_schedule.restype = ctypes.c_int
@@ -114,6 +116,12 @@ def direct_workspace_bytes(batch, hq, hkv, context) -> int:
     """Workspace bytes with which a direct (num_splits == 1) launch runs its full internal
     split (pkv_direct_workspace_bytes)."""
     return int(lib().pkv_direct_workspace_bytes(batch, hq, hkv, context))
+
+
+def split_workspace_bytes(batch, hq, hkv, context, num_splits) -> int:
+    """Workspace bytes with which a split launch of few units runs its full internal
+    sub-split (pkv_split_workspace_bytes); the reference's size when it is not sub-split."""
+    return int(lib().pkv_split_workspace_bytes(batch, hq, hkv, context, num_splits))
 
 
 def workqueue_balanced_workspace_bytes(batch, hq, hkv) -> int:

@@ -381,7 +381,8 @@ def compile_step(w: Workload, step_index: int, device) -> StepMeta:
 def workspace_for(w: Workload, metas, device, balanced=True):
     """One fp32 workspace for every step of ``metas``: the work queue's partial states
     (and, with ``balanced``, at least what its balanced schedule needs,
-    pkv_workqueue_balanced_workspace_bytes), a split grid's, or for a direct
+    pkv_workqueue_balanced_workspace_bytes), a split grid's with room for its internal
+    sub-split (pkv_split_workspace_bytes), or for a direct
     (num_splits == 1) launch the size at which the op runs its full internal split
     (pkv_direct_workspace_bytes)."""
     floats = 1
@@ -392,7 +393,8 @@ def workspace_for(w: Workload, metas, device, balanced=True):
                 floats = max(floats, pkv_native.workqueue_balanced_workspace_bytes(
                     len(m.seq_lens), w.hq, w.hkv) // 4)
         elif m.splits > 1:
-            floats = max(floats, len(m.seq_lens) * w.hq * m.splits * (2 + HEAD_DIM))
+            floats = max(floats, pkv_native.split_workspace_bytes(
+                len(m.seq_lens), w.hq, w.hkv, m.bucket_length, m.splits) // 4)
         else:
             floats = max(floats, pkv_native.direct_workspace_bytes(
                 len(m.seq_lens), w.hq, w.hkv, m.bucket_length) // 4)

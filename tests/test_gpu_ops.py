@@ -288,6 +288,62 @@ def test_workqueue_matches_indexed_split_grid(ext, gpu):
     assert_parity(grid_out, ref)
 
 
+# (op, lengths, Hq, Hkv, splits, dtype): split launches of fewer units than 3/4 of the CUs
+SUBDIVIDED = [
+    ("paged", [8192], 32, 8, 16, F16),         # B1 G4 8k, S 16: 128 units, 2 sub-splits
+    ("paged", [3000], 8, 8, 4, BF16),          # 32 units, 8 sub-splits
+    ("masked", [3000, 100], 32, 8, 8, F16),    # short row: empty sub-splits
+    ("indexed", [2500, 33, 900], 32, 8, 4, BF16),
+    ("contiguous", [8192], 32, 8, 16, F16),    # the reference's B1 G4 8k performance case
+]
+
+
+def _split_op(ext, gpu, op, case, lengths, hq, hkv, splits, floats):
+    """One launch of ``op`` with a workspace of ``floats`` fp32 elements."""
+    q, k, v, bt, sl = _dev(case, gpu)
+    b, ctx = len(lengths), max(lengths)
+    ws = torch.empty(floats, dtype=torch.float32, device=gpu)
+    out = torch.full((b, hq, 128), float("nan"), dtype=case.q.dtype, device=gpu)
+    if op == "paged":
+        ext.paged_attention(q, k, v, bt, out, ws, ctx, 16, splits)
+    elif op == "masked":
+        ext.paged_attention_masked(q, k, v, bt, sl, out, ws, ctx, 16, splits)
+    elif op == "indexed":
+        idx = torch.arange(b, dtype=torch.int32, device=gpu).flip(0).contiguous()
+        ext.paged_attention_indexed(q, k, v, bt, sl, idx, idx, out, ws, ctx, 16, splits)
+    else:  # the row's pages laid end to end: [1, Hkv, ctx, 128]
+        pages = case.block_table[0, :-(-ctx // 16)].long()
+        kc, vc = (p[pages].permute(1, 0, 2, 3).reshape(1, hkv, -1, 128)[:, :, :ctx].contiguous()
+                  for p in (case.k_pages, case.v_pages))
+        ext.attention_contiguous(q, kc.to(gpu), vc.to(gpu), out, ws, splits)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("op,lengths,hq,hkv,splits,dtype", SUBDIVIDED)
+def test_split_launch_subdivided(ext, gpu, op, lengths, hq, hkv, splits, dtype):
+    """With the workspace of split_workspace_floats the op cuts each split into sub-splits
+    (merged together); it matches the oracle, and the reference-sized workspace (caller's
+    split only) and an in-between size give the same output to fp32 rounding."""
+    case = make_case(lengths, hq, hkv, 16, dtype, seed=len(lengths) * 7 + splits)
+    b, ctx = len(lengths), max(lengths)
+    ref_floats = b * hq * splits * 130
+    full = ext.split_workspace_floats(b, hq, hkv, ctx, splits)
+    assert full >= 2 * ref_floats  # the launch is sub-split
+    if op == "indexed":
+        idx = torch.arange(b, dtype=torch.int32).flip(0)
+        ref = oracle.paged_decode(case.q, case.k_pages, case.v_pages, case.block_table,
+                                  case.seq_lens, idx, idx, b)
+    else:
+        ref = oracle.paged_decode(case.q, case.k_pages, case.v_pages, case.block_table, case.seq_lens)
+    outs = [_split_op(ext, gpu, op, case, lengths, hq, hkv, splits, f)
+            for f in (full, ref_floats + (full - ref_floats) // 2, ref_floats)]
+    for out in outs:
+        assert_parity(out, ref)
+    for out in outs[1:]:
+        assert (out.float() - outs[0].float()).abs().max().item() < 1e-3
+
+
 def test_split_partial_states_match_oracle(ext, gpu):
     """The workspace holds the reference's partial-state format (cuh:615-632): per
     (row, head, split) m in natural-log units of the scaled score, l, acc[128]."""

@@ -68,6 +68,14 @@ def test_workspace_sizes():
     assert pkv_native.direct_workspace_bytes(1, 32, 8, 200) == 1 * 32 * 3 * 130 * 4  # 7 tiles
     assert pkv_native.direct_workspace_bytes(1, 32, 8, 64) == 0    # 2 tiles: not split
     assert pkv_native.direct_workspace_bytes(16, 32, 8, 8192) == 0  # 128 units: not split
+    # split launches of few units: sub-splits to about one unit per CU (256 without a GPU)
+    ref = lambda b, hq, s: lib.pkv_workspace_bytes(b, hq, s)
+    assert pkv_native.split_workspace_bytes(1, 32, 8, 8192, 16) == ref(1, 32, 32)   # 128 units, k 2
+    assert pkv_native.split_workspace_bytes(1, 8, 8, 8192, 4) == ref(1, 8, 32)      # 32 units, k 8
+    assert pkv_native.split_workspace_bytes(1, 32, 8, 32768, 32) == ref(1, 32, 32)  # 256 units
+    assert pkv_native.split_workspace_bytes(1, 32, 8, 1024, 16) == ref(1, 32, 16)   # 32 tiles only
+    assert pkv_native.split_workspace_bytes(8, 32, 32, 4096, 8) == ref(8, 32, 8)    # 2048 units
+    assert pkv_native.split_workspace_bytes(1, 32, 8, 8192, 1) == 0                 # direct launch
 
 
 def _call_paged(**overrides):
