@@ -65,7 +65,7 @@ void pkv_cost_model_preset(int32_t policy, pkv_cost_model* m) {
   if (policy == PKV_POLICY_MI355X) {
     m->compute_units = kMiComputeUnits;
     m->read_gbps = 8000.0 * 0.70;   // 70 % of the 8 TB/s HBM3E peak
-    m->launch_overhead_us = 4.0;
+    m->launch_overhead_us = 1.5;    // gap between dependent launches on one stream
     m->min_ctas_per_cu = 2.0;
     m->supported_group = 0;         // every G runs natively
   } else {
@@ -119,12 +119,21 @@ int32_t pkv_choose_splits(const int32_t* lengths, int32_t count, int32_t request
   const int64_t hkv = num_kv_heads > 0 ? num_kv_heads : 1;
   auto clamp4 = [&](int64_t cap) { return (int32_t)std::max<int64_t>(4, std::min(cap, t_min)); };
   if (policy == PKV_POLICY_MI355X) {
-    // One split count for the whole bucket: enough items for every CU, at least
-    // kMiMinTilesPerItem tiles per item on the shortest row.
-    const int64_t target = kMiTargetItems;
-    int64_t s = ceil_div_pos(target, hkv * batch);
-    s = std::min<int64_t>(s, std::max<int64_t>(1, t_min / kMiMinTilesPerItem));
-    return (int32_t)std::max<int64_t>(1, std::min<int64_t>(s, std::min<int64_t>(kMiMaxSplits, t_min)));
+    // One split count for the whole launch (a bucket, or a ragged grid with row-local
+    // split bounds).  Rows of one length: one unit per CU, every unit in the first round
+    // (C3 at 32k, B1 Hkv 8: 27.6 us per step with 32 splits against 32.2 us with 64 and
+    // 40 us with 48 in the serving harness).  Rows of mixed lengths: also enough splits
+    // that the longest row's unit is at most a quarter of a CU's share of the tiles, so
+    // that it does not end the launch alone (C2, B8 MHA with lengths in [1024, 8192]:
+    // 112 us per step with 8 splits against 130 us with 2).  At least 2 tiles per unit
+    // of the longest row; shorter rows may hold empty splits.
+    int64_t total = 0;
+    for (int i = 0; i < count; ++i) total += std::max<int64_t>(1, tiles_of(lengths[i]));
+    int64_t s = ceil_div_pos(kMiComputeUnits, hkv * batch);
+    if (t_max * 10 > t_min * 11)
+      s = std::max<int64_t>(s, ceil_div_pos(4 * t_max * kMiComputeUnits, hkv * total));
+    s = std::min<int64_t>(s, std::max<int64_t>(1, t_max / 2));
+    return (int32_t)std::max<int64_t>(1, std::min<int64_t>(s, kMiMaxSplits));
   }
   if (single_bucket) {
     if (batch >= 8) return clamp4(40);
@@ -172,10 +181,53 @@ int32_t pkv_model_workqueue_splits(const int32_t* lengths, int32_t count, int32_
   return best;
 }
 
+// MI355X route cost: the makespan of the launch on this engine's kernels, in place of
+// the reference's occupancy-penalty model (which charges a launch with fewer than
+// min_ctas_per_cu workgroups per CU, while one equal unit per CU is this engine's fastest
+// grid).  Each CU streams one 32-token tile of one kv head (16 KB at D = 128, 2-byte K/V)
+// in tile_us at read_gbps / compute_units.
+//   split grid (S splits per row, row-local bounds): max(share, longest unit) tiles,
+//     plus a fixed cost per round of two 8-wave workgroups per CU, plus the merge;
+//   work queue (balanced schedule: equal tile shares per wave): share tiles plus its merge.
+// Calibration (measured step times): C3 at 32k (B1 Hkv 8) grid S=32 27.6 us, queue ~31;
+// C4 queue 45 us; C2 (B8 MHA) grid S=8 112 us, queue ~115; C5 G=32 queue 67 us.
+constexpr double kMiUnitRoundUs = 1.5;   // Q load, pipeline ramp and combine per round
+constexpr double kMiGridMergeUs = 4.0;   // split-grid merge kernel
+constexpr double kMiQueueMergeUs = 7.0;  // balanced-schedule merge (recomputes the layout)
+
+double mi355x_route_us(const int32_t* lengths, int32_t count, int32_t route, int32_t splits,
+                       const pkv_cost_model* m) {
+  const int64_t hkv = m->num_kv_heads > 0 ? m->num_kv_heads : 1;
+  const int64_t cus = m->compute_units > 0 ? m->compute_units : kMiComputeUnits;
+  const double tile_bytes = (double)kTileTokens * m->head_dim * 2 * 2;
+  const double tile_us = tile_bytes / (m->read_gbps * 1e3 / (double)cus);  // GB/s = 1e3 B/us
+  int64_t total = 0, longest = 0;
+  for (int i = 0; i < count; ++i) {
+    const int64_t t = tiles_of(std::max<int32_t>(lengths[i], 0));
+    total += t * hkv;
+    longest = std::max(longest, t);
+  }
+  const double share = (double)total / (double)cus;
+  const double launches_us = 2.0 * m->launch_overhead_us;
+  if (route == PKV_ROUTE_WORKQUEUE) return share * tile_us + kMiQueueMergeUs + launches_us;
+  const int64_t s = std::max<int32_t>(1, splits);
+  const double unit = (double)ceil_div_pos(std::max<int64_t>(longest, 1), s);
+  const double units = (double)count * hkv * s;
+  const double rounds = std::ceil(units / (2.0 * cus));
+  return std::max(share, unit) * tile_us + rounds * kMiUnitRoundUs +
+         (s > 1 ? kMiGridMergeUs + launches_us : 0.5 * launches_us);
+}
+
 // estimate_route_ms, benchmark_serving_trace.py:418-442 (and useful_kv_mb_for_state :511-513).
+// The MI355X policy prices PKV_ROUTE_BUCKET (the split grid) and PKV_ROUTE_WORKQUEUE with
+// mi355x_route_us.
 double pkv_estimate_route_ms(const int32_t* lengths, int32_t count, int32_t route, int32_t splits,
                              const pkv_cost_model* m) {
   if (!m || (!lengths && count > 0)) return NAN;
+  if (m->policy == PKV_POLICY_MI355X) {
+    if (route != PKV_ROUTE_BUCKET && route != PKV_ROUTE_WORKQUEUE) return NAN;
+    return mi355x_route_us(lengths, count, route, splits, m) / 1000.0;
+  }
   int64_t sum_len = 0;
   std::set<int32_t> unique;
   for (int i = 0; i < count; ++i) {
@@ -196,10 +248,8 @@ double pkv_estimate_route_ms(const int32_t* lengths, int32_t count, int32_t rout
     merge_mb = 0.0;
   } else if (route == PKV_ROUTE_BUCKET) {
     ctas_per_cu = (double)(active * m->num_kv_heads * splits) / (double)m->compute_units;
-    // The reference launches decode + merge per exact-length bucket.  The MI355X harness
-    // runs the step as one ragged grid (row-local split bounds): decode plus a merge, or
-    // one direct launch that splits itself into the caller's workspace.
-    launch_count = m->policy == PKV_POLICY_MI355X ? 2 : 2 * (int64_t)unique.size();
+    // The reference launches decode + merge per exact-length bucket.
+    launch_count = 2 * (int64_t)unique.size();
     merge_mb = (double)merge_bytes / (1024.0 * 1024.0);
   } else if (route == PKV_ROUTE_WORKQUEUE) {
     ctas_per_cu = (double)(active * m->num_kv_heads * splits) / (double)m->compute_units;

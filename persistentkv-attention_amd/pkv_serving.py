@@ -181,14 +181,15 @@ def compile_bucket_step(w, step_index, device, requested_splits, auto_splits=Fal
 
 
 def bucket_workspace(w, steps, device):
-    """fp32 workspace for every bucket launch of ``steps`` (split partial states, or the
-    direct launch's internal split)."""
+    """fp32 workspace for every bucket launch of ``steps`` (split partial states with room
+    for a few-unit launch's sub-splits, or the direct launch's internal split)."""
     floats = 1
     for s in steps:
         for b in s.buckets:
             rows = int(b.seq_lens.numel())
             if b.launch_splits > 1:
-                floats = max(floats, rows * w.hq * b.launch_splits * (2 + HEAD_DIM))
+                floats = max(floats, pkv_native.split_workspace_bytes(
+                    rows, w.hq, w.hkv, b.bucket_length, b.launch_splits) // 4)
             else:
                 floats = max(floats, pkv_native.direct_workspace_bytes(rows, w.hq, w.hkv,
                                                                        b.bucket_length) // 4)

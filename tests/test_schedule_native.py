@@ -143,3 +143,37 @@ def test_mi355x_router_never_leaves_the_engine(golden):
             assert splits >= 1 and ms > 0
             routes.add(route)
     assert routes == {"persistentkv_bucket", "persistentkv_workqueue"}
+
+
+def test_mi355x_router_choices():
+    """The MI355X cost model's choices on the configs' shapes: equal rows run the split
+    grid with one unit per CU (B1 Hkv 8: 32 splits; the direct launch's own split count);
+    mixed lengths run the balanced work queue."""
+    m = nat.cost_model(nat.POLICY_MI355X, num_q_heads=32, num_kv_heads=8)
+    for lens in ([32768], [16384], [2048], [8192]):
+        route, splits, _ = nat.choose_adaptive_route(lens, m)
+        assert (route, splits) == ("persistentkv_bucket", 32), lens
+    route, _, _ = nat.choose_adaptive_route([20000, 300, 700, 256, 1024, 512, 600, 31000], m)
+    assert route == "persistentkv_workqueue"
+    mha = nat.cost_model(nat.POLICY_MI355X, num_q_heads=32, num_kv_heads=32)
+    assert nat.choose_adaptive_route([4096] * 8, mha)[:2] == ("persistentkv_bucket", 1)
+    for hkv in (1, 4):
+        zipf = [128 + (65536 - 128) // (i + 1) ** 2 for i in range(64)]
+        m = nat.cost_model(nat.POLICY_MI355X, num_q_heads=32, num_kv_heads=hkv)
+        assert nat.choose_adaptive_route(zipf, m)[0] == "persistentkv_workqueue"
+
+
+def test_mi355x_grid_split_rule():
+    """pkv_choose_splits (MI355X): one unit per CU for rows of one length; for mixed
+    lengths, units of the longest row at most a quarter of a CU's tile share; at least
+    two tiles per unit of the longest row."""
+    P = nat.POLICY_MI355X
+    assert nat.choose_splits([32768], 1, True, False, 8, P) == 32        # 8 x 32 = 256 units
+    assert nat.choose_splits([4096] * 8, 1, True, False, 8, P) == 4      # 8 x 8 x 4 = 256
+    assert nat.choose_splits([4096] * 8, 1, True, False, 32, P) == 1     # 256 rows x heads
+    assert nat.choose_splits([100], 1, True, False, 8, P) == 2           # 4 tiles: 2 per unit
+    lens = [1024 + 900 * i for i in range(8)]                            # C2-like, MHA
+    tiles = [(x + 31) // 32 for x in lens]
+    s = nat.choose_splits(lens, 1, True, False, 32, P)
+    assert -(-max(tiles) // s) <= 32 * sum(tiles) / 256 / 4 + 1
+    assert s == -(-4 * max(tiles) * 256 // (32 * sum(tiles)))
