@@ -111,3 +111,22 @@ def test_start_up_positions_shift_tiles_away_from_short_rows():
     assert abs(inside - among_short) <= 1
     inside, among_short = tiles_of_waves(max(KERNEL_H, 1))
     assert among_short < inside
+
+
+def test_a_merge_that_does_not_skip_empty_waves_fails_when_waves_outnumber_positions():
+    """Planted mistake: folding every group p + va .. p + vb (no empty-wave skip) reads
+    groups no piece wrote as soon as some wave holds no position (T < V), and only then."""
+    def unskipped(p, starts, tiles, total, waves, h):
+        if tiles == 0:
+            return []
+        x0 = starts[p] + h
+        va = ((x0 + 1) * waves + total - 1) // total - 1
+        vb = ((x0 + tiles) * waves + total - 1) // total - 1
+        return [p + v for v in range(va, vb + 1)]
+    for tiles, hkv, waves, fewer in (([125, 19, 254], 2, 1024, True), ([1024, 1024, 20], 8, 64, False)):
+        pairs, starts, total, pieces = decode_pieces(tiles, hkv, waves, KERNEL_H)
+        assert (total < waves) == fewer
+        mismatch = any(
+            unskipped(p, starts, tiles[pairs[p][0]], total, waves, KERNEL_H)
+            != sorted(pp + v for pp, v, _, _ in pieces if pp == p) for p in range(len(pairs)))
+        assert mismatch == fewer
