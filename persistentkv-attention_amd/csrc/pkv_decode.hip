@@ -1841,17 +1841,22 @@ int check_geometry(const Geometry& g, const void* q, const void* k, const void* 
   return PKV_OK;
 }
 
-// Waves per decode workgroup.  Eight spread each unit over more waves (shorter critical
-// path, full occupancy with fewer units); G > 16 runs one wave per SIMD and stays at four.
-// PKV_DECODE_WAVES=4|8 overrides the choice (tuning).
-int decode_waves(int hb) {
+// Waves per decode workgroup.  The grid ops (direct and split units) run four: with every
+// CU streaming, 64 KB in flight per CU already holds HBM at its ceiling, and the launch's
+// tail after its last requests is about one loaded latency, which grows with the bytes in
+// flight (probes: 1.3 us at 32 KB per CU, 5.4 us at 128 KB, the same bandwidth).  Measured
+// against eight: C2 105.4 against 107.9 us, C3 at 32k 27.6 against 27.9 us, B1 G4 32k
+// 27.6 against 28.2 us.  Work-queue items (the per-item schedule) keep eight, which spread
+// a long item over more waves (C4 per item: 52.2 against 55.4 us).  G > 16 runs one wave
+// per SIMD and stays at four.  PKV_DECODE_WAVES=4|8 overrides the choice (tuning).
+int decode_waves(int hb, int mode) {
   static const int forced = [] {
     const char* e = getenv("PKV_DECODE_WAVES");
     return e ? atoi(e) : 0;
   }();
   if (hb > 1) return 4;
   if (forced == 4 || forced == 8) return forced;
-  return 8;
+  return mode == kQueue ? 8 : 4;
 }
 
 // Compute units of the current device (cached per device).
@@ -1883,7 +1888,7 @@ bool use_async_combine(int units) {
 
 template <class Elem, int HB, int PG, int MODE>
 hipError_t launch_decode(const DecodeArgs& a, int grid, hipStream_t stream) {
-  if (HB == 1 && decode_waves(HB) == 8) {
+  if (HB == 1 && decode_waves(HB, MODE) == 8) {
     if constexpr (HB == 1 && PG != kPgGeneric && PG != kPgContig && MODE != kDirect) {
       if (use_async_combine(grid)) {
         decode_kernel<Elem, HB, PG, MODE, 8, true>
