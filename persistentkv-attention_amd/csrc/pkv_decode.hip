@@ -823,7 +823,6 @@ __device__ inline f32x2 get_f32x2(const float* p) {
   return *(const f32x2*)p;
 }
 // Waits until every memory access this wave issued has completed.
-__device__ inline void wait_memory() { __builtin_amdgcn_s_waitcnt(0); }
 
 // Neutral partial state of an empty split (cuh:340-363): m = -FLT_MAX, l = 0, acc = 0.
 __device__ inline void write_neutral(const DecodeArgs& a, long state0, long state_stride,
@@ -1009,19 +1008,25 @@ __device__ inline int expected_arrivals(const Unit& u) {
   return u.row_splits < total ? u.row_splits : total;
 }
 
-// Arrival of a unit whose partial states are written (with agent-scope stores): the last
-// unit of its (row, kv head) merges the group's G heads and clears the counter.  With
-// `nwaves` > 1 the whole workgroup calls this (it synchronises); with 1, a single wave.
+// Arrival of a unit whose partial states are written: the last unit of its (row, kv head)
+// merges the group's G heads and clears the counter.  With `nwaves` > 1 the whole
+// workgroup calls this (it synchronises); with 1, a single wave.
+//
+// Ordering, by the memory model: the workgroup's state stores happen before the barrier
+// (with one wave, its lanes issue in lock step, which the AMDGPU memory model treats as
+// ordered at wavefront scope); wave 0's lane 0 counts the arrival with an agent-scope
+// acq_rel read-modify-write, which releases those stores to every other unit of the group
+// and, for the last arrival, acquires theirs (the release sequence on the counter ties all
+// arrivals together); the second barrier passes the acquire on to the merging waves.
 template <class Elem>
 __device__ inline void arrive(const DecodeArgs& a, const Unit& u, int qh0, int lane, int wave,
                               int nwaves) {
   __shared__ int last_flag;
   int32_t* counter = a.merge_counters + (long)u.row * a.hkv + u.kvh;
-  wait_memory();  // this wave's partial-state stores have completed
   if (nwaves > 1) __syncthreads();
   int last = 0;
   if (wave == 0 && lane == 0) {
-    const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     last = old == expected_arrivals(u) - 1;
     if (nwaves > 1) last_flag = last;
   }
