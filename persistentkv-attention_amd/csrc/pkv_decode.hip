@@ -1600,12 +1600,26 @@ struct RowTable {
   long total;
 };
 
-__device__ inline long wave_incl_scan(long x, int lane) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const long y = __shfl_up(x, o);
-    if (lane >= o) x += y;
-  }
+// One DPP step of the scan: x plus the value of the lane `ctrl` selects (0 where it selects
+// none, or in the rows row_mask leaves out), on both 32-bit halves.
+template <int CTRL, int ROW_MASK>
+__device__ inline long dpp_add(long x) {
+  const uint64_t u = (uint64_t)x;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, ROW_MASK, 0xf, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, ROW_MASK, 0xf, false);
+  return x + (long)(((uint64_t)hi << 32) | lo);
+}
+
+// Inclusive prefix sum over the wave's 64 lanes with DPP (no LDS): within each row of 16
+// lanes by shifts of 1, 2, 4 and 8, then row 0's total into rows 1 and 3 (row_bcast:15)
+// and rows 0-1's into rows 2 and 3 (row_bcast:31).
+__device__ inline long wave_incl_scan(long x, int) {
+  x = dpp_add<0x111, 0xf>(x);  // row_shr:1
+  x = dpp_add<0x112, 0xf>(x);  // row_shr:2
+  x = dpp_add<0x114, 0xf>(x);  // row_shr:4
+  x = dpp_add<0x118, 0xf>(x);  // row_shr:8
+  x = dpp_add<0x142, 0xa>(x);  // row_bcast:15
+  x = dpp_add<0x143, 0xc>(x);  // row_bcast:31
   return x;
 }
 
