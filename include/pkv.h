@@ -194,7 +194,8 @@ int pkv_workqueue_schedule(int32_t batch, int32_t num_q_heads, int32_t num_kv_he
                            int32_t page_size, size_t workspace_bytes, int32_t fused_merge);
 
 /* Workspace bytes the balanced schedule needs on the current device:
- * (batch * num_kv_heads + 4 * CUs) * (num_q_heads / num_kv_heads) * 130 * 4.  A complete
+ * (batch * num_kv_heads + 4 * CUs) * (num_q_heads / num_kv_heads) * 130 * 4; 0 for sizes
+ * it never takes (G > 16 or batch > 256).  A complete
  * queue's reference-sized workspace (pkv_workqueue_workspace_bytes) often holds it already
  * (C4: 2.66 MB against 2.26 MB).  No counterpart in the reference. */
 size_t pkv_workqueue_balanced_workspace_bytes(int32_t batch, int32_t num_q_heads,

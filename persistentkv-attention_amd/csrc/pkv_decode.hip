@@ -2605,8 +2605,9 @@ int pkv_paged_attention_workqueue_stage(
 
 size_t pkv_workqueue_balanced_workspace_bytes(int32_t batch, int32_t num_q_heads,
                                               int32_t num_kv_heads) {
-  if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0)
-    return 0;
+  if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 ||
+      num_q_heads / num_kv_heads > 16 || batch > 64 * kBalRowChunks)
+    return 0;  // sizes the balanced schedule never takes
   const long waves = (long)kBalWaves * cu_count();
   return (size_t)(((long)batch * num_kv_heads + waves) * (num_q_heads / num_kv_heads)) *
          (kD + 2) * sizeof(float);

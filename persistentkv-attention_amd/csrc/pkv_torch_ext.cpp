@@ -699,6 +699,7 @@ void persistentkv_paged_attention_workqueue_stage(
 int64_t persistentkv_workqueue_schedule(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
                                         int64_t page_size, int64_t workspace_floats,
                                         bool fused_merge) {
+  TORCH_CHECK(workspace_floats >= 0, "workspace_floats must be non-negative");
   return pkv_workqueue_schedule(i32(batch, "batch"), i32(num_q_heads, "Hq"),
                                 i32(num_kv_heads, "Hkv"), i32(page_size, "page_size"),
                                 (size_t)workspace_floats * sizeof(float), fused_merge ? 1 : 0);
