@@ -301,10 +301,22 @@ def main():
                                                 m.out_indices, m.output, ws, m.bucket_length,
                                                 w.page_size, m.total_partial_slots, w.kv_fp8,
                                                 w.k_scale, w.v_scale)
+        # Launched one by one from Python, a merge of a few microseconds waits on the host's
+        # launch rate; the same launches replayed from one HIP graph time the GPU alone.
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            merge_stage(0)
+            with torch.cuda.graph(graph, stream=side):
+                for k in range(args.steps):
+                    merge_stage(k)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
         m0, m1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         m0.record()
-        for k in range(args.steps):
-            merge_stage(k)
+        graph.replay()
         m1.record()
         torch.cuda.synchronize()
         merge_us = m0.elapsed_time(m1) * 1e3 / args.steps
