@@ -1380,8 +1380,8 @@ __device__ void solo_unit(const DecodeArgs& a, const Unit& u, int q_loaded, int 
 //
 // ASYNC selects the barrier-free combine (combine_async) for multi-wave units; it pays
 // when the launch has several units per CU, whose next workgroup then starts early.
-template <class Elem, int HB, int PG, int MODE, int NW, bool ASYNC>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(HB == 1 ? 2 : 1)))
+template <class Elem, int HB, int PG, int MODE, int NW, bool ASYNC, int DEPTH = HB>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu((HB == 1 && DEPTH == 1) ? 2 : 1)))
 void decode_kernel(DecodeArgs a) {
   constexpr int kWaves = NW;
   constexpr int kThreads = NW * 64;
@@ -1463,8 +1463,8 @@ void decode_kernel(DecodeArgs a) {
   // Contiguous sub-range of the unit's tiles for this wave.
   const int w0 = uniform(u.tb + (n * wave) / kWaves);
   const int w1 = uniform(u.tb + (n * (wave + 1)) / kWaves);
-  stream_unit<Elem, HB, PG>(a, st, qf, u.row, u.kvh, w0, w1, u.len, lane, w0 == first_tile,
-                              first0, first1);
+  stream_unit<Elem, HB, PG, DEPTH>(a, st, qf, u.row, u.kvh, w0, w1, u.len, lane,
+                                   w0 == first_tile, first0, first1);
   const int out_row = MODE == kDirect ? (a.out_indices ? a.out_indices[u.row] : u.row) : 0;
   if constexpr (ASYNC) {
     if (!combine_async<Elem, HB, NW, MODE == kDirect>(a, st, lds, &arrivals, qh0, out_row, d, lane, wave))
@@ -1860,22 +1860,30 @@ int check_geometry(const Geometry& g, const void* q, const void* k, const void* 
   return PKV_OK;
 }
 
-// Waves per decode workgroup.  The grid ops (direct and split units) run four: with every
-// CU streaming, 64 KB in flight per CU already holds HBM at its ceiling, and the launch's
-// tail after its last requests is about one loaded latency, which grows with the bytes in
-// flight (probes: 1.3 us at 32 KB per CU, 5.4 us at 128 KB, the same bandwidth).  Measured
-// against eight: C2 105.4 against 107.9 us, C3 at 32k 27.6 against 27.9 us, B1 G4 32k
-// 27.6 against 28.2 us.  Work-queue items (the per-item schedule) keep eight, which spread
-// a long item over more waves (C4 per item: 52.2 against 55.4 us).  G > 16 runs one wave
-// per SIMD and stays at four.  PKV_DECODE_WAVES=4|8 overrides the choice (tuning).
-int decode_waves(int hb, int mode) {
+// Waves per decode workgroup.  With every CU streaming, 32-64 KB in flight per CU already
+// holds HBM at its ceiling, and a launch ends about one loaded latency after its last
+// requests, a latency that grows with the bytes in flight (probes: 1.3 us at 32 KB per CU,
+// 5.4 us at 128 KB, the same bandwidth).  So the grid ops (direct and split units) keep
+// little in flight:
+//   - at most one unit per CU: 2 waves with two 16 KB tiles in flight each, one workgroup
+//     per CU (C3 at 32k 27.15 against 27.5 us with 4 x 1, B1 G4 32k 26.7 against 28.1 us,
+//     C3 at 16k 17.6 against 18.3 us);
+//   - more units: 4 waves with one tile each (C2, 8 units per CU: 106.3 us, against 107.9
+//     with 8 waves and 110.5 with 2 x 2).
+// Work-queue items (the per-item schedule) keep eight, which spread a long item over more
+// waves (per-item C4: 52.2 against 55.4 us with 4).  G > 16 runs one wave per SIMD with
+// two tiles in flight and stays at four.  PKV_DECODE_WAVES=2|4|8 overrides the choice.
+int cu_count();
+
+int decode_waves(int hb, int mode, int units) {
   static const int forced = [] {
     const char* e = getenv("PKV_DECODE_WAVES");
     return e ? atoi(e) : 0;
   }();
   if (hb > 1) return 4;
-  if (forced == 4 || forced == 8) return forced;
-  return mode == kQueue ? 8 : 4;
+  if (forced == 2 || forced == 4 || forced == 8) return forced;
+  if (mode == kQueue) return 8;
+  return units <= cu_count() ? 2 : 4;
 }
 
 // Compute units of the current device (cached per device).
@@ -1907,7 +1915,16 @@ bool use_async_combine(int units) {
 
 template <class Elem, int HB, int PG, int MODE>
 hipError_t launch_decode(const DecodeArgs& a, int grid, hipStream_t stream) {
-  if (HB == 1 && decode_waves(HB, MODE) == 8) {
+  const int nw = decode_waves(HB, MODE, grid);
+  if constexpr (HB == 1) {
+    if (nw == 2) {
+      // 96 KB of LDS per workgroup keeps one workgroup, two waves, on each CU.
+      decode_kernel<Elem, 1, PG, MODE, 2, false, 2>
+          <<<dim3(grid), dim3(2 * 64), 96 * 1024, stream>>>(a);
+      return hipGetLastError();
+    }
+  }
+  if (HB == 1 && nw == 8) {
     if constexpr (HB == 1 && PG != kPgGeneric && PG != kPgContig && MODE != kDirect) {
       if (use_async_combine(grid)) {
         decode_kernel<Elem, HB, PG, MODE, 8, true>
