@@ -1357,7 +1357,7 @@ __device__ inline bool combine_async(const DecodeArgs& a, const WaveState<HB>& s
 // ---------------------------------------------------------------------------------
 constexpr int kSoloTiles = 2;
 
-template <class Elem, int HB, int PG, int MODE>
+template <class Elem, int HB, int PG, int MODE, int DEPTH = HB>
 __device__ void solo_unit(const DecodeArgs& a, const Unit& u, int q_loaded, int t0, int t1,
                           const Dest& d, int lane, bool have_first, FastPager::Pages f0,
                           FastPager::Pages f1) {
@@ -1366,7 +1366,8 @@ __device__ void solo_unit(const DecodeArgs& a, const Unit& u, int q_loaded, int 
   load_q<HB>(a, q_loaded, u.row, qh0, lane, qf);
   WaveState<HB> st;
   init_state<HB>(st);
-  stream_unit<Elem, HB, PG>(a, st, qf, u.row, u.kvh, t0, t1, u.len, lane, have_first, f0, f1);
+  stream_unit<Elem, HB, PG, DEPTH>(a, st, qf, u.row, u.kvh, t0, t1, u.len, lane, have_first, f0,
+                                   f1);
   const int out_row = MODE == kDirect ? (a.out_indices ? a.out_indices[u.row] : u.row) : 0;
   write_wave_state<Elem, HB, MODE == kDirect>(a, st, qh0, out_row, d, lane);
   if (MODE == kQueue && a.merge_counters != nullptr) arrive<Elem>(a, u, qh0, lane, 0, 1);
@@ -1446,8 +1447,8 @@ void decode_kernel(DecodeArgs a) {
   const int n = u.te - u.tb;
   if (n <= kSoloTiles) {
     if (wave == 0)
-      solo_unit<Elem, HB, PG, MODE>(a, u, q_loaded, u.tb, u.te, d, lane, u.tb == first_tile, first0,
-                                    first1);
+      solo_unit<Elem, HB, PG, MODE, DEPTH>(a, u, q_loaded, u.tb, u.te, d, lane,
+                                           u.tb == first_tile, first0, first1);
     return;
   }
 
