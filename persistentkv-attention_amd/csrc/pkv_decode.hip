@@ -790,11 +790,9 @@ __device__ inline Unit resolve_unit(const DecodeArgs& a, int idx) {
 
 // ---------------------------------------------------------------------------------
 // Partial-state stores and loads.  With the fused merge another workgroup (possibly on
-// another XCD, behind another L2) reads the states in the same launch.  They are then
-// written with agent-scope atomic stores (write-through to the coherence point) and
-// read with agent-scope atomic loads; the writer waits for its stores to complete
-// before it counts its arrival.  That replaces an agent-scope release fence, which
-// would write back the whole L2 on every arrival.
+// another XCD, behind another L2) reads the states in the same launch: they are written
+// and read with agent-scope atomic accesses, and ordered by the release/acquire of the
+// arrival counter (arrive).
 // ---------------------------------------------------------------------------------
 __device__ inline void put_f32(float* p, float v, bool coherent) {
   if (coherent) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
