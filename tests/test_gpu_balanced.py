@@ -207,3 +207,28 @@ def test_schedule_rules(ext, gpu):
     need = pkv_native.workqueue_balanced_workspace_bytes(8, 32, 8) // 4
     assert ext.workqueue_schedule(8, 32, 8, 16, need, False) == 1
     assert ext.workqueue_schedule(8, 32, 8, 16, need - 1, False) == 0
+
+
+@pytest.mark.parametrize("balanced", [False, True])
+def test_lengths_and_page_ids_outside_the_table_are_clamped(ext, gpu, balanced):
+    """The work-queue op in both schedules on inputs the reference would read out of bounds
+    with: a length past the table's capacity is clamped to max_pages * page_size, a negative
+    length counts as 0 (zeros), a page id outside the pool is clamped into it.  Expected: the
+    oracle on the same inputs with those rules applied on the host."""
+    lengths, hq, hkv = [100, 64, 40, 77], 32, 8
+    case = make_case(lengths, hq, hkv, 16, F16, seed=31)
+    meta = _meta(case, 2, hkv)
+    bt = torch.as_tensor(meta["block_table"], dtype=torch.int32)
+    pages, cols = case.k_pages.shape[0], bt.shape[1]
+    bt[1, 1], bt[1, 2] = -7, 10 ** 6
+    sl = torch.tensor([100 + 500, 64, 40, -5], dtype=torch.int32)
+    meta = dict(meta, block_table=bt.tolist(), seq_lens=sl.tolist())
+    bt_ref, sl_ref = bt.clamp(0, pages - 1), sl.clamp(0, cols * 16)
+    floats = (_balanced_floats(ext, case, meta, hkv) if balanced
+              else meta["total_partial_slots"] * hq * 130)
+    assert ext.workqueue_schedule(4, hq, hkv, 16, floats, False) == int(balanced)
+    out = _run(ext, gpu, case, meta, hkv, floats)
+    ref = oracle.paged_decode(case.q, case.k_pages, case.v_pages, bt_ref, sl_ref,
+                              meta["q_indices"], meta["out_indices"])
+    assert sl_ref.tolist() == [cols * 16, 64, 40, 0]
+    assert_parity(out, ref)
