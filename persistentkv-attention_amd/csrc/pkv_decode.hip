@@ -1639,13 +1639,17 @@ __device__ inline void row_chunk(const DecodeArgs& a, int lane, int k, int raw, 
   carry = read_lane64(incl, 63);
 }
 
-// Loads every row's length (the loads of all chunks are issued together) and builds the
-// prefix of row weights.  batch <= 64 * kBalRowChunks (checked on the host).
+// Loads every row's length and builds the prefix of row weights.  batch <= 64 *
+// kBalRowChunks (checked on the host).  The lengths are read through one buffer descriptor
+// that covers seq_lens[0, batch): the four loads go out together with no branch between
+// them, and lanes past the batch read 0 without touching memory.
 __device__ inline void row_table(const DecodeArgs& a, int lane, RowTable& t) {
-  const int raw0 = lane < a.batch ? a.seq_lens[lane] : 0;
-  const int raw1 = lane + 64 < a.batch ? a.seq_lens[lane + 64] : 0;
-  const int raw2 = lane + 128 < a.batch ? a.seq_lens[lane + 128] : 0;
-  const int raw3 = lane + 192 < a.batch ? a.seq_lens[lane + 192] : 0;
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+      uniform_ptr(a.seq_lens), (short)0, uniform(a.batch > 0 ? a.batch * 4 : 0), kRsrcWord3);
+  const int raw0 = (int)__builtin_amdgcn_raw_buffer_load_b32(r, 4 * lane, 0, 0);
+  const int raw1 = (int)__builtin_amdgcn_raw_buffer_load_b32(r, 4 * lane + 256, 0, 0);
+  const int raw2 = (int)__builtin_amdgcn_raw_buffer_load_b32(r, 4 * lane + 512, 0, 0);
+  const int raw3 = (int)__builtin_amdgcn_raw_buffer_load_b32(r, 4 * lane + 768, 0, 0);
   // Chunks past the batch hold no row: their prefix is the total.
   long carry = 0;
   row_chunk(a, lane, 0, raw0, t.len0, t.incl0, carry);
