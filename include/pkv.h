@@ -185,7 +185,7 @@ int pkv_paged_attention_workqueue_noalloc(
  * work item.  The balanced schedule streams every (row, kv head) pair's tiles with an equal
  * share per wave (4 waves per CU) and merges the pieces; it applies when fused_merge == 0,
  * G = num_q_heads / num_kv_heads <= 16, page_size is a multiple of 16, batch <= 256 and
- * the workspace holds (batch * num_kv_heads + 4 * CUs) * G partial states of 130 floats.
+ * the workspace holds pkv_workqueue_balanced_workspace_bytes.
  * It reads the work items' row set, not their tile ranges: the queue must be complete
  * (every non-empty split of every kv head of every row, as pkv_build_workqueue builds it),
  * which is the only input on which the reference's merge reads no unwritten slot.  Both
@@ -193,11 +193,13 @@ int pkv_paged_attention_workqueue_noalloc(
 int pkv_workqueue_schedule(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
                            int32_t page_size, size_t workspace_bytes, int32_t fused_merge);
 
-/* Workspace bytes the balanced schedule needs on the current device:
- * (batch * num_kv_heads + 4 * CUs) * (num_q_heads / num_kv_heads) * 130 * 4; 0 for sizes
- * it never takes (G > 16 or batch > 256).  A complete
- * queue's reference-sized workspace (pkv_workqueue_workspace_bytes) often holds it already
- * (C4: 2.66 MB against 2.26 MB).  No counterpart in the reference. */
+/* Workspace bytes the balanced schedule needs on the current device: the partial states,
+ * (batch * num_kv_heads + 4 * CUs) * (num_q_heads / num_kv_heads) * 130 * 4 bytes, then
+ * at the next 16-byte boundary a 16-byte plan entry per (row, kv head) pair (the waves that
+ * hold the pair's tiles, written by the decode stage for the merge stage); 0 for sizes it
+ * never takes (G > 16 or batch > 256).  A complete queue's reference-sized workspace
+ * (pkv_workqueue_workspace_bytes) often holds it already (C4: 2.66 MB against 2.26 MB).
+ * No counterpart in the reference. */
 size_t pkv_workqueue_balanced_workspace_bytes(int32_t batch, int32_t num_q_heads,
                                               int32_t num_kv_heads);
 

@@ -149,6 +149,9 @@ struct DecodeArgs {
   // newest token, [B, Hkv, 128] in the KV dtype, written to position seq_lens[b] - 1.
   const uint8_t* k_new;
   const uint8_t* v_new;
+  // Balanced schedule only: per (row, kv head) pair, {first wave, waves, T low, T high} of
+  // its tiles, written by the decode for the merge (16-byte entries, 16-byte aligned).
+  int32_t* bal_plan;
 };
 
 // ---------------------------------------------------------------------------------
@@ -945,8 +948,10 @@ __device__ inline void load_chunk_if(SlotChunk& c, const float* pm, const float*
 // tiles empty (split0 + s of nsplit splits over `total` tiles).
 template <bool QUEUE>
 __device__ inline bool slot_live(int s, int count, long total, int nsplit, int split0) {
-  return s < count &&
-         !(QUEUE && total * (split0 + s) / nsplit == total * (split0 + s + 1) / nsplit);
+  // With at least as many tiles as splits every split holds one (the divisions are
+  // skipped: total and nsplit are wave-uniform).
+  return s < count && !(QUEUE && total < nsplit &&
+                        total * (split0 + s) / nsplit == total * (split0 + s + 1) / nsplit);
 }
 
 // Folds slot states [c_begin, count) into acc, 32 at a time.
@@ -1726,6 +1731,15 @@ void balanced_decode_kernel(DecodeArgs a) {
     const int qh0 = kvh * G;
     u32x4 qf[1][4];
     load_q<1>(a, q_loaded, r, qh0, lane, qf);
+    if (t0 == 0) {
+      // The wave that holds the pair's first tile records the waves its tiles span (the
+      // last tile, pair0 + kBalPieceCost + tiles - 1, lies in wave ceil((x + 1) V / T) - 1)
+      // while its first loads are in flight: the merge then needs no row table.
+      const long vb = ((pair0 + kBalPieceCost + tiles) * V + T - 1) / T - 1;
+      if (lane == 0)
+        *(u32x4*)(a.bal_plan + ((long)r * a.hkv + kvh) * 4) =
+            u32x4{(uint32_t)v, (uint32_t)(vb - v + 1), (uint32_t)T, (uint32_t)(T >> 32)};
+    }
     WaveState<1> st;
     init_state<1>(st);
     stream_unit<Elem, 1, PG, 2>(a, st, qf, r, kvh, t0, t1, len, lane, true, f0, f1);
@@ -1737,9 +1751,9 @@ void balanced_decode_kernel(DecodeArgs a) {
 }
 
 // Merge of the balanced schedule: one workgroup of nw = blockDim.x / 64 waves (1, 2 or
-// kBalMergeWaves) per (row, query head) folds the groups of its pair (the recomputed
-// layout of balanced_decode_kernel over `waves` waves): wave w folds the w-th of nw equal
-// shares of the groups, and the partial merges are combined through LDS.  A few long
+// kBalMergeWaves) per (row, query head) folds the groups of its pair (the decode's waves
+// va .. va + count - 1 of `waves`, from the pair's plan entry): wave w folds the w-th of nw
+// equal shares of the groups, and the partial merges are combined through LDS.  A few long
 // pairs (~70 groups each at 8 rows) take 4 waves each; many short rows take one wave
 // each, so that the whole grid is resident at once (the kernel needs ~165 VGPRs).
 constexpr int kBalMergeWaves = 4;
@@ -1755,22 +1769,23 @@ __global__ __launch_bounds__(kBalMergeWaves * 64) void balanced_merge_kernel(Dec
   if (wg >= a.batch * a.hq) return;  // whole workgroup
   const int row = uniform(wg / a.hq);
   const int qh = uniform(wg - row * a.hq);
+  const int kvh = uniform(qh / a.group), h = qh - kvh * a.group;
+  // One round trip: the output row, the row's length and the pair's plan entry (written by
+  // the decode's wave that holds the pair's first tile) are loaded together.
   const int out_row_loaded = load_vector_deferred(a.out_indices ? a.out_indices + row : nullptr);
-  RowTable t;
-  row_table(a, lane, t);
-  const int kvh = qh / a.group, h = qh - kvh * a.group;
-  const long tiles = ceil_tiles(table_len(t, row));
-  const long T = t.total;
-  int count = 0, va = 0;
-  long base = 0;
-  if (tiles > 0) {
-    const long span = tiles + kBalPieceCost;
-    const long x0 = table_incl(t, row) - span * a.hkv + kvh * span + kBalPieceCost;  // first tile
-    va = (int)(((x0 + 1) * waves + T - 1) / T - 1);                      // wave of x0
-    const int vb = (int)(((x0 + tiles) * waves + T - 1) / T - 1);         // wave of the last
-    count = vb - va + 1;
-    base = ((long)row * a.hkv + kvh + va) * a.group + h;
-  }
+  const int len_loaded = load_vector_deferred(a.seq_lens + row);
+  const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+      uniform_ptr(a.bal_plan + ((long)row * a.hkv + kvh) * 4), (short)0, 16, kRsrcWord3);
+  const u32x4 plan = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, 0, 0, 0));
+  // Selected, not branched on, so that the plan load is issued beside the length load.
+  // Clamped so that the state loads stay inside the workspace whatever it holds.
+  int va = uniform((int)plan[0]);
+  va = va < 0 ? 0 : (va >= waves ? waves - 1 : va);
+  int count = uniform((int)plan[1]);
+  count = count < 0 ? 0 : (count > waves - va ? waves - va : count);
+  const long T = (long)(((uint64_t)(uint32_t)uniform((int)plan[3]) << 32) | (uint32_t)uniform((int)plan[2]));
+  if (ceil_tiles(clamp_length(a, uniform(len_loaded))) == 0) count = 0;  // no plan entry
+  const long base = ((long)row * a.hkv + kvh + va) * a.group + h;
   // This wave's share of the groups [c0, c1).
   const int c0 = count * wave / nw, c1 = count * (wave + 1) / nw;
   LseAcc acc;
@@ -2334,8 +2349,18 @@ int run_indexed(const Geometry& g, const void* q_source, int32_t q_rows, const v
 // Waves of the balanced schedule for a work-queue call (kBalWaves per CU), or 0 when the
 // call takes the per-item schedule: with the fused merge, with G > 16 (the two-head-block
 // kernel), with page sizes that are not multiples of 16, with more than 256 rows, or when
-// the workspace cannot hold (batch * Hkv + waves) * G partial states.  PKV_BALANCED=0
+// the workspace cannot hold (batch * Hkv + waves) * G partial states and the plan.  PKV_BALANCED=0
 // keeps every call on the per-item schedule (tuning).
+// Layout of the balanced schedule's workspace: (pairs + waves) * G partial states (m, l,
+// acc), then at the next 16-byte boundary one 16-byte plan entry per (row, kv head) pair.
+size_t balanced_plan_offset(long pairs, long waves, int G) {
+  const size_t states = (size_t)((pairs + waves) * G) * (kD + 2) * sizeof(float);
+  return (states + 15) & ~(size_t)15;
+}
+size_t balanced_bytes(long pairs, long waves, int G) {
+  return balanced_plan_offset(pairs, waves, G) + (size_t)pairs * 16;
+}
+
 int balanced_waves(const Geometry& g, size_t ws_bytes, int fused_merge) {
   static const bool on = [] {
     const char* e = getenv("PKV_BALANCED");
@@ -2345,8 +2370,7 @@ int balanced_waves(const Geometry& g, size_t ws_bytes, int fused_merge) {
   const int G = g.hq / g.hkv;
   if (G > 16 || g.page_size % 16 != 0 || g.batch > 64 * kBalRowChunks) return 0;
   const long waves = (long)kBalWaves * cu_count();
-  const long states = (long)(ws_bytes / ((kD + 2) * sizeof(float)));
-  if (((long)g.batch * g.hkv + waves) * G > states) return 0;
+  if (balanced_bytes((long)g.batch * g.hkv, waves, G) > ws_bytes) return 0;
   return (int)waves;
 }
 
@@ -2371,10 +2395,12 @@ int run_workqueue(const QueueCall& c, int32_t fused_merge, hipStream_t stream, c
     if (st != PKV_OK) return st;
   }
   if (waves > 0) {
-    const long states = ((long)c.g.batch * c.g.hkv + waves) * a.group;
+    const long pairs = (long)c.g.batch * c.g.hkv;
+    const long states = (pairs + waves) * a.group;
     a.part_m = (float*)c.ws;
     a.part_l = a.part_m + states;
     a.part_acc = a.part_l + states;
+    a.bal_plan = (int32_t*)((uint8_t*)c.ws + balanced_plan_offset(pairs, waves, a.group));
     hipError_t e = hipSuccess;
     if (stages & 1) {
       // 96 KB of LDS per workgroup keeps one workgroup on each CU.
@@ -2629,8 +2655,7 @@ size_t pkv_workqueue_balanced_workspace_bytes(int32_t batch, int32_t num_q_heads
       num_q_heads / num_kv_heads > 16 || batch > 64 * kBalRowChunks)
     return 0;  // sizes the balanced schedule never takes
   const long waves = (long)kBalWaves * cu_count();
-  return (size_t)(((long)batch * num_kv_heads + waves) * (num_q_heads / num_kv_heads)) *
-         (kD + 2) * sizeof(float);
+  return balanced_bytes((long)batch * num_kv_heads, waves, num_q_heads / num_kv_heads);
 }
 
 int pkv_workqueue_schedule(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,

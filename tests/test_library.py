@@ -77,7 +77,9 @@ def test_workspace_sizes():
     assert pkv_native.split_workspace_bytes(8, 32, 32, 4096, 8) == ref(8, 32, 8)    # 2048 units
     assert pkv_native.split_workspace_bytes(1, 32, 8, 8192, 1) == 0                 # direct launch
     # the balanced work-queue schedule: (B*Hkv + 4 waves x CUs) groups of G states
-    assert pkv_native.workqueue_balanced_workspace_bytes(8, 32, 8) == (8 * 8 + 4 * 256) * 4 * 130 * 4
+    # states of (pairs + waves) * G heads, then one 16-byte plan entry per pair
+    assert pkv_native.workqueue_balanced_workspace_bytes(8, 32, 8) == (8 * 8 + 4 * 256) * 4 * 130 * 4 + 8 * 8 * 16
+    assert pkv_native.workqueue_balanced_workspace_bytes(3, 3, 1) == -(-(3 + 4 * 256) * 3 * 520 // 16) * 16 + 3 * 16
     assert pkv_native.workqueue_balanced_workspace_bytes(8, 32, 1) == 0    # G = 32: never taken
     assert pkv_native.workqueue_balanced_workspace_bytes(257, 32, 8) == 0  # more than 256 rows
 
