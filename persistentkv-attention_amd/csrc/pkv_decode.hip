@@ -847,15 +847,35 @@ __device__ inline void store_out4(uint8_t* out, long elem, f32x4 v) {
   *(u32x2*)(out + elem * 2) = w;
 }
 
+// Reductions over the wave's 64 lanes with DPP (no LDS): within quads (quad_perm), half
+// rows and rows (mirrors), then row 0 into row 1 and row 2 into row 3 (row_bcast:15, rows
+// 1 and 3 only) and rows 0-1 into rows 2-3 (row_bcast:31, rows 2 and 3 only).  Lane 63
+// then holds the result, which is returned to every lane as a scalar.  Rows left out by a
+// row mask keep `ident`.
+template <int CTRL, int ROW_MASK>
+__device__ inline float dpp_f32(float ident, float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, ident),
+                                                               __builtin_bit_cast(int, x), CTRL,
+                                                               ROW_MASK, 0xf, false));
+}
 __device__ inline float wave_max(float x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-  return x;
+  constexpr float id = -FLT_MAX;
+  x = fmaxf(x, dpp_f32<0xb1, 0xf>(id, x));   // quad_perm:[1,0,3,2]
+  x = fmaxf(x, dpp_f32<0x4e, 0xf>(id, x));   // quad_perm:[2,3,0,1]
+  x = fmaxf(x, dpp_f32<0x141, 0xf>(id, x));  // row_half_mirror
+  x = fmaxf(x, dpp_f32<0x140, 0xf>(id, x));  // row_mirror
+  x = fmaxf(x, dpp_f32<0x142, 0xa>(id, x));  // row_bcast:15
+  x = fmaxf(x, dpp_f32<0x143, 0xc>(id, x));  // row_bcast:31
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
 }
 __device__ inline float wave_sum(float x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
-  return x;
+  x += dpp_f32<0xb1, 0xf>(0.f, x);
+  x += dpp_f32<0x4e, 0xf>(0.f, x);
+  x += dpp_f32<0x141, 0xf>(0.f, x);
+  x += dpp_f32<0x140, 0xf>(0.f, x);
+  x += dpp_f32<0x142, 0xa>(0.f, x);
+  x += dpp_f32<0x143, 0xc>(0.f, x);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
 }
 
 // ---------------------------------------------------------------------------------
