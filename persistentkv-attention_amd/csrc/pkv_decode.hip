@@ -1795,7 +1795,8 @@ __global__ __launch_bounds__(kBalMergeWaves * 64) void balanced_merge_kernel(Dec
   const int out_row_loaded = load_vector_deferred(a.out_indices ? a.out_indices + row : nullptr);
   const int len_loaded = load_vector_deferred(a.seq_lens + row);
   const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
-      uniform_ptr(a.bal_plan + ((long)row * a.hkv + kvh) * 4), (short)0, 16, kRsrcWord3);
+      uniform_ptr(a.bal_plan + ((long)row * a.hkv + kvh) * 4), (short)0, a.bal_plan ? 16 : 0,
+      kRsrcWord3);  // a null plan reads zeros
   const u32x4 plan = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, 0, 0, 0));
   // Selected, not branched on, so that the plan load is issued beside the length load.
   // Clamped so that the state loads stay inside the workspace whatever it holds.
