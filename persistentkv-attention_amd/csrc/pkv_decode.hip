@@ -902,7 +902,7 @@ struct LseAcc {
     const float corr = __builtin_amdgcn_exp2f((M - m_new) * kLog2e);
     M = m_new;
     const float w = ok ? __builtin_amdgcn_exp2f((ms - M) * kLog2e) : 0.f;
-    L = L * corr + wave_sum(w * ls);
+    L = L * corr + wave_sum(ok ? w * ls : 0.f);  // select: skipped slots may hold NaN
     A *= corr;
 #pragma unroll
     for (int j = 0; j < kMergeChunk; ++j) {
@@ -1007,6 +1007,60 @@ __device__ inline void fold_slots_pipelined(LseAcc& acc, const float* pm, const 
              cur.v);
     cur = nxt;
   }
+}
+
+// Wide fold of up to kWideStates states of one query head by one wave, every load in
+// flight at once (one memory round trip; a wave tracks at most 63 vector loads, so the
+// 8-byte loads of fold_slots fit 32 states per round trip).  Lanes 0-31 load the even
+// states and lanes 32-63 the odd ones with 16-byte loads (4 dims per lane): 2 states per
+// load.  Lane j holds (m, l) of states j and j + 64.  Each half accumulates its states;
+// the halves are added and the result is returned in the LseAcc layout (lane owns dims
+// 2 lane, 2 lane + 1).  States are base + s * stride, s < n (wave-uniform, 1 <= n <=
+// kWideStates); in queue mode, slots of empty splits are skipped as in fold_slots.
+constexpr int kWideLoads = 56;
+constexpr int kWideStates = 2 * kWideLoads;
+
+__device__ inline void fold_wide(LseAcc& acc, const float* pm, const float* pl, const float* pacc,
+                                 long base, long stride, int n, long total, int nsplit,
+                                 int split0, int lane) {
+  n = uniform(n);
+  const int half = lane >> 5, q = lane & 31;
+  const int s0 = lane < n ? lane : n - 1, s1 = lane + 64 < n ? lane + 64 : n - 1;
+  const float m0 = pm[base + (long)s0 * stride], l0 = pl[base + (long)s0 * stride];
+  const float m1 = pm[base + (long)s1 * stride], l1 = pl[base + (long)s1 * stride];
+  f32x4 v[kWideLoads];
+#pragma unroll
+  for (int i = 0; i < kWideLoads; ++i) {
+    const int st = 2 * i + half < n ? 2 * i + half : n - 1;
+    v[i] = 2 * i < n ? *(const f32x4*)(pacc + (base + (long)st * stride) * kD + 4 * q)
+                     : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  const bool ok0 = lane < n && slot_live<true>(lane, n, total, nsplit, split0);
+  const bool ok1 = lane + 64 < n && slot_live<true>(lane + 64, n, total, nsplit, split0);
+  const float M = wave_max(fmaxf(ok0 ? m0 : -FLT_MAX, ok1 ? m1 : -FLT_MAX));
+  const float w0 = ok0 ? __builtin_amdgcn_exp2f((m0 - M) * kLog2e) : 0.f;
+  const float w1 = ok1 ? __builtin_amdgcn_exp2f((m1 - M) * kLog2e) : 0.f;
+  const float L = wave_sum((ok0 ? w0 * l0 : 0.f) + (ok1 ? w1 * l1 : 0.f));  // skipped slots may hold NaN
+  f32x4 A = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < kWideLoads; ++i) {
+    if (2 * i >= n) break;
+    const float src_e = 2 * i < 64 ? w0 : w1, src_o = 2 * i + 1 < 64 ? w0 : w1;
+    const float we = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, src_e), (2 * i) & 63));
+    const float wo = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, src_o), (2 * i + 1) & 63));
+    const float w = half ? wo : we;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) A[k] += w != 0.f ? w * v[i][k] : 0.f;  // select: unused slots may hold NaN
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) A[k] += __shfl_xor(A[k], 32);
+  // Lane j's dims 2j, 2j + 1 sit in lane j / 2 (components 0-1 or 2-3).
+  const int src = (lane >> 1) & 31;
+  const float x0 = __shfl(A[0], src), x1 = __shfl(A[1], src);
+  const float x2 = __shfl(A[2], src), x3 = __shfl(A[3], src);
+  acc.M = M;
+  acc.L = L;
+  acc.A = (lane & 1) ? f32x2{x2, x3} : f32x2{x0, x1};
 }
 
 // Fused merge of query head qh of a work-queue row by one wave, run by the last work item
@@ -1775,10 +1829,11 @@ void balanced_decode_kernel(DecodeArgs a) {
 // va .. va + count - 1 of `waves`, from the pair's plan entry): wave w folds the w-th of nw
 // equal shares of the groups, and the partial merges are combined through LDS.  A few long
 // pairs (~70 groups each at 8 rows) take 4 waves each; many short rows take one wave
-// each, so that the whole grid is resident at once (the kernel needs ~165 VGPRs).
+// each, so that the whole grid is resident at once (the kernel needs ~165 VGPRs, ~250 with
+// the wide fold).
 constexpr int kBalMergeWaves = 4;
 
-template <class Elem>
+template <class Elem, bool WIDE>
 __global__ __launch_bounds__(kBalMergeWaves * 64) void balanced_merge_kernel(DecodeArgs a, int waves) {
   __shared__ float sm_ml[kBalMergeWaves][2];
   __shared__ f32x2 sm_a[kBalMergeWaves][64];
@@ -1810,9 +1865,14 @@ __global__ __launch_bounds__(kBalMergeWaves * 64) void balanced_merge_kernel(Dec
   // This wave's share of the groups [c0, c1).
   const int c0 = count * wave / nw, c1 = count * (wave + 1) / nw;
   LseAcc acc;
-  // Groups of waves with no position are skipped, as the empty splits of a queue are.
-  fold_slots_pipelined<true>(acc, a.part_m, a.part_l, a.part_acc, base + (long)c0 * a.group,
-                             a.group, c1 - c0, T, waves, va + c0, lane);
+  // Groups of waves with no position are skipped, as the empty splits of a queue are.  A
+  // share of more than one chunk is folded in one round trip when it fits.
+  if (WIDE && c1 - c0 > kMergeChunk && c1 - c0 <= kWideStates)
+    fold_wide(acc, a.part_m, a.part_l, a.part_acc, base + (long)c0 * a.group, a.group, c1 - c0, T,
+              waves, va + c0, lane);
+  else
+    fold_slots_pipelined<true>(acc, a.part_m, a.part_l, a.part_acc, base + (long)c0 * a.group,
+                               a.group, c1 - c0, T, waves, va + c0, lane);
   float M = acc.M, L = acc.L;
   f32x2 A = acc.A;
   if (nw > 1) {
@@ -2447,8 +2507,17 @@ int run_workqueue(const QueueCall& c, int32_t fused_merge, hipStream_t stream, c
       int merge_waves = kBalMergeWaves;
       while (merge_waves > 1 && (long)grid * merge_waves > 8L * cu_count()) merge_waves >>= 1;
       const int block = merge_waves * 64;
-      if (c.g.dtype == PKV_DTYPE_BF16) balanced_merge_kernel<BFloat><<<grid, block, 0, stream>>>(a, waves);
-      else balanced_merge_kernel<Half><<<grid, block, 0, stream>>>(a, waves);
+      // The wide fold (one round trip for up to kWideStates groups, ~250 VGPRs) where a
+      // merge wave's share can exceed one chunk: few pairs per merge wave.
+      const bool wide = (long)c.g.batch * c.g.hkv * merge_waves * kMergeChunk < waves;
+      const bool bf = c.g.dtype == PKV_DTYPE_BF16;
+      if (wide) {
+        if (bf) balanced_merge_kernel<BFloat, true><<<grid, block, 0, stream>>>(a, waves);
+        else balanced_merge_kernel<Half, true><<<grid, block, 0, stream>>>(a, waves);
+      } else {
+        if (bf) balanced_merge_kernel<BFloat, false><<<grid, block, 0, stream>>>(a, waves);
+        else balanced_merge_kernel<Half, false><<<grid, block, 0, stream>>>(a, waves);
+      }
       e = hipGetLastError();
       if (e != hipSuccess) return fail(PKV_ERR_LAUNCH, "merge launch failed: %s", hipGetErrorString(e));
     }

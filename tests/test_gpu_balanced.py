@@ -26,13 +26,15 @@ def _dev_meta(meta, gpu):
                                     "q_indices", "out_indices")}
 
 
-def _run(ext, gpu, case, meta, hkv, floats, k=None, v=None, out_rows=None, kv=None):
+def _run(ext, gpu, case, meta, hkv, floats, k=None, v=None, out_rows=None, kv=None, ws_fill=None):
     """The combined op with a workspace of ``floats`` fp32 elements."""
     d = _dev_meta(meta, gpu)
     hq = case.q.shape[1]
     b = len(meta["seq_lens"])
     out = torch.full((out_rows or b, hq, 128), float("nan"), dtype=case.q.dtype, device=gpu)
     ws = torch.empty(floats, dtype=torch.float32, device=gpu)
+    if ws_fill is not None:
+        ws.fill_(ws_fill)
     counters = torch.zeros(b, hkv, dtype=torch.int32, device=gpu)
     k = case.k_pages.to(gpu) if k is None else k
     v = case.v_pages.to(gpu) if v is None else v
@@ -68,6 +70,8 @@ CASES = [
     ([25000 if i % 8 == 0 else 200 + 97 * i for i in range(24)], 32, 8, 16, 3, BF16),
     # 72 rows x 32 heads: one merge wave, two long rows with more than 32 groups per pair
     ([30000 if i % 36 == 0 else 100 + 7 * i for i in range(72)], 32, 8, 16, 2, F16),
+    # 2 rows x 2 kv heads: pairs over hundreds of waves, folded by the wide merge
+    ([30000, 9000], 16, 2, 16, 5, BF16),
 ]
 
 
@@ -82,6 +86,21 @@ def test_balanced_schedule_matches_oracle(ext, gpu, lengths, hq, hkv, ps, splits
     assert_parity(out, ref)
     again = _run(ext, gpu, case, meta, hkv, _balanced_floats(ext, case, meta, hkv))
     assert torch.equal(out, again)  # the schedule depends on the sizes only
+
+
+@pytest.mark.parametrize("lengths,hq,hkv", [([40, 70], 32, 8), ([1, 33, 2], 32, 4), ([90], 16, 2)])
+def test_balanced_few_positions_ignore_workspace_contents(ext, gpu, lengths, hq, hkv):
+    """With fewer positions than waves (T < V) most waves hold none, and the groups of a
+    pair's range that such waves would own are never written: the merge skips them
+    whatever they hold (NaN, infinities)."""
+    case = make_case(lengths, hq, hkv, 16, F16, seed=5)
+    meta = _meta(case, 4, hkv, list(range(len(lengths))))
+    ref = oracle.paged_decode(case.q, case.k_pages, case.v_pages, meta["block_table"],
+                              meta["seq_lens"], meta["q_indices"], meta["out_indices"])
+    floats = _balanced_floats(ext, case, meta, hkv)
+    assert ext.workqueue_schedule(len(lengths), hq, hkv, 16, floats, False) == 1
+    for fill in (float("nan"), float("inf"), -float("inf")):
+        assert_parity(_run(ext, gpu, case, meta, hkv, floats, ws_fill=fill), ref)
 
 
 def test_balanced_equals_per_item_schedule(ext, gpu):

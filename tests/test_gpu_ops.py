@@ -124,11 +124,13 @@ def _queue(case, requested, auto, hkv, policy=pkv_native.POLICY_REFERENCE, reque
                                       requested, auto, hkv, policy)
 
 
-def _run_queue(ext, gpu, case, meta, hq, hkv, fused, out_rows=None):
+def _run_queue(ext, gpu, case, meta, hq, hkv, fused, out_rows=None, ws_fill=None):
     t = lambda a: torch.as_tensor(a, dtype=torch.int32, device=gpu)
     b = len(meta["seq_lens"])
     out = torch.full((out_rows or b, hq, 128), float("nan"), dtype=case.q.dtype, device=gpu)
     ws = torch.empty(meta["total_partial_slots"] * hq * 130, dtype=torch.float32, device=gpu)
+    if ws_fill is not None:
+        ws.fill_(ws_fill)
     counters = torch.zeros(b, hkv, dtype=torch.int32, device=gpu)
     ext.paged_attention_workqueue(
         case.q.to(gpu), case.k_pages.to(gpu), case.v_pages.to(gpu), t(meta["block_table"]),
@@ -195,6 +197,19 @@ def test_paged_attention_workqueue(ext, gpu, lengths, hq, hkv, ps, req, auto, dt
     assert int(counters.abs().sum()) == 0  # the fused merge leaves the counters at zero
 
 
+@pytest.mark.parametrize("lengths,req", [([64, 33, 1], 20), ([300, 17000, 700, 256], 20)])
+def test_workqueue_empty_split_slots_ignore_workspace_contents(ext, gpu, lengths, req):
+    """Slots of splits the builder leaves empty are never written; the merge skips them
+    whatever they hold (here NaN and infinities), in the max, the sum and the output."""
+    case = make_case(lengths, 32, 8, 16, F16, seed=77)
+    meta = _queue(case, req, False, 8)
+    ref = oracle.paged_decode(case.q, case.k_pages, case.v_pages, meta["block_table"],
+                              meta["seq_lens"], meta["q_indices"], meta["out_indices"])
+    for fill in (float("nan"), float("inf"), -float("inf")):
+        out, _ = _run_queue(ext, gpu, case, meta, 32, 8, False, ws_fill=fill)
+        assert_parity(out, ref)
+
+
 def _with_row_splits(case, meta, row_splits, hkv):
     """Work items and split_offsets for per-row split counts (the builder's emission
     order: row, then split, then kv head; empty splits counted in split_offsets)."""
@@ -226,10 +241,14 @@ ROW_SPLITS = [
 @pytest.mark.parametrize("lengths,row_splits", ROW_SPLITS)
 def test_workqueue_per_row_split_counts(ext, gpu, lengths, row_splits):
     """Merges of rows whose split counts differ, including totals that make the merge's
-    fixed-split guess of the slot range look possible but wrong."""
-    case = make_case(lengths, 32, 8, 16, F16, seed=sum(row_splits), q_rows=len(lengths) + 1)
+    fixed-split guess of the slot range look possible but wrong.  Page 8 keeps both calls
+    on the per-item schedule (the balanced one needs pages of a multiple of 16), so that
+    the per-item merge kernel and the fused merge fold the same states."""
+    case = make_case(lengths, 32, 8, 8, F16, seed=sum(row_splits), q_rows=len(lengths) + 1)
     ids = [len(lengths) - i for i in range(len(lengths))]
     meta = _with_row_splits(case, _queue(case, 1, False, 8, request_ids=ids), row_splits, 8)
+    floats = meta["total_partial_slots"] * 32 * 130
+    assert ext.workqueue_schedule(len(lengths), 32, 8, 8, floats, False) == 0
     unfused, _ = _run_queue(ext, gpu, case, meta, 32, 8, False)
     fused, counters = _run_queue(ext, gpu, case, meta, 32, 8, True)
     ref = oracle.paged_decode(case.q, case.k_pages, case.v_pages, meta["block_table"],
@@ -250,10 +269,15 @@ def test_workqueue_mi355x_policy(ext, gpu):
 
 
 def test_workqueue_stages_equal_combined(ext, gpu):
+    """The reference's two stages (workqueue_decode, workqueue_merge: one workgroup per item,
+    the reference's partial-state layout) equal the combined op with the fused merge (the
+    same schedule) bit for bit, and the combined op without it bit for bit when it runs
+    the per-item schedule, to fp32 rounding when it runs the balanced one."""
     lengths = [3000, 200, 9000]
     case = make_case(lengths, 32, 8, 16, F16, seed=5)
     meta = _queue(case, 20, False, 8)
     combined, _ = _run_queue(ext, gpu, case, meta, 32, 8, False)
+    per_item, _ = _run_queue(ext, gpu, case, meta, 32, 8, True)
     t = lambda a: torch.as_tensor(a, dtype=torch.int32, device=gpu)
     staged = torch.full_like(combined, float("nan"))
     ws = torch.empty(meta["total_partial_slots"] * 32 * 130, dtype=torch.float32, device=gpu)
@@ -264,7 +288,11 @@ def test_workqueue_stages_equal_combined(ext, gpu):
     ext.workqueue_merge(t(meta["seq_lens"]), t(meta["split_offsets"]), t(meta["out_indices"]),
                         staged, ws, meta["total_partial_slots"])
     torch.cuda.synchronize()
-    assert torch.equal(staged, combined)
+    assert torch.equal(staged, per_item)
+    if ext.workqueue_schedule(len(lengths), 32, 8, 16, ws.numel(), False) == 0:
+        assert torch.equal(staged, combined)
+    else:
+        assert (staged.float() - combined.float()).abs().max().item() < 1e-3
 
 
 def test_workqueue_matches_indexed_split_grid(ext, gpu):
