@@ -25,7 +25,8 @@
  *   split_offsets  [batch + 1]                                int32 prefix sum of row splits
  *   merge_counters [batch, num_kv_heads]                      int32, zero on entry and exit
  *   workspace      fp32 [m: n][l: n][acc: n x 128] with n = batch*num_q_heads*num_splits
- *                  (grid split) or total_partial_slots*num_q_heads (work queue).
+ *                  (grid split) or total_partial_slots*num_q_heads (work queue),
+ *                  16-byte aligned (as any torch allocation is; others are rejected).
  *
  * Query head h reads KV head h / G with G = num_q_heads / num_kv_heads.  The softmax
  * scale is fixed at 1/sqrt(128).  G may be any integer in [1, 32]; the reference accepts

@@ -2164,6 +2164,15 @@ struct GridPlan {
   void* ws;
 };
 
+// The partial states are written and read with 8- and 16-byte vector accesses (and the
+// balanced schedule's plan entries with 16-byte ones at 16-byte offsets), so a workspace
+// must be 16-byte aligned, as every torch allocation is.
+int check_workspace_alignment(const void* ws) {
+  if (ws && ((uintptr_t)ws & 15))
+    return fail(PKV_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+  return PKV_OK;
+}
+
 // Chooses the launches of a grid op and checks the workspace, before anything is launched
 // (cuh:929-974 persistentkv_launch).  `internal_split` lets a launch of few units split
 // itself further into the caller's workspace when it is large enough: a direct launch
@@ -2172,6 +2181,8 @@ int plan_grid(const Geometry& g, const DecodeArgs& a, void* ws, size_t ws_bytes,
               bool internal_split, GridPlan& plan) {
   plan.splits = num_splits;
   plan.ws = ws;
+  const int st = check_workspace_alignment(ws);
+  if (st != PKV_OK) return st;
   if (num_splits == 1) {
     plan.splits = internal_split && ws ? direct_splits(g, a.context, ws_bytes) : 1;
     return PKV_OK;
@@ -2375,7 +2386,7 @@ int check_queue(const QueueCall& c, bool need_out) {
   if (!c.ws || c.ws_bytes < need)
     return fail(PKV_ERR_WORKSPACE_TOO_SMALL, "work-queue dispatch requires a workspace of %zu bytes (got %zu)",
                 need, c.ws ? c.ws_bytes : (size_t)0);
-  return PKV_OK;
+  return check_workspace_alignment(c.ws);
 }
 
 DecodeArgs queue_args(const QueueCall& c) {
@@ -2924,6 +2935,7 @@ int pkv_workqueue_merge(const int32_t* seq_lens, const int32_t* split_offsets,
   const size_t need = pkv_workqueue_workspace_bytes(total_partial_slots, num_q_heads);
   if (!workspace || workspace_bytes < need)
     return fail(PKV_ERR_WORKSPACE_TOO_SMALL, "merge requires a workspace of %zu bytes", need);
+  if (check_workspace_alignment(workspace) != PKV_OK) return PKV_ERR_INVALID_ARGUMENT;
   if (batch == 0) return ok();
   const long states = (long)total_partial_slots * num_q_heads;
   MergeArgs m = {};

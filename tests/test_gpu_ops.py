@@ -490,6 +490,36 @@ def test_validation_errors(ext, gpu):
         ext.attention_query_head_baseline(q, kc, kc[:, :, :32].contiguous(), out)
 
 
+def test_misaligned_workspace_is_rejected_before_launch(ext, gpu):
+    """Partial states are accessed with 16-byte vector loads and stores: a workspace that
+    is not 16-byte aligned (here a float32 tensor offset by one element) is rejected on the
+    host, and nothing is launched (the output keeps its sentinel)."""
+    lengths = [700, 40]
+    case = make_case(lengths, 32, 8, 16, F16, seed=3)
+    q, k, v, bt, sl = _dev(case, gpu)
+    meta = _queue(case, 4, False, 8)
+    t = lambda a: torch.as_tensor(a, dtype=torch.int32, device=gpu)
+    floats = max(meta["total_partial_slots"], 2 * 64) * 32 * 130
+    ws = torch.empty(floats + 4, dtype=torch.float32, device=gpu)[1:]
+    assert ws.data_ptr() % 16 == 4
+    out = torch.full((2, 32, 128), float("nan"), dtype=F16, device=gpu)
+    counters = torch.zeros(2, 8, dtype=torch.int32, device=gpu)
+    with pytest.raises(RuntimeError, match="16-byte aligned"):
+        ext.paged_attention_masked(q, k, v, bt, sl, out, ws, 704, 16, 4)
+    with pytest.raises(RuntimeError, match="16-byte aligned"):
+        ext.paged_attention(q[:1].contiguous(), k, v, bt[:1].contiguous(), out[:1], ws, 704, 16, 1)
+    with pytest.raises(RuntimeError, match="16-byte aligned"):
+        ext.paged_attention_workqueue(q, k, v, t(meta["block_table"]), t(meta["seq_lens"]),
+                                      t(meta["work_items"]), t(meta["split_offsets"]), counters,
+                                      t(meta["q_indices"]), t(meta["out_indices"]), out, ws,
+                                      meta["bucket_length"], 16, meta["total_partial_slots"], False)
+    with pytest.raises(RuntimeError, match="16-byte aligned"):
+        ext.workqueue_merge(t(meta["seq_lens"]), t(meta["split_offsets"]), t(meta["out_indices"]),
+                            out, ws, meta["total_partial_slots"])
+    torch.cuda.synchronize()
+    assert torch.isnan(out.float()).all()
+
+
 @pytest.mark.parametrize("op", ["masked", "indexed"])
 def test_lengths_and_page_ids_outside_the_table_are_clamped(ext, gpu, op):
     """Inputs the reference would read out of bounds with: a length past the table's
