@@ -1458,6 +1458,21 @@ __device__ void solo_unit(const DecodeArgs& a, const Unit& u, int q_loaded, int 
 //
 // ASYNC selects the barrier-free combine (combine_async) for multi-wave units; it pays
 // when the launch has several units per CU, whose next workgroup then starts early.
+// With the fused merge, the last work item of a (row, kv head) to finish writes that part
+// of the row's output, and a row without tokens has no work items (as the builder emits
+// them): its output, 0 by the merges' L == 0 rule, is written here instead, rows strided
+// over the grid.  No work item writes such a row, so nothing races with these stores.
+template <class Elem>
+__device__ inline void zero_empty_rows(const DecodeArgs& a, int tid, int threads) {
+  for (int r = blockIdx.x; r < a.batch; r += gridDim.x) {
+    if (row_length(a, r) > 0) continue;
+    const int out_row = a.out_indices ? a.out_indices[r] : r;
+    if (out_row < 0 || out_row >= a.out_rows) continue;
+    uint32_t* o = (uint32_t*)(a.out + (long)out_row * a.hq * kD * 2);
+    for (int i = tid; i < a.hq * kD / 2; i += threads) o[i] = 0u;  // +0 in fp16 and bf16
+  }
+}
+
 template <class Elem, int HB, int PG, int MODE, int NW, bool ASYNC, int DEPTH = HB>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu((HB == 1 && DEPTH == 1) ? 2 : 1)))
 void decode_kernel(DecodeArgs a) {
@@ -1469,6 +1484,9 @@ void decode_kernel(DecodeArgs a) {
   const int lane = tid & 63;
   const int wave = uniform(tid >> 6);
   const int G = a.group;
+  if constexpr (MODE == kQueue) {
+    if (a.merge_counters) zero_empty_rows<Elem>(a, tid, kThreads);
+  }
 
   // Work-queue units: one dependent round trip for the work item, then one for all it
   // points to, issued together: the row's length, slot offsets and query row (vector

@@ -175,6 +175,7 @@ QUEUE = [
     ([300, 17000, 700, 256], 32, 8, 16, 20, False, F16),   # c4-like; empty splits on short rows
     ([300, 17000, 700, 256], 32, 8, 16, 1, True, F16),     # reference auto policy
     ([64, 33, 1], 32, 8, 16, 20, False, F16),              # more splits than tiles everywhere
+    ([700, 0, 300], 32, 8, 16, 6, False, F16),             # a row with no tokens (no work items)
     ([5000, 120], 32, 32, 16, 8, False, F16),              # G = 1
     ([2000, 4000, 900], 32, 1, 32, 12, False, BF16),       # G = 32 (MQA), page 32
     ([1500, 77], 32, 4, 32, 6, False, BF16),               # G = 8
