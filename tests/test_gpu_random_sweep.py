@@ -1,6 +1,6 @@
 """Seeded random sweep over the ops' argument space, against the repack + fp32 SDPA oracle.
 
-The parametrised tests elsewhere pin chosen shapes; this sweep draws 96 configurations from
+The parametrised tests elsewhere pin chosen shapes; this sweep draws 512 configurations from
 one seeded generator so that combinations no table lists are run too: every op (direct and
 split paged_attention, masked, indexed with permuted and sparse output rows, the work queue
 in both schedules and with the fused merge, contiguous K/V), G in {1, 2, 3, 4, 5, 8, 16,
@@ -43,7 +43,7 @@ def _ws(floats, gpu):
     return torch.empty(max(floats, 1), dtype=torch.float32, device=gpu)
 
 
-@pytest.mark.parametrize("i", range(96))
+@pytest.mark.parametrize("i", range(512))
 def test_random_configuration_matches_oracle(ext, gpu, i):
     c = _draw(i)
     op, hq, hkv, ps, lengths, splits, dtype = (c[k] for k in ("op", "hq", "hkv", "ps", "lengths",

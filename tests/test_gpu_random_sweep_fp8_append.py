@@ -1,6 +1,6 @@
 """Seeded random sweep over the fp8 and fused-append entry points.
 
-56 configurations from one seeded generator over paged_attention_indexed_fp8,
+256 configurations from one seeded generator over paged_attention_indexed_fp8,
 paged_attention_workqueue_fp8 and the five ops with the KV-cache append fused in (masked,
 indexed and work queue on 2-byte pools, indexed and work queue on fp8 pools): G 1-32,
 page sizes 5-64 (fp8 pools: 16, 32, 64, as the fp8 ops require), fp16 and bf16
@@ -51,7 +51,7 @@ def _quantise(x, scale):
     return (x.float() / scale).clamp(-448.0, 448.0).to(F8)
 
 
-@pytest.mark.parametrize("i", range(56))
+@pytest.mark.parametrize("i", range(256))
 def test_random_fp8_and_append_configuration(ext, gpu, i):
     c = _draw(i)
     print(f"case {i}: {c}", flush=True)

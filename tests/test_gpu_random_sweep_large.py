@@ -1,6 +1,6 @@
 """Seeded random sweep at serving-like sizes, against the repack + fp32 SDPA oracle.
 
-16 configurations with 20-256 rows whose lengths follow a heavy-tailed draw up to 20k
+40 configurations with 20-256 rows whose lengths follow a heavy-tailed draw up to 20k
 tokens (some 0), over the masked, indexed and work-queue ops (the work queue in both
 schedules: beyond 64 rows the balanced kernels read the row lengths in 2-4 chunks of 64),
 G in {1, 4, 8, 16, 32}, pages 16 and 32, fp16 and bf16, 1-20 splits.  Each case prints its
@@ -33,7 +33,7 @@ def _draw(i):
                 dtype=rng.choice([F16, BF16]), balanced=rng.random() < 0.7)
 
 
-@pytest.mark.parametrize("i", range(16))
+@pytest.mark.parametrize("i", range(40))
 def test_random_large_configuration_matches_oracle(ext, gpu, i):
     c = _draw(i)
     op, hq, hkv, ps, lengths, dtype = (c[k] for k in ("op", "hq", "hkv", "ps", "lengths", "dtype"))

@@ -1,6 +1,6 @@
 """Seeded random sweep over the work-queue op's stage entry points.
 
-24 configurations (G 1-32, pages 5-64, fp16 and bf16, fp8 K/V on a third of the draws
+128 configurations (G 1-32, pages 5-64, fp16 and bf16, fp8 K/V on a third of the draws
 with pages of a multiple of 16, 1-6 rows of 0-3000 tokens, 1-12 splits, both schedules):
 - paged_attention_workqueue_stage(1) then (2) on one workspace equals the combined op
   (the same schedule, chosen by the workspace size) bit for bit;
@@ -37,7 +37,7 @@ def _draw(i):
                 fp8=fp8, scale=rng.choice([0.03, 0.06]), balanced=rng.random() < 0.6)
 
 
-@pytest.mark.parametrize("i", range(24))
+@pytest.mark.parametrize("i", range(128))
 def test_random_stages_equal_combined(ext, gpu, i):
     c = _draw(i)
     print(f"case {i}: {c}", flush=True)
