@@ -261,10 +261,15 @@ struct TileRegs {
   u32x4 v[8];     // v[j]: V row of token slot j (v_slot_token), dims 8c .. +8
 };
 
-// fp8 K/V tile as loaded: the same lanes and rows as TileRegs, 8 one-byte elements per
-// 16-byte fp16 chunk.
+// fp8 K/V tile as loaded.  K: lane (g, c) holds 16 bytes of token c (+ 16b) per half h,
+// dims 64h + 16g .. +16; MFMA k-block kk takes the 8 bytes at dims 64(kk/2) + 16g +
+// 8(kk%2), and Q is loaded with the same dims (load_q<HB, true>).  A 16-byte load per lane
+// takes half of each 128-byte token row per instruction, as the 2-byte K loads do; 8-byte
+// loads (a quarter row, four requests per line) held the fp8 decode to 0.47 of 8 TB/s
+// against 0.62 with this layout.  V: the same lanes and rows as TileRegs, 8 one-byte
+// elements per 16-byte fp16 chunk.
 struct Fp8Tile {
-  u32x2 k[2][4];
+  u32x4 k[2][2];
   u32x2 v[8];
 };
 
@@ -437,8 +442,8 @@ struct ContigPager {
 };
 
 // Page-16 pager over fp8 (OCP e4m3) K/V: FastPager's table reads and per-lane rows with
-// 1-byte elements (a token row is 128 bytes), loaded 8 bytes per chunk and unpacked
-// exactly to fp16 / bf16 just before the tile is computed.
+// 1-byte elements (a token row is 128 bytes), K in 16-byte and V in 8-byte chunks (the
+// Fp8Tile layout), unpacked exactly to fp16 / bf16 just before the tile is computed.
 struct Fp8Pager {
   using Pages = FastPager::Pages;
   using Raw = Fp8Tile;
@@ -447,7 +452,7 @@ struct Fp8Pager {
   int lim;
   long head_bytes;   // kvh * ps * 128
   long page_bytes;   // Hkv * ps * 128
-  uint32_t koff[4];
+  uint32_t koff[2];
   uint32_t voff[8];
 
   __device__ Fp8Pager(const DecodeArgs& args, int row, int kvh, int limit, int lane)
@@ -457,7 +462,7 @@ struct Fp8Pager {
     page_bytes = (long)a.hkv * a.page_size * kD;
     const int c = lane & 15, g = lane >> 4;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) koff[kk] = c * 128 + kk * 32 + g * 8;
+    for (int h = 0; h < 2; ++h) koff[h] = c * 128 + h * 64 + g * 16;
 #pragma unroll
     for (int j = 0; j < 8; ++j) voff[j] = (4 * g + (j & 3)) * 128 + c * 8;
   }
@@ -491,7 +496,7 @@ struct Fp8Pager {
       const __amdgpu_buffer_rsrc_t rv =
           __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(a.v_pages + off), (short)0, nrec, kRsrcWord3);
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) r.k[b][kk] = __builtin_amdgcn_raw_buffer_load_b64(rk, koff[kk], 0, kKvLoadPolicy);
+      for (int h = 0; h < 2; ++h) r.k[b][h] = __builtin_amdgcn_raw_buffer_load_b128(rk, koff[h], 0, kKvLoadPolicy);
 #pragma unroll
       for (int j = 0; j < 4; ++j) r.v[b * 4 + j] = __builtin_amdgcn_raw_buffer_load_b64(rv, voff[b * 4 + j], 0, kKvLoadPolicy);
     }
@@ -578,7 +583,10 @@ __device__ inline u32x4 tile_k(const TileRegs& r, int b, int kk) { return r.k[b]
 template <class Elem>
 __device__ inline u32x4 tile_v(const TileRegs& r, int j) { return r.v[j]; }
 template <class Elem>
-__device__ inline u32x4 tile_k(const Fp8Tile& r, int b, int kk) { return Elem::unpack8(r.k[b][kk]); }
+__device__ inline u32x4 tile_k(const Fp8Tile& r, int b, int kk) {
+  const u32x4 w = r.k[b][kk >> 1];
+  return Elem::unpack8((kk & 1) ? u32x2{w[2], w[3]} : u32x2{w[0], w[1]});
+}
 template <class Elem>
 __device__ inline u32x4 tile_v(const Fp8Tile& r, int j) { return Elem::unpack8(r.v[j]); }
 
@@ -1137,11 +1145,12 @@ __device__ inline void unit_states(const DecodeArgs& a, const Unit& u, int qh0, 
   }
 }
 
-// Q^T operand: lane (g, c) holds head hb*16 + c, dims 32kk + 8g .. +8.  The query row is
+// Q^T operand: lane (g, c) holds head hb*16 + c, dims 32kk + 8g .. +8 (with K16, for fp8
+// K, dims 64(kk/2) + 16g + 8(kk%2) .. +8, matching Fp8Tile's K layout).  The query row is
 // `row`, or `q_loaded` (q_indices[row], the same in every lane) when q_indices is set.
 // q_loaded may still be in flight: the address is formed per lane, so its wait falls
 // right before the Q loads.
-template <int HB>
+template <int HB, bool K16 = false>
 __device__ inline void load_q(const DecodeArgs& a, int q_loaded, int row, int qh0, int lane,
                               u32x4 (&qf)[HB][4]) {
   const int c = lane & 15, g = lane >> 4;
@@ -1150,11 +1159,12 @@ __device__ inline void load_q(const DecodeArgs& a, int q_loaded, int row, int qh
 #pragma unroll
   for (int hb = 0; hb < HB; ++hb) {
     const int h = hb * 16 + c;
-    const uint8_t* qp = a.q + (((long)q_row * a.hq + qh0 + h) * kD + 8 * g) * 2;
+    const uint8_t* qp = a.q + (((long)q_row * a.hq + qh0 + h) * kD + (K16 ? 16 : 8) * g) * 2;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const u32x4 z = {0u, 0u, 0u, 0u};
-      qf[hb][kk] = h < a.group ? *(const u32x4*)(qp + kk * 64) : z;
+      const int off = K16 ? (64 * (kk >> 1) + 8 * (kk & 1)) * 2 : kk * 64;
+      qf[hb][kk] = h < a.group ? *(const u32x4*)(qp + off) : z;
     }
   }
 }
@@ -1440,7 +1450,7 @@ __device__ void solo_unit(const DecodeArgs& a, const Unit& u, int q_loaded, int 
                           FastPager::Pages f1) {
   const int qh0 = u.kvh * a.group;
   u32x4 qf[HB][4];
-  load_q<HB>(a, q_loaded, u.row, qh0, lane, qf);
+  load_q<HB, PG == kPgFp8>(a, q_loaded, u.row, qh0, lane, qf);
   WaveState<HB> st;
   init_state<HB>(st);
   stream_unit<Elem, HB, PG, DEPTH>(a, st, qf, u.row, u.kvh, t0, t1, u.len, lane, have_first, f0,
@@ -1552,7 +1562,7 @@ void decode_kernel(DecodeArgs a) {
     __syncthreads();
   }
   u32x4 qf[HB][4];
-  load_q<HB>(a, q_loaded, u.row, qh0, lane, qf);
+  load_q<HB, PG == kPgFp8>(a, q_loaded, u.row, qh0, lane, qf);
   WaveState<HB> st;
   init_state<HB>(st);
 
@@ -1822,7 +1832,7 @@ void balanced_decode_kernel(DecodeArgs a) {
     }
     const int qh0 = kvh * G;
     u32x4 qf[1][4];
-    load_q<1>(a, q_loaded, r, qh0, lane, qf);
+    load_q<1, PG == kPgFp8>(a, q_loaded, r, qh0, lane, qf);
     if (t0 == 0) {
       // The wave that holds the pair's first tile records the waves its tiles span (the
       // last tile, pair0 + kBalPieceCost + tiles - 1, lies in wave ceil((x + 1) V / T) - 1)

@@ -48,6 +48,7 @@ def main(argv=None):
     p.add_argument("--launches", type=int, default=96)
     p.add_argument("--kernel", default="pkv::decode_kernel")
     p.add_argument("--workload", default="c4")
+    p.add_argument("--kv-fp8", action="store_true", help="1-byte K/V elements (bench.py --kv-fp8)")
     p.add_argument("--seed", type=int, default=20260623)
     p.add_argument("-o", "--output", required=True)
     a = p.parse_args(argv)
@@ -65,13 +66,14 @@ def main(argv=None):
     import pkv_workloads as wl
 
     work = wl.CONFIGS[a.workload](seed=a.seed)
-    elem = 2
+    elem = 1 if a.kv_fp8 else 2
     step_bytes = [sum(s.lengths) * work.hkv * 128 * 2 * elem for s in work.steps]
     from bench import trace_sample  # the trace steps bench.py's decode-only pass replays
 
     alg = sum(step_bytes[i] for i in trace_sample(a.launches, len(step_bytes))) / a.launches
     out = {
-        "kernel": a.kernel, "workload": a.workload, "launches": len(f),
+        "kernel": a.kernel, "workload": a.workload + ("_fp8kv" if a.kv_fp8 else ""),
+        "launches": len(f),
         "fetch_kib_per_launch": round(sum(f) / len(f), 3),
         "write_kib_per_launch": round(sum(w) / len(w), 3),
         "fetch_scale": round(fetch_scale, 4), "write_scale": round(write_scale, 4),
