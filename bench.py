@@ -54,6 +54,7 @@ PUBLISHED_GBPS = {"smoke_g4_8k": 237.1, "smoke_g4_32k": 238.6}
 HBM_PEAK_GBPS = 8000.0
 MALL_BYTES = 256 * 2 ** 20  # MI355X Infinity Cache
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "c4_decode_traffic.json")
+TRAFFIC_FILE_FP8 = os.path.join(ROOT, "profiles", "c4_fp8_decode_traffic.json")
 
 
 def parse_args():
@@ -337,15 +338,16 @@ def main():
     alg_per_launch = total_bytes / args.steps
     achieved = total_bytes / (batched_us * 1e-6 * args.steps) / 1e9
     traffic, traffic_note = None, None
-    if args.workload == "c4" and queue and not w.kv_fp8 and os.path.exists(TRAFFIC_FILE):
-        with open(TRAFFIC_FILE) as fh:
+    traffic_file = TRAFFIC_FILE_FP8 if w.kv_fp8 else TRAFFIC_FILE
+    if args.workload == "c4" and queue and os.path.exists(traffic_file):
+        with open(traffic_file) as fh:
             prof = json.load(fh)
         ratio = prof["hbm_bytes_per_launch"] / prof["algorithmic_bytes_per_launch"]
         traffic = int(round(ratio * alg_per_launch))
         traffic_note = (f"rocprofv3 FETCH_SIZE x {prof['fetch_scale']:.2f} + WRITE_SIZE x "
                         f"{prof['write_scale']:.2f} = {ratio:.4f} x algorithmic bytes "
-                        f"(profiles/c4_decode_traffic.json, {prof['launches']} launches), "
-                        f"scaled to this sample")
+                        f"(profiles/{os.path.basename(traffic_file)}, {prof['launches']} "
+                        f"launches), scaled to this sample")
 
     value = total_bytes / (gpu_ms / 1e3) / 1e9
     kernel = {"paged_attention_workqueue": ("balanced_decode_kernel (stage 1 only)"
