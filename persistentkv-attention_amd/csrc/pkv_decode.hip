@@ -266,7 +266,7 @@ struct TileRegs {
 // 8(kk%2), and Q is loaded with the same dims (load_q<HB, true>).  A 16-byte load per lane
 // takes half of each 128-byte token row per instruction, as the 2-byte K loads do; 8-byte
 // loads (a quarter row, four requests per line) held the fp8 decode to 0.47 of 8 TB/s
-// against 0.62 with this layout.  V: the same lanes and rows as TileRegs, 8 one-byte
+// against 0.61 with this layout.  V: the same lanes and rows as TileRegs, 8 one-byte
 // elements per 16-byte fp16 chunk.
 struct Fp8Tile {
   u32x4 k[2][2];
