@@ -31,7 +31,8 @@ Differences from the reference, on purpose:
     where the reference reuses one pool.
 
 Command line (GPU):  python pkv_serving.py --workload c4 [--workload c3_32k ...]
-                      [--engines bucket workqueue adaptive] [--repeats 1] [--json F] [--md F]
+                      [--engines bucket workqueue adaptive] [--repeats 1] [--kv-fp8]
+                      [--json F] [--md F]
 """
 from __future__ import annotations
 
@@ -418,13 +419,15 @@ def benchmark_engine(step_fn, w, warmup_steps, repeats):
 # ---------------------------------------------------------------------------------
 # Driver.
 # ---------------------------------------------------------------------------------
-def run_workload(ext, name, engines, repeats, warmup, rotations, device, seed):
+def run_workload(ext, name, engines, repeats, warmup, rotations, device, seed, kv_fp8=False):
     w = wl.CONFIGS[name](seed=seed)
+    w.kv_fp8 = kv_fp8
     q_pool = wl.make_q_pool(w, device)
     k0, v0 = wl.make_kv_pool(w, device)
     pools = [(k0, v0)] + [(k0.clone(), v0.clone()) for _ in range(max(1, rotations) - 1)]
     report = {"workload": name, "hq": w.hq, "hkv": w.hkv, "page_size": w.page_size,
-              "dtype": str(w.dtype).replace("torch.", ""), "trace_steps": len(w.steps),
+              "dtype": str(w.dtype).replace("torch.", "") + (" (fp8 e4m3 K/V)" if kv_fp8 else ""),
+              "trace_steps": len(w.steps),
               "requests": len(w.requests), "repeats": repeats,
               "active_mean": statistics.mean(len(s.active_ids) for s in w.steps),
               "useful_kv_mb_per_step": statistics.mean(_mb(w.kv_bytes(i)) for i in range(len(w.steps))),
@@ -497,6 +500,9 @@ def main(argv=None):
     p.add_argument("--rotations", type=int, default=4,
                    help="KV pool replicas rotated per step (1 reuses one pool, as the reference)")
     p.add_argument("--seed", type=int, default=wl.DEFAULT_SEED)
+    p.add_argument("--kv-fp8", action="store_true",
+                   help="K/V pools in fp8 (OCP e4m3) with the workload's per-tensor scales; every "
+                        "engine runs the *_fp8 ops and the gate uses the dequantised pages")
     p.add_argument("--json")
     p.add_argument("--md")
     a = p.parse_args(argv)
@@ -506,7 +512,7 @@ def main(argv=None):
     reports = []
     for name in names:
         reports.append(run_workload(ext, name, a.engines, a.repeats, a.warmup, a.rotations,
-                                    device, a.seed))
+                                    device, a.seed, a.kv_fp8))
         torch.cuda.empty_cache()
     text = markdown(reports)
     print(text, flush=True)

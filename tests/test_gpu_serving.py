@@ -79,3 +79,26 @@ def test_harness_run_reports_every_engine(ext, gpu):
         assert s["event_p50_ms"] <= s["event_p95_ms"] <= s["event_p99_ms"]
     assert rep["engines"]["bucket"]["profile"]["launches_per_step"] == 2.0
     assert "persistentkv_workqueue" in rep["engines"]["workqueue"]["profile"]["route_counts"]
+
+
+def test_harness_fp8_engines_match_oracle(ext, gpu):
+    """fp8 (e4m3) pools through the three engines: the bucket engine's
+    paged_attention_indexed_fp8 launches, the work queue's paged_attention_workqueue_fp8 and
+    the adaptive engine's routed steps each match the repack + fp32 SDPA oracle on the
+    dequantised pages; a harness run passes its gate with every engine."""
+    w = wl.config_c4()
+    w.kv_fp8 = True
+    q_pool = wl.make_q_pool(w, gpu)
+    k, v = wl.make_kv_pool(w, gpu)
+    assert k.dtype == torch.float8_e4m3fn
+    kd, vd = serving.dequantize_pool(k, w.k_scale), serving.dequantize_pool(v, w.v_scale)
+    for name in ("bucket", "workqueue", "adaptive"):
+        eng = serving.Engine(name, w, gpu)
+        for i in (3, len(w.steps) - 1):
+            out = eng.run(ext, i, q_pool, k, v)
+            torch.cuda.synchronize()
+            assert_parity(out, _oracle(w, eng.gate_meta(i), q_pool[i], kd, vd))
+    rep = serving.run_workload(ext, "c4", ["bucket", "workqueue", "adaptive"], 1, 1, 2, gpu,
+                               wl.DEFAULT_SEED, kv_fp8=True)
+    assert "fp8" in rep["dtype"]
+    assert all(e["gate"]["pass"] for e in rep["engines"].values())
