@@ -140,7 +140,21 @@ int pkv_paged_attention_indexed(
 /* Compact work queue: one partial state per work item, then a segmented LSE merge
  * (or, with fused_merge != 0, the last work item of each (row, kv head) merges).
  * Replaces persistentkv_paged_attention_workqueue (extension.cu:230-317) and
- * persistentkv_paged_workqueue_indexed_dispatch (cuh:1191-1261). */
+ * persistentkv_paged_workqueue_indexed_dispatch (cuh:1191-1261).
+ * Work-queue contract (the reference's, cuh:294-363, :648-716, :753-784):
+ * - item (row, kvh, split, tile_begin, tile_end) writes the state of its own 32-token
+ *   tile range into slot split_offsets[row] + split; a negative bound stands for the
+ *   row-local split bound (cuh:330-337); a range without tiles writes the neutral state;
+ *   items with row, kvh, split or slot out of range are ignored;
+ * - row b's output folds the slots [split_offsets[b], split_offsets[b + 1]): every slot
+ *   when num_tasks >= num_kv_heads x (split_offsets[batch] - split_offsets[0]) (a queue
+ *   that writes each slot once, the queues on which the reference reads no unwritten
+ *   memory); otherwise the slots of splits whose row-local range is empty are skipped
+ *   (the builder's queues emit no item for them, and the reference then merges
+ *   uninitialised memory);
+ * - the fused merge waits for one arrival per slot in the first case (the reference's
+ *   row_splits arrivals, cuh:659) and one per non-empty split in the second, and also
+ *   merges rows of one slot (which the reference leaves unwritten). */
 int pkv_paged_attention_workqueue(
     const void* q_source, int32_t q_rows,
     const void* k_pages, const void* v_pages,
@@ -183,22 +197,26 @@ int pkv_paged_attention_workqueue_noalloc(
 
 /* Which schedule pkv_paged_attention_workqueue (and its fp8 and append variants) runs
  * for these sizes on the current device: 1 = the balanced schedule, 0 = one workgroup per
- * work item.  The balanced schedule streams every (row, kv head) pair's tiles with an equal
- * share per wave (4 waves per CU) and merges the pieces; it applies when fused_merge == 0,
- * G = num_q_heads / num_kv_heads <= 16, page_size is a multiple of 16, batch <= 256 and
- * the workspace holds pkv_workqueue_balanced_workspace_bytes.
- * It reads the work items' row set, not their tile ranges: the queue must be complete
- * (every non-empty split of every kv head of every row, as pkv_build_workqueue builds it),
- * which is the only input on which the reference's merge reads no unwritten slot.  Both
- * schedules give the same result to fp32 rounding.  No counterpart in the reference. */
+ * work item.  The balanced schedule streams every (row, kv head) pair's tiles [0, T) with
+ * an equal share per wave (4 waves per CU) and merges the pieces; it applies when
+ * fused_merge == 0, G = num_q_heads / num_kv_heads <= 16, page_size is a multiple of 16,
+ * batch <= 256 and the workspace holds pkv_workqueue_balanced_workspace_bytes.
+ * Streaming [0, T) is the reference's result for the queue pkv_build_workqueue (the
+ * reference's compile_persistentkv_metadata) builds.  The decode checks on the device that
+ * the caller's queue is exactly that one; for any other queue the merge stage computes
+ * each (row, kv head) pair from the items' own tile ranges instead (slower), so both
+ * schedules give the reference's result, to fp32 rounding, on every queue that writes
+ * each slot once, and the builder's result on the builder's queues.  No counterpart in
+ * the reference. */
 int pkv_workqueue_schedule(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
                            int32_t page_size, size_t workspace_bytes, int32_t fused_merge);
 
 /* Workspace bytes the balanced schedule needs on the current device: the partial states,
- * (batch * num_kv_heads + 4 * CUs) * (num_q_heads / num_kv_heads) * 130 * 4 bytes, then
- * at the next 16-byte boundary a 16-byte plan entry per (row, kv head) pair (the waves that
- * hold the pair's tiles, written by the decode stage for the merge stage); 0 for sizes it
- * never takes (G > 16 or batch > 256).  A complete queue's reference-sized workspace
+ * (batch * num_kv_heads + 4 * CUs) * (num_q_heads / num_kv_heads) rounded up to even,
+ * times 130 * 4 bytes, then a 16-byte plan entry per (row, kv head) pair (the waves that
+ * hold the pair's tiles, written by the decode stage for the merge stage), then 4 bytes
+ * per CU (each decode workgroup's part of the queue check); 0 for sizes it never takes
+ * (G > 16 or batch > 256).  A complete queue's reference-sized workspace
  * (pkv_workqueue_workspace_bytes) often holds it already (C4: 2.66 MB against 2.26 MB).
  * No counterpart in the reference. */
 size_t pkv_workqueue_balanced_workspace_bytes(int32_t batch, int32_t num_q_heads,
@@ -241,12 +259,17 @@ int pkv_workqueue_decode(
     int32_t num_pages, int32_t page_size, int32_t max_pages,
     int32_t bucket_context, int32_t total_partial_slots, int32_t dtype, void* stream);
 
+/* num_tasks and num_kv_heads are the queue's item count and Hkv.  When num_tasks >=
+ * num_kv_heads x (split_offsets[batch] - split_offsets[0]) (a queue that writes every
+ * slot) the merge folds every slot of a row, as the reference's does (cuh:766-780);
+ * otherwise (the builder's queues, whose splits without tiles emit no item) it skips the
+ * slots whose row-local bounds are empty.  num_tasks < 0 selects the second rule. */
 int pkv_workqueue_merge(
     const int32_t* seq_lens, const int32_t* split_offsets, const int32_t* out_indices,
     void* output, int32_t out_rows,
     const void* workspace, size_t workspace_bytes,
     int32_t batch, int32_t num_q_heads, int32_t total_partial_slots,
-    int32_t dtype, void* stream);
+    int32_t num_tasks, int32_t num_kv_heads, int32_t dtype, void* stream);
 
 /* ---------------------------------------------------------------------------------
  * fp8 K/V: the same ops over K and V pages of OCP fp8 e4m3 (1 byte per element, same

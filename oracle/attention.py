@@ -222,3 +222,72 @@ def append_kv(k_pages, v_pages, block_table, seq_lens, k_new, v_new):
             k_out[page, :, pos % ps] = _cpu(k_new)[b].to(k_out.dtype)
             v_out[page, :, pos % ps] = _cpu(v_new)[b].to(v_out.dtype)
     return k_out, v_out
+
+
+def workqueue_decode(q_source, k_pages, v_pages, block_table, seq_lens, work_items,
+                     split_offsets, q_indices, out_indices, out_rows, total_slots=None):
+    """Result of the work-queue op for any work queue, float32 ``[out_rows, Hq, 128]``.
+
+    Restates the reference's two kernels over a caller's queue, not only the builder's:
+    - each item ``(row, kvh, split, tb, te)`` writes the partial state of its tile range
+      for the G query heads of KV head ``kvh`` into slot ``split_offsets[row] + split``
+      (cuh:294-363, :615-632).  A negative ``tb`` or ``te`` means the row-local split
+      bound ``T*split//S`` or ``T*(split+1)//S`` (cuh:330-337, S = the row's slot count);
+      tokens at or past ``seq_lens[row]`` are masked (cuh:217-219), so a range past the
+      row's tiles contributes nothing, and a range with ``te <= tb`` is the neutral state
+      (cuh:340-363);
+    - row ``b``'s output folds every slot of ``[split_offsets[b], split_offsets[b+1])``
+      (cuh:753-784) into output row ``out_indices[b]``.
+    A slot that no item writes holds uninitialised memory in the reference (its result is
+    then undefined); here it is the neutral state, which is what the builder's queues
+    (empty splits emit no item) need.  Items whose row, KV head, split or slot lie outside
+    their ranges are ignored (the reference writes out of bounds there).  When several
+    items write one slot (a race in the reference), the last in queue order is kept.
+    """
+    q_source = _cpu(q_source)
+    hq = q_source.shape[1]
+    hkv = _cpu(k_pages).shape[1]
+    g = hq // hkv
+    table = _cpu(block_table)
+    lens = [int(x) for x in _cpu(seq_lens).tolist()]
+    offsets = [int(x) for x in _cpu(split_offsets).tolist()]
+    items = [[int(x) for x in it] for it in _cpu(work_items).reshape(-1, 5).tolist()]
+    q_idx = [int(x) for x in _cpu(q_indices).tolist()]
+    o_idx = [int(x) for x in _cpu(out_indices).tolist()]
+    batch = len(lens)
+    slots = total_slots if total_slots is not None else offsets[-1]
+    states = {}  # (slot, qh) -> (m, l, acc)
+    rows = {}
+    for row, kvh, split, tb, te in items:
+        if not (0 <= row < batch and 0 <= kvh < hkv):
+            continue
+        n_split = offsets[row + 1] - offsets[row]
+        slot = offsets[row] + split
+        if not (0 <= split < n_split and 0 <= slot < slots):
+            continue
+        length = lens[row]
+        total = (length + TILE - 1) // TILE
+        tb = tb if tb >= 0 else total * split // n_split
+        te = te if te >= 0 else total * (split + 1) // n_split
+        if row not in rows:
+            rows[row] = gather_row(k_pages, v_pages, table[row], length)
+        k, v = rows[row]
+        heads = range(kvh * g, (kvh + 1) * g)
+        m, l, acc = split_partials(q_source[q_idx[row]], k, v, [(max(tb, 0), max(te, 0))])
+        for h in heads:
+            states[(slot, h)] = (m[h, 0], l[h, 0], acc[h, 0])
+    out = torch.zeros(out_rows, hq, HEAD_DIM, dtype=torch.float32)
+    neutral = (float(NEG_FLT_MAX), 0.0, np.zeros(HEAD_DIM))
+    for b in range(batch):
+        lo, hi = max(offsets[b], 0), min(offsets[b + 1], slots)
+        if not 0 <= o_idx[b] < out_rows:
+            continue
+        for h in range(hq):
+            picked = [states.get((s, h), neutral) for s in range(lo, hi)]
+            if not picked:
+                continue
+            m = np.array([p[0] for p in picked])
+            l = np.array([p[1] for p in picked])
+            acc = np.stack([p[2] for p in picked])
+            out[o_idx[b], h] = torch.from_numpy(lse_merge(m, l, acc)).float()
+    return out

@@ -34,6 +34,7 @@
 #include <cmath>
 #include <mutex>
 #include <tuple>
+#include <type_traits>
 #include <vector>
 
 #include "pkv.h"
@@ -59,6 +60,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
@@ -150,8 +152,10 @@ struct DecodeArgs {
   const uint8_t* k_new;
   const uint8_t* v_new;
   // Balanced schedule only: per (row, kv head) pair, {first wave, waves, T low, T high} of
-  // its tiles, written by the decode for the merge (16-byte entries, 16-byte aligned).
+  // its tiles, written by the decode for the merge (16-byte entries, 16-byte aligned), and
+  // per decode workgroup the result of its part of the queue check (1 = passed).
   int32_t* bal_plan;
+  int32_t* bal_flags;
 };
 
 // ---------------------------------------------------------------------------------
@@ -717,6 +721,26 @@ __device__ inline void stream_range_from(WaveState<HB>& st, const Pager& pg,
   }
 }
 
+// The two-tiles-in-flight loop of stream_range_from entered with tiles t0 and t0 + 1
+// already issued (ra, rb) and the block-table read of tile t0 + 2 (pa) in flight.
+template <class Elem, int HB, class Pager>
+__device__ inline void stream_range_issued(WaveState<HB>& st, const Pager& pg,
+                                           const u32x4 (&qf)[HB][4], int t0, int t1, int lim,
+                                           int lane, float qk, typename Pager::Raw& ra,
+                                           typename Pager::Raw& rb, typename Pager::Pages pa) {
+  typename Pager::Pages pb;
+  for (int t = t0;; t += 2) {
+    compute_tile<Elem, HB>(st, ra, qf, t, lim, lane, qk);
+    if (t + 1 >= t1) break;
+    pg.issue(t + 2, pa, ra);
+    pb = pg.lookup(t + 3);
+    compute_tile<Elem, HB>(st, rb, qf, t + 1, lim, lane, qk);
+    if (t + 2 >= t1) break;
+    pg.issue(t + 3, pb, rb);
+    pa = pg.lookup(t + 4);
+  }
+}
+
 template <class Elem, int HB, class Pager, int DEPTH = HB>
 __device__ inline void stream_range(WaveState<HB>& st, const Pager& pg, const u32x4 (&qf)[HB][4],
                                     int t0, int t1, int lim, int lane, float qk) {
@@ -736,8 +760,12 @@ struct Unit {
 
 __device__ inline int ceil_tiles(int len) { return (len + kTile - 1) / kTile; }
 
-// Work-queue unit from a work item and its row's length and slot offsets.  Malformed
-// items are marked invalid (and skipped) instead of addressing outside the buffers.
+// Work-queue unit from a work item and its row's length and slot offsets.  The item's
+// tile range is honoured as given (cuh:298-337); a negative bound stands for the
+// row-local split bound of its split (cuh:330-337), and the range is clamped to the
+// row's tiles (tokens past the length are masked in the reference, cuh:217-219).
+// Malformed items are marked invalid (and skipped) instead of addressing outside the
+// buffers.
 __device__ inline Unit queue_unit(const DecodeArgs& a, int row, int kvh, int split, int tb, int te,
                                   int len, int so0, int so1) {
   Unit u;
@@ -745,8 +773,8 @@ __device__ inline Unit queue_unit(const DecodeArgs& a, int row, int kvh, int spl
   u.row = row;
   u.kvh = kvh;
   u.split = split;
-  u.tb = tb < 0 ? 0 : tb;
-  u.te = te;
+  u.tb = 0;
+  u.te = 0;
   u.len = 0;
   u.slot_base = 0;
   u.row_splits = 1;
@@ -758,8 +786,14 @@ __device__ inline Unit queue_unit(const DecodeArgs& a, int row, int kvh, int spl
   u.slot_base = so0;
   u.row_splits = so1 - so0;
   const int total = ceil_tiles(u.len);
-  if (split >= u.row_splits) u.valid = false;
-  if (u.te > total) u.te = total;
+  if (split >= u.row_splits) {
+    u.valid = false;
+    return u;
+  }
+  if (tb < 0) tb = (int)(((long)total * split) / u.row_splits);
+  if (te < 0) te = (int)(((long)total * (split + 1)) / u.row_splits);
+  u.tb = tb;
+  u.te = te > total ? total : te;
   if (u.slot_base < 0 || u.slot_base + split >= a.total_slots) u.valid = false;
   return u;
 }
@@ -972,26 +1006,39 @@ __device__ inline void load_chunk_if(SlotChunk& c, const float* pm, const float*
                    : f32x2{0.f, 0.f};
 }
 
-// Whether slot s of a row holds a state: in queue mode the builder leaves splits with no
-// tiles empty (split0 + s of nsplit splits over `total` tiles).
+// Whether slot s of a row holds a state.  In queue mode the builder leaves splits with no
+// tiles unwritten (split0 + s of nsplit splits over `total` tiles); `all` (a queue that
+// writes every slot, see queue_writes_every_slot) folds every slot, as the reference does.
 template <bool QUEUE>
-__device__ inline bool slot_live(int s, int count, long total, int nsplit, int split0) {
+__device__ inline bool slot_live(int s, int count, long total, int nsplit, int split0,
+                                 bool all = false) {
   // With at least as many tiles as splits every split holds one (the divisions are
   // skipped: total and nsplit are wave-uniform).
-  return s < count && !(QUEUE && total < nsplit &&
-                        total * (split0 + s) / nsplit == total * (split0 + s + 1) / nsplit);
+  return s < count && (all || !(QUEUE && total < nsplit &&
+                                total * (split0 + s) / nsplit == total * (split0 + s + 1) / nsplit));
+}
+
+// Whether a work queue writes every slot of its rows: the reference merges every slot of
+// a row (cuh:753-784), so a queue it defines has one item per (slot, kv head), i.e. at
+// least Hkv x (split_offsets[B] - split_offsets[0]) items.  The builder's queues emit no
+// item for a split without tiles (benchmark_serving_trace.py:699-700), leaving those slots
+// unwritten (the reference then merges uninitialised memory); with fewer items the merge
+// therefore skips the slots whose row-local bounds are empty and folds the rest.
+__device__ inline bool queue_writes_every_slot(long num_tasks, int hkv, int so_first, int so_last) {
+  return num_tasks >= (long)hkv * ((long)so_last - so_first);
 }
 
 // Folds slot states [c_begin, count) into acc, 32 at a time.
 template <bool QUEUE, bool COHERENT>
 __device__ inline void fold_slots(LseAcc& acc, const float* pm, const float* pl, const float* pacc,
                                   long base, long stride, int count, long total, int nsplit,
-                                  int split0, int lane, int c_begin = 0) {
+                                  int split0, int lane, int c_begin = 0, bool all = false) {
   for (int c0 = c_begin; c0 < count; c0 += kMergeChunk) {
     const int n = count - c0 < kMergeChunk ? count - c0 : kMergeChunk;
     SlotChunk c;
     load_chunk<COHERENT>(c, pm, pl, pacc, base, stride, c0, n, lane);
-    acc.fold(lane < n && slot_live<QUEUE>(c0 + lane, count, total, nsplit, split0), c.ms, c.ls, c.v);
+    acc.fold(lane < n && slot_live<QUEUE>(c0 + lane, count, total, nsplit, split0, all), c.ms,
+             c.ls, c.v);
   }
 }
 
@@ -1074,21 +1121,27 @@ __device__ inline void fold_wide(LseAcc& acc, const float* pm, const float* pl, 
 // Fused merge of query head qh of a work-queue row by one wave, run by the last work item
 // of the row's (row, kv head) group to finish (cuh:648-716).  Slots are
 // (split_offsets[row] + s)*Hq + qh.
+__device__ inline int unit_slot_count(const DecodeArgs& a, const Unit& u) {
+  return u.slot_base + u.row_splits > a.total_slots ? a.total_slots - u.slot_base : u.row_splits;
+}
+
+// `all`: the queue writes every slot (queue_writes_every_slot).
 template <class Elem>
-__device__ inline void fused_merge_head(const DecodeArgs& a, const Unit& u, int qh, int lane) {
+__device__ inline void fused_merge_head(const DecodeArgs& a, const Unit& u, int qh, int lane,
+                                        bool all) {
   const int out_row = a.out_indices ? a.out_indices[u.row] : u.row;
   if (out_row < 0 || out_row >= a.out_rows) return;
-  const int count = u.slot_base + u.row_splits > a.total_slots ? a.total_slots - u.slot_base
-                                                                : u.row_splits;
   LseAcc acc;
   fold_slots<true, true>(acc, a.part_m, a.part_l, a.part_acc, (long)u.slot_base * a.hq + qh, a.hq,
-                         count, ceil_tiles(u.len), u.row_splits, 0, lane);
+                         unit_slot_count(a, u), ceil_tiles(u.len), u.row_splits, 0, lane, 0, all);
   acc.store<Elem>(a.out + ((long)out_row * a.hq + qh) * kD * 2, lane);
 }
 
-// Work items of one (row, kv head): one per non-empty split (the builder emits no empty
-// ones), so the last arrival is the min(S_row, T)-th.
-__device__ inline int expected_arrivals(const Unit& u) {
+// Work items of one (row, kv head): one per slot of the row when the queue writes every
+// slot (the reference's count, row_splits, cuh:659), else one per non-empty split (the
+// builder emits no empty ones), min(S_row, T).
+__device__ inline int expected_arrivals(const DecodeArgs& a, const Unit& u, bool all) {
+  if (all) return unit_slot_count(a, u);
   const int total = ceil_tiles(u.len);
   return u.row_splits < total ? u.row_splits : total;
 }
@@ -1105,14 +1158,14 @@ __device__ inline int expected_arrivals(const Unit& u) {
 // arrivals together); the second barrier passes the acquire on to the merging waves.
 template <class Elem>
 __device__ inline void arrive(const DecodeArgs& a, const Unit& u, int qh0, int lane, int wave,
-                              int nwaves) {
+                              int nwaves, bool all) {
   __shared__ int last_flag;
   int32_t* counter = a.merge_counters + (long)u.row * a.hkv + u.kvh;
   if (nwaves > 1) __syncthreads();
   int last = 0;
   if (wave == 0 && lane == 0) {
     const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    last = old == expected_arrivals(u) - 1;
+    last = old == expected_arrivals(a, u, all) - 1;
     if (nwaves > 1) last_flag = last;
   }
   if (nwaves > 1) {
@@ -1122,7 +1175,7 @@ __device__ inline void arrive(const DecodeArgs& a, const Unit& u, int qh0, int l
     last = uniform(last);
   }
   if (last) {
-    for (int h = wave; h < a.group; h += nwaves) fused_merge_head<Elem>(a, u, qh0 + h, lane);
+    for (int h = wave; h < a.group; h += nwaves) fused_merge_head<Elem>(a, u, qh0 + h, lane, all);
     if (wave == 0 && lane == 0)
       __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
@@ -1185,11 +1238,13 @@ __device__ inline void init_state(WaveState<HB>& st) {
 // size, or contiguous.
 enum : int { kPgGeneric = 0, kPgFast = 1, kPgContig = 2, kPgFp8 = 3, kPgAppend = 4 };
 
+// Streams tiles [t0, t1) of (row, kvh) into the wave state without finishing it, so that
+// several ranges can be streamed into one state (finish_state ends it).
 template <class Elem, int HB, int PG, int DEPTH = HB>
-__device__ inline void stream_unit(const DecodeArgs& a, WaveState<HB>& st, const u32x4 (&qf)[HB][4],
-                                   int row, int kvh, int t0, int t1, int len, int lane,
-                                   bool have_first = false, FastPager::Pages f0 = {},
-                                   FastPager::Pages f1 = {}) {
+__device__ inline void stream_tiles(const DecodeArgs& a, WaveState<HB>& st, const u32x4 (&qf)[HB][4],
+                                    int row, int kvh, int t0, int t1, int len, int lane,
+                                    bool have_first = false, FastPager::Pages f0 = {},
+                                    FastPager::Pages f1 = {}) {
   const long lim_l = (long)t1 * kTile;
   const int lim = uniform(lim_l < len ? (int)lim_l : len);
   const float qk = a.score_scale;
@@ -1212,11 +1267,26 @@ __device__ inline void stream_unit(const DecodeArgs& a, WaveState<HB>& st, const
     GenericPager pg(a, row, kvh, lim, lane);
     stream_range<Elem, HB, decltype(pg), DEPTH>(st, pg, qf, t0, t1, lim, lane, qk);
   }
+}
+
+// Ends a wave state: the lane-partial sums and maxima of each head are reduced over the
+// head's four lanes.
+template <int HB>
+__device__ inline void finish_state(WaveState<HB>& st) {
 #pragma unroll
   for (int hb = 0; hb < HB; ++hb) {
     st.l[hb] = head_sum(st.l[hb]);
     st.mx[hb] = head_max(st.mx[hb]);
   }
+}
+
+template <class Elem, int HB, int PG, int DEPTH = HB>
+__device__ inline void stream_unit(const DecodeArgs& a, WaveState<HB>& st, const u32x4 (&qf)[HB][4],
+                                   int row, int kvh, int t0, int t1, int len, int lane,
+                                   bool have_first = false, FastPager::Pages f0 = {},
+                                   FastPager::Pages f1 = {}) {
+  stream_tiles<Elem, HB, PG, DEPTH>(a, st, qf, row, kvh, t0, t1, len, lane, have_first, f0, f1);
+  finish_state<HB>(st);
 }
 
 // ---------------------------------------------------------------------------------
@@ -1447,7 +1517,7 @@ constexpr int kSoloTiles = 2;
 template <class Elem, int HB, int PG, int MODE, int DEPTH = HB>
 __device__ void solo_unit(const DecodeArgs& a, const Unit& u, int q_loaded, int t0, int t1,
                           const Dest& d, int lane, bool have_first, FastPager::Pages f0,
-                          FastPager::Pages f1) {
+                          FastPager::Pages f1, bool fused_all) {
   const int qh0 = u.kvh * a.group;
   u32x4 qf[HB][4];
   load_q<HB, PG == kPgFp8>(a, q_loaded, u.row, qh0, lane, qf);
@@ -1457,7 +1527,7 @@ __device__ void solo_unit(const DecodeArgs& a, const Unit& u, int q_loaded, int 
                                    f1);
   const int out_row = MODE == kDirect ? (a.out_indices ? a.out_indices[u.row] : u.row) : 0;
   write_wave_state<Elem, HB, MODE == kDirect>(a, st, qh0, out_row, d, lane);
-  if (MODE == kQueue && a.merge_counters != nullptr) arrive<Elem>(a, u, qh0, lane, 0, 1);
+  if (MODE == kQueue && a.merge_counters != nullptr) arrive<Elem>(a, u, qh0, lane, 0, 1, fused_all);
 }
 
 // ---------------------------------------------------------------------------------
@@ -1494,8 +1564,15 @@ void decode_kernel(DecodeArgs a) {
   const int lane = tid & 63;
   const int wave = uniform(tid >> 6);
   const int G = a.group;
+  // Fused merge: whether the queue writes every slot (the arrival count and the merge's
+  // slot rule follow from it).  Loaded here, waited for at the arrival.
+  int so_first = 0, so_last = 0;
   if constexpr (MODE == kQueue) {
-    if (a.merge_counters) zero_empty_rows<Elem>(a, tid, kThreads);
+    if (a.merge_counters) {
+      so_first = load_vector_deferred(a.split_offsets);
+      so_last = load_vector_deferred(a.split_offsets + a.batch);
+      zero_empty_rows<Elem>(a, tid, kThreads);
+    }
   }
 
   // Work-queue units: one dependent round trip for the work item, then one for all it
@@ -1540,10 +1617,15 @@ void decode_kernel(DecodeArgs a) {
   long state0, state_stride;
   unit_states<MODE>(a, u, qh0, state0, state_stride);
   const bool fused = MODE == kQueue && a.merge_counters != nullptr;
+  const bool fused_all =
+      fused && queue_writes_every_slot(a.num_tasks, a.hkv, uniform(so_first), uniform(so_last));
   const Dest d{a.part_m, a.part_l, a.part_acc, state0, state_stride, fused};
 
   if (MODE != kDirect && u.tb >= u.te) {
     write_neutral(a, state0, state_stride, G, tid, kThreads, fused);
+    // An item without tiles is one of its row's arrivals too (a queue that writes every
+    // slot; the builder emits none).
+    if (fused) arrive<Elem>(a, u, qh0, lane, wave, kWaves, fused_all);
     return;
   }
 
@@ -1553,7 +1635,7 @@ void decode_kernel(DecodeArgs a) {
   if (n <= kSoloTiles) {
     if (wave == 0)
       solo_unit<Elem, HB, PG, MODE, DEPTH>(a, u, q_loaded, u.tb, u.te, d, lane,
-                                           u.tb == first_tile, first0, first1);
+                                           u.tb == first_tile, first0, first1, fused_all);
     return;
   }
 
@@ -1575,10 +1657,10 @@ void decode_kernel(DecodeArgs a) {
   if constexpr (ASYNC) {
     if (!combine_async<Elem, HB, NW, MODE == kDirect>(a, st, lds, &arrivals, qh0, out_row, d, lane, wave))
       return;
-    if (fused) arrive<Elem>(a, u, qh0, lane, 0, 1);
+    if (fused) arrive<Elem>(a, u, qh0, lane, 0, 1, fused_all);
   } else {
     combine_waves<Elem, HB, NW, MODE == kDirect>(a, st, lds, qh0, out_row, d, tid, lane, wave);
-    if (fused) arrive<Elem>(a, u, qh0, lane, wave, kWaves);
+    if (fused) arrive<Elem>(a, u, qh0, lane, wave, kWaves, fused_all);
   }
 }
 
@@ -1599,6 +1681,7 @@ struct MergeArgs {
   int32_t num_splits;            // split mode
   int32_t total_slots;           // queue mode
   int32_t context, max_tokens;   // split mode length fallback / clamp
+  int32_t num_tasks, hkv;        // queue mode: the queue's item count (-1: unknown) and Hkv
 };
 
 template <class Elem, bool QUEUE>
@@ -1611,6 +1694,7 @@ __global__ __launch_bounds__(64) void merge_kernel(MergeArgs a) {
   // The output row is loaded first and waited for last, so it costs no round trip of its own.
   const int out_row_loaded = load_vector_deferred(a.out_indices ? a.out_indices + row : nullptr);
   int count, total = 0, nsplit = 1, split0 = 0;
+  bool all = false;  // queue mode: every slot of the row is folded
   long base, stride;
   SlotChunk guessed;
   bool hit = false;
@@ -1619,9 +1703,13 @@ __global__ __launch_bounds__(64) void merge_kernel(MergeArgs a) {
     // of that slot range is loaded right behind the row's offsets and length and used when
     // the offsets match: the merge then waits for one memory round trip instead of two.
     // (Vector loads complete in issue order, so the offsets can be waited for alone.)
+    const int so_first = load_vector_deferred(a.split_offsets);
+    const int so_last = load_vector_deferred(a.split_offsets + a.batch);
     const int o0 = load_vector_uniform(a.split_offsets + row);
     const int o1 = load_vector_uniform(a.split_offsets + row + 1);
     int len = load_vector_uniform(a.seq_lens + row);
+    all = a.num_tasks >= 0 && queue_writes_every_slot(a.num_tasks, a.hkv, uniform(so_first),
+                                                      uniform(so_last));
     const int per_row = a.total_slots / a.batch;
     const bool guess = per_row > 0 && per_row * a.batch == a.total_slots;
     load_chunk_if(guessed, a.part_m, a.part_l, a.part_acc, (long)row * per_row * a.hq + qh, a.hq,
@@ -1656,12 +1744,13 @@ __global__ __launch_bounds__(64) void merge_kernel(MergeArgs a) {
     c.ls = hit ? guessed.ls : c.ls;
 #pragma unroll
     for (int j = 0; j < kMergeChunk; ++j) c.v[j] = hit ? guessed.v[j] : c.v[j];
-    acc.fold(lane < count && lane < kMergeChunk && slot_live<QUEUE>(lane, count, total, nsplit, split0),
+    acc.fold(lane < count && lane < kMergeChunk &&
+                 slot_live<QUEUE>(lane, count, total, nsplit, split0, all),
              c.ms, c.ls, c.v);
     c_begin = kMergeChunk;
   }
   fold_slots<QUEUE, false>(acc, a.part_m, a.part_l, a.part_acc, base, stride, count, total, nsplit,
-                           split0, lane, c_begin);
+                           split0, lane, c_begin, all);
   const int out_row = a.out_indices ? uniform(out_row_loaded) : row;
   if (out_row < 0 || out_row >= a.out_rows) return;
   acc.store<Elem>(a.out + ((long)out_row * a.hq + qh) * kD * 2, lane);
@@ -1750,13 +1839,24 @@ __device__ inline void row_chunk(const DecodeArgs& a, int lane, int k, int raw, 
 // kBalRowChunks (checked on the host).  The lengths are read through one buffer descriptor
 // that covers seq_lens[0, batch): the four loads go out together with no branch between
 // them, and lanes past the batch read 0 without touching memory.
-__device__ inline void row_table(const DecodeArgs& a, int lane, RowTable& t) {
+// Lanes' raw values of an int32 array at rows lane + 64k, k < 4, read through one buffer
+// descriptor over [0, n): the four loads go out together, and lanes past n read 0.
+struct RowInts {
+  int v0, v1, v2, v3;
+};
+__device__ inline RowInts load_row_ints(const int32_t* p, int n, int lane, int shift = 0) {
   const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
-      uniform_ptr(a.seq_lens), (short)0, uniform(a.batch > 0 ? a.batch * 4 : 0), kRsrcWord3);
-  const int raw0 = (int)__builtin_amdgcn_raw_buffer_load_b32(r, 4 * lane, 0, 0);
-  const int raw1 = (int)__builtin_amdgcn_raw_buffer_load_b32(r, 4 * lane + 256, 0, 0);
-  const int raw2 = (int)__builtin_amdgcn_raw_buffer_load_b32(r, 4 * lane + 512, 0, 0);
-  const int raw3 = (int)__builtin_amdgcn_raw_buffer_load_b32(r, 4 * lane + 768, 0, 0);
+      uniform_ptr(p), (short)0, uniform(n > 0 ? n * 4 : 0), kRsrcWord3);
+  const int o = 4 * (lane + shift);
+  return RowInts{(int)__builtin_amdgcn_raw_buffer_load_b32(r, o, 0, 0),
+                 (int)__builtin_amdgcn_raw_buffer_load_b32(r, o + 256, 0, 0),
+                 (int)__builtin_amdgcn_raw_buffer_load_b32(r, o + 512, 0, 0),
+                 (int)__builtin_amdgcn_raw_buffer_load_b32(r, o + 768, 0, 0)};
+}
+
+__device__ inline void row_table_from(const DecodeArgs& a, int lane, const RowInts& raw,
+                                      RowTable& t) {
+  const int raw0 = raw.v0, raw1 = raw.v1, raw2 = raw.v2, raw3 = raw.v3;
   // Chunks past the batch hold no row: their prefix is the total.
   long carry = 0;
   row_chunk(a, lane, 0, raw0, t.len0, t.incl0, carry);
@@ -1768,6 +1868,10 @@ __device__ inline void row_table(const DecodeArgs& a, int lane, RowTable& t) {
   if (a.batch <= 128) t.incl2 = carry;
   if (a.batch <= 192) t.incl3 = carry;
   t.total = carry;
+}
+
+__device__ inline void row_table(const DecodeArgs& a, int lane, RowTable& t) {
+  row_table_from(a, lane, load_row_ints(a.seq_lens, a.batch, lane), t);
 }
 
 // Length and inclusive prefix of row r (wave-uniform r): each chunk's value at lane r % 64
@@ -1793,16 +1897,149 @@ __device__ inline int table_row(const RowTable& t, long x) {
          __builtin_popcountll(__builtin_amdgcn_ballot_w64(t.incl3 <= x));
 }
 
+// ---------------------------------------------------------------------------------
+// Queue check of the balanced schedule.  The schedule streams each (row, kv head) pair's
+// tiles [0, T) once, which is what the reference computes for the queue that
+// compile_persistentkv_metadata builds (benchmark_serving_trace.py:668-729): for each row
+// in order, each split s of its S = split_offsets[row + 1] - split_offsets[row] with a
+// non-empty row-local range [T s / S, T (s + 1) / S) (cuh:330-337), the items
+// (row, kvh, s, range) for kvh = 0 .. Hkv - 1.  The queue is that one when
+// - every row has S >= 0, and S >= 1 when it has tiles; split_offsets[0] >= 0 and
+//   split_offsets[B] <= total_slots;
+// - num_tasks = Hkv x sum over rows of min(S, T) (the non-empty splits);
+// - every item idx = (r, k, s, tb, te) has 0 <= r < B, 0 <= k < Hkv, 0 <= s < S_r, the
+//   row-local range of split s (a negative bound standing for it, cuh:330-337), which is
+//   non-empty, and idx = Hkv x (P_r + n) + k, with P_r the non-empty splits of the rows
+//   before r and n = min(s, tb) those of row r before split s (with T >= S every split
+//   is non-empty, n = s; with T < S each holds one tile, n = tb).
+// The index rule maps distinct (r, s, k) to distinct positions of [0, num_tasks), so such
+// a queue holds each expected item once and nothing else.  Decode workgroup w checks the
+// row conditions and the items [w c, (w + 1) c), c = ceil(num_tasks / workgroups), in its
+// wave 0 before that wave's pieces (~5 items at C4's 1,280 over 256 workgroups; checking
+// every item in every workgroup cost the decode ~3 us, checking after the pieces ~0.7 us,
+// against ~0.3 us here), and writes the result to bal_flags[w]; the merge reads every
+// flag, and on any failure computes the pairs itself (balanced_merge_fallback).
+// ---------------------------------------------------------------------------------
+constexpr int kRowEntry = 4;                                   // ints per row: {P, T, S, len}
+
+// Fields of up to 64 items, one per lane: items first + lane (buffer loads that read 0 past
+// num_tasks).
+struct ItemLane {
+  int f[5];
+};
+__device__ inline ItemLane load_item_lane(const DecodeArgs& a, long first, int lane) {
+  const long idx = first + lane;
+  const int off = idx < a.num_tasks ? (int)(idx * 20) : 0;
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+      uniform_ptr(a.work_items), (short)0, uniform(a.num_tasks * 20), kRsrcWord3);
+  ItemLane it;
+#pragma unroll
+  for (int q = 0; q < 5; ++q)
+    it.f[q] = idx < a.num_tasks ? (int)__builtin_amdgcn_raw_buffer_load_b32(r, off + 4 * q, 0, 0) : 0;
+  return it;
+}
+
+// Whether item idx (fields f) is the builder's idx-th item; e is the row entry of row f[0]
+// clamped into the batch.
+__device__ inline bool item_is_builders(const DecodeArgs& a, long idx, const int (&f)[5],
+                                        const i32x4& e) {
+  const int r = f[0], k = f[1], s = f[2];
+  const long T = e[1], S = e[2];
+  const bool fields = (unsigned)r < (unsigned)a.batch && (unsigned)k < (unsigned)a.hkv &&
+                      s >= 0 && s < S;
+  const long ts = T * s, ts1 = ts + T;
+  long tb = f[3], te = f[4];
+  // A negative bound stands for the row-local one (a division, taken only when a lane of
+  // the wave has such a bound; the builder writes none).
+  if (__builtin_amdgcn_ballot_w64(fields && (tb < 0 || te < 0)) != 0) {
+    const long Sd = S > 0 ? S : 1;
+    if (tb < 0) tb = ts / Sd;
+    if (te < 0) te = ts1 / Sd;
+  }
+  // tb = floor(T s / S) and te = floor(T (s + 1) / S), checked without dividing.
+  const bool bounds = tb * S <= ts && ts < (tb + 1) * S && te * S <= ts1 && ts1 < (te + 1) * S;
+  const long n = T >= S ? s : tb;
+  return idx >= a.num_tasks ||
+         (fields && bounds && te > tb && idx == (long)a.hkv * (e[0] + n) + k);
+}
+
+// One chunk of the row table for the check: lane holds row r = lane + 64 k; returns its
+// count of non-empty splits and folds the row-level conditions into ok.
+__device__ inline long check_row(const DecodeArgs& a, int lane, int k, int len, int so0, int so1,
+                                 bool& ok) {
+  const int r = lane + 64 * k;
+  if (r >= a.batch) return 0;
+  const int T = ceil_tiles(len);
+  const int S = so1 - so0;
+  if (S < 0 || (T > 0 && S < 1)) ok = false;
+  return T > 0 && S > 0 ? (S < T ? S : T) : 0;
+}
+
+// This workgroup's part of the check, by one wave: the row conditions, then the items
+// [first, first + count) against a table of the rows {P, T, S, len} in the wave's LDS
+// `rows` (a wave's LDS stores are visible to its later LDS loads).  `lead` holds items
+// first .. first + 63 as loaded at the kernel's start.
+__device__ inline bool check_queue_part(const DecodeArgs& a, const RowTable& t, const RowInts& so0,
+                                        const RowInts& so1, int so_last, int32_t* rows,
+                                        const ItemLane& lead, long first, long count, int lane) {
+  bool ok = true;
+  const int lens[4] = {t.len0, t.len1, t.len2, t.len3};
+  const int s0[4] = {so0.v0, so0.v1, so0.v2, so0.v3};
+  const int s1[4] = {so1.v0, so1.v1, so1.v2, so1.v3};
+  long carry = 0;
+#pragma unroll
+  for (int k = 0; k < kBalRowChunks; ++k) {
+    if (k * 64 >= a.batch) break;
+    const long ne = check_row(a, lane, k, lens[k], s0[k], s1[k], ok);
+    const long incl = wave_incl_scan(ne, lane) + carry;
+    carry = read_lane64(incl, 63);
+    const int r = lane + 64 * k;
+    if (r < a.batch) {
+      const long p = incl - ne;
+      *(i32x4*)(rows + r * kRowEntry) =
+          i32x4{p < 0x7fffffffL ? (int)p : 0x7fffffff, ceil_tiles(lens[k]), s1[k] - s0[k], lens[k]};
+    }
+  }
+  ok = __builtin_amdgcn_ballot_w64(!ok) == 0;
+  ok = ok && a.num_tasks == (long)a.hkv * carry && uniform(s0[0]) >= 0 && so_last <= a.total_slots;
+  for (long c0 = 0; c0 < count; c0 += 64) {
+    const ItemLane it = c0 == 0 ? lead : load_item_lane(a, first + c0, lane);
+    const int r = (unsigned)it.f[0] < (unsigned)a.batch ? it.f[0] : 0;
+    const i32x4 e = *(const i32x4*)(rows + r * kRowEntry);
+    const bool mine = c0 + lane < count;
+    ok = ok && __builtin_amdgcn_ballot_w64(mine && !item_is_builders(a, first + c0 + lane, it.f, e)) == 0;
+  }
+  return ok;
+}
+
 // One workgroup of kBalWaves independent waves per CU (the launch asks for enough LDS that
-// no two share a CU).  The caller's work items are not read: the queue is complete.
+// no two share a CU).
 template <class Elem, int PG>
 __global__ __launch_bounds__(kBalWaves * 64) __attribute__((amdgpu_waves_per_eu(1)))
 void balanced_decode_kernel(DecodeArgs a) {
+  extern __shared__ int32_t bal_lds[];  // wave 0: the row table of the queue check
   const int lane = threadIdx.x & 63;
+  const int wave = uniform(threadIdx.x >> 6);
   const long V = (long)gridDim.x * kBalWaves;
-  const long v = (long)blockIdx.x * kBalWaves + uniform(threadIdx.x >> 6);
+  const long v = (long)blockIdx.x * kBalWaves + wave;
+  // This workgroup's items of the queue check (wave 0), loaded with the lengths and slot
+  // offsets; lanes past the queue load nothing.
+  const int per_wg = (int)(((unsigned)a.num_tasks + gridDim.x - 1) / gridDim.x);
+  const long item0 = (long)blockIdx.x * per_wg;
+  const long items = item0 >= a.num_tasks ? 0 : (a.num_tasks - item0 < per_wg ? a.num_tasks - item0 : per_wg);
   RowTable t;
-  row_table(a, lane, t);
+  if (wave == 0) {
+    const RowInts lens = load_row_ints(a.seq_lens, a.batch, lane);
+    const RowInts so0 = load_row_ints(a.split_offsets, a.batch + 1, lane);
+    const RowInts so1 = load_row_ints(a.split_offsets, a.batch + 1, lane, 1);
+    const int so_last = load_vector_deferred(a.split_offsets + a.batch);
+    const ItemLane lead = load_item_lane(a, items > 0 ? item0 : a.num_tasks, lane);
+    row_table_from(a, lane, lens, t);
+    const bool ok = check_queue_part(a, t, so0, so1, uniform(so_last), bal_lds, lead, item0, items, lane);
+    if (lane == 0) a.bal_flags[blockIdx.x] = ok ? 1 : 0;
+  } else {
+    row_table(a, lane, t);
+  }
   const long T = t.total;
   long x = v * T / V;
   const long x1 = (v + 1) * T / V;
@@ -1850,6 +2087,67 @@ void balanced_decode_kernel(DecodeArgs a) {
     write_wave_state<Elem, 1, false>(a, st, qh0, 0, d, lane);
     x = pair0 + kBalPieceCost + t1;
   }
+
+}
+
+// The merge's answer for a queue other than the builder's (some decode workgroup's check
+// failed), for the G query heads of pair (row, kvh), by one wave.  The reference's result
+// for such a queue (each slot of the row folded, a slot holding the state of the item that
+// writes it) is attention over the union of the row's items' tile ranges, with unwritten
+// slots taken as neutral as the per-item schedule takes the builder's empty splits.  The
+// wave scans the whole queue and streams the ranges of the pair's valid items (row and kv
+// head the pair's, split below the row's slot count, slot inside the workspace) in queue
+// order into one state, and writes the normalised output.  Slow (a pass over the queue
+// and a serial stream per pair), and only for queues other than the builder's; the fused
+// append's token is already in the pool (the decode wrote it).
+template <class Elem, int PG>
+__device__ void balanced_merge_fallback(const DecodeArgs& a, int row, int kvh, int out_row, int lane) {
+  const int len = uniform(clamp_length(a, a.seq_lens[row]));
+  const int T = ceil_tiles(len);
+  const int so0 = uniform(a.split_offsets[row]);
+  const int S = uniform(a.split_offsets[row + 1]) - so0;
+  const int G = a.group;
+  const int q_loaded = a.q_indices ? a.q_indices[row] : 0;
+  u32x4 qf[1][4];
+  load_q<1, PG == kPgFp8>(a, q_loaded, row, kvh * G, lane, qf);
+  WaveState<1> st;
+  init_state<1>(st);
+  for (long i0 = 0; T > 0 && i0 < a.num_tasks; i0 += 64) {
+    const ItemLane it = load_item_lane(a, i0, lane);
+    const int s = it.f[2];
+    const bool match = i0 + lane < a.num_tasks && it.f[0] == row && it.f[1] == kvh && s >= 0 &&
+                       s < S && (long)so0 + s >= 0 && (long)so0 + s < a.total_slots;
+    uint64_t hits = __builtin_amdgcn_ballot_w64(match);
+    while (hits) {
+      const int src = __builtin_ctzll(hits);
+      hits &= hits - 1;
+      const int ss = __builtin_amdgcn_readlane(s, src);
+      long tb = __builtin_amdgcn_readlane(it.f[3], src), te = __builtin_amdgcn_readlane(it.f[4], src);
+      if (tb < 0) tb = (long)T * ss / S;
+      if (te < 0) te = (long)T * (ss + 1) / S;
+      const int t0 = uniform((int)(tb < 0 ? 0 : tb)), t1 = uniform((int)(te > T ? T : te));
+      if (t1 > t0) stream_tiles<Elem, 1, PG, 2>(a, st, qf, row, kvh, t0, t1, len, lane);
+    }
+  }
+  finish_state<1>(st);
+  const Dest d{nullptr, nullptr, nullptr, 0, 1, false};
+  write_wave_state<Elem, 1, true>(a, st, kvh * G, out_row, d, lane);
+}
+
+// Whether every decode workgroup's part of the queue check passed (bal_flags[0, n)), by
+// one wave: 16-byte loads, all issued together for up to 1024 workgroups.
+__device__ inline bool queue_checks_passed(const DecodeArgs& a, int n, int lane) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+      uniform_ptr(a.bal_flags), (short)0, uniform(n * 4), kRsrcWord3);
+  bool ok = true;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    if (k * 256 >= n) break;
+    const u32x4 f = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (k * 64 + lane) * 16, 0, 0));
+#pragma unroll
+    for (int q = 0; q < 4; ++q) ok = ok && (k * 256 + lane * 4 + q >= n || f[q] == 1);
+  }
+  return __builtin_amdgcn_ballot_w64(!ok) == 0;
 }
 
 // Merge of the balanced schedule: one workgroup of nw = blockDim.x / 64 waves (1, 2 or
@@ -1861,8 +2159,9 @@ void balanced_decode_kernel(DecodeArgs a) {
 // the wide fold).
 constexpr int kBalMergeWaves = 4;
 
-template <class Elem, bool WIDE>
-__global__ __launch_bounds__(kBalMergeWaves * 64) void balanced_merge_kernel(DecodeArgs a, int waves) {
+template <class Elem, bool WIDE, int PG>
+__global__ __launch_bounds__(kBalMergeWaves * 64) void balanced_merge_kernel(DecodeArgs a, int waves,
+                                                                             int check_wgs) {
   __shared__ float sm_ml[kBalMergeWaves][2];
   __shared__ f32x2 sm_a[kBalMergeWaves][64];
   const int lane = threadIdx.x & 63;
@@ -1881,6 +2180,15 @@ __global__ __launch_bounds__(kBalMergeWaves * 64) void balanced_merge_kernel(Dec
       uniform_ptr(a.bal_plan + ((long)row * a.hkv + kvh) * 4), (short)0, a.bal_plan ? 16 : 0,
       kRsrcWord3);  // a null plan reads zeros
   const u32x4 plan = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, 0, 0, 0));
+  // The decode's queue check, in the same round trip.  A queue other than the builder's is
+  // computed here instead, pair by pair, by the first query head's workgroup.
+  if (!queue_checks_passed(a, check_wgs, lane)) {
+    if (h == 0 && wave == 0) {
+      const int out_row = a.out_indices ? uniform(out_row_loaded) : row;
+      balanced_merge_fallback<Elem, PG>(a, row, kvh, out_row, lane);
+    }
+    return;
+  }
   // Selected, not branched on, so that the plan load is issued beside the length load.
   // Clamped so that the state loads stay inside the workspace whatever it holds.
   int va = uniform((int)plan[0]);
@@ -2447,6 +2755,8 @@ MergeArgs queue_merge_args(const DecodeArgs& a) {
   m.hq = a.hq;
   m.out_rows = a.out_rows;
   m.total_slots = a.total_slots;
+  m.num_tasks = a.num_tasks;
+  m.hkv = a.hkv;
   m.max_tokens = (int)((long)a.max_pages * a.page_size > 0x7fffffffL ? 0x7fffffff
                                                                      : (long)a.max_pages * a.page_size);
   return m;
@@ -2472,13 +2782,18 @@ int run_indexed(const Geometry& g, const void* q_source, int32_t q_rows, const v
 // the workspace cannot hold (batch * Hkv + waves) * G partial states and the plan.  PKV_BALANCED=0
 // keeps every call on the per-item schedule (tuning).
 // Layout of the balanced schedule's workspace: (pairs + waves) * G partial states (m, l,
-// acc), then at the next 16-byte boundary one 16-byte plan entry per (row, kv head) pair.
+// acc), rounded up to an even count so that acc, at 8 bytes per state, starts on a 16-byte
+// boundary (the merge reads it with 16-byte loads); then one 16-byte plan entry per
+// (row, kv head) pair; then one int per decode workgroup, its part of the queue check.
+long balanced_states(long pairs, long waves, int G) { return ((pairs + waves) * G + 1) & ~1L; }
 size_t balanced_plan_offset(long pairs, long waves, int G) {
-  const size_t states = (size_t)((pairs + waves) * G) * (kD + 2) * sizeof(float);
-  return (states + 15) & ~(size_t)15;
+  return (size_t)balanced_states(pairs, waves, G) * (kD + 2) * sizeof(float);
+}
+size_t balanced_flags_offset(long pairs, long waves, int G) {
+  return balanced_plan_offset(pairs, waves, G) + (size_t)pairs * 16;
 }
 size_t balanced_bytes(long pairs, long waves, int G) {
-  return balanced_plan_offset(pairs, waves, G) + (size_t)pairs * 16;
+  return balanced_flags_offset(pairs, waves, G) + (size_t)(waves / kBalWaves) * sizeof(int32_t);
 }
 
 int balanced_waves(const Geometry& g, size_t ws_bytes, int fused_merge) {
@@ -2516,11 +2831,13 @@ int run_workqueue(const QueueCall& c, int32_t fused_merge, hipStream_t stream, c
   }
   if (waves > 0) {
     const long pairs = (long)c.g.batch * c.g.hkv;
-    const long states = (pairs + waves) * a.group;
+    const long states = balanced_states(pairs, waves, a.group);
     a.part_m = (float*)c.ws;
     a.part_l = a.part_m + states;
     a.part_acc = a.part_l + states;
     a.bal_plan = (int32_t*)((uint8_t*)c.ws + balanced_plan_offset(pairs, waves, a.group));
+    a.bal_flags = (int32_t*)((uint8_t*)c.ws + balanced_flags_offset(pairs, waves, a.group));
+    const int check_wgs = waves / kBalWaves;
     hipError_t e = hipSuccess;
     if (stages & 1) {
       // 96 KB of LDS per workgroup keeps one workgroup on each CU.
@@ -2550,12 +2867,22 @@ int run_workqueue(const QueueCall& c, int32_t fused_merge, hipStream_t stream, c
       // merge wave's share can exceed one chunk: few pairs per merge wave.
       const bool wide = (long)c.g.batch * c.g.hkv * merge_waves * kMergeChunk < waves;
       const bool bf = c.g.dtype == PKV_DTYPE_BF16;
-      if (wide) {
-        if (bf) balanced_merge_kernel<BFloat, true><<<grid, block, 0, stream>>>(a, waves);
-        else balanced_merge_kernel<Half, true><<<grid, block, 0, stream>>>(a, waves);
+      // The pager of the merge's fallback: fp8 pages, else 2-byte pages (with the fused
+      // append the decode has already written the new token).
+      if (a.kv_fp8) {
+        if (wide) {
+          if (bf) balanced_merge_kernel<BFloat, true, kPgFp8><<<grid, block, 0, stream>>>(a, waves, check_wgs);
+          else balanced_merge_kernel<Half, true, kPgFp8><<<grid, block, 0, stream>>>(a, waves, check_wgs);
+        } else {
+          if (bf) balanced_merge_kernel<BFloat, false, kPgFp8><<<grid, block, 0, stream>>>(a, waves, check_wgs);
+          else balanced_merge_kernel<Half, false, kPgFp8><<<grid, block, 0, stream>>>(a, waves, check_wgs);
+        }
+      } else if (wide) {
+        if (bf) balanced_merge_kernel<BFloat, true, kPgFast><<<grid, block, 0, stream>>>(a, waves, check_wgs);
+        else balanced_merge_kernel<Half, true, kPgFast><<<grid, block, 0, stream>>>(a, waves, check_wgs);
       } else {
-        if (bf) balanced_merge_kernel<BFloat, false><<<grid, block, 0, stream>>>(a, waves);
-        else balanced_merge_kernel<Half, false><<<grid, block, 0, stream>>>(a, waves);
+        if (bf) balanced_merge_kernel<BFloat, false, kPgFast><<<grid, block, 0, stream>>>(a, waves, check_wgs);
+        else balanced_merge_kernel<Half, false, kPgFast><<<grid, block, 0, stream>>>(a, waves, check_wgs);
       }
       e = hipGetLastError();
       if (e != hipSuccess) return fail(PKV_ERR_LAUNCH, "merge launch failed: %s", hipGetErrorString(e));
@@ -2951,11 +3278,13 @@ int pkv_workqueue_decode_fp8(const void* q_source, int32_t q_rows, const void* k
 int pkv_workqueue_merge(const int32_t* seq_lens, const int32_t* split_offsets,
                         const int32_t* out_indices, void* output, int32_t out_rows,
                         const void* workspace, size_t workspace_bytes, int32_t batch,
-                        int32_t num_q_heads, int32_t total_partial_slots, int32_t dtype,
-                        void* stream) {
+                        int32_t num_q_heads, int32_t total_partial_slots, int32_t num_tasks,
+                        int32_t num_kv_heads, int32_t dtype, void* stream) {
   if (dtype != PKV_DTYPE_F16 && dtype != PKV_DTYPE_BF16)
     return fail(PKV_ERR_UNSUPPORTED, "dtype must be fp16 or bf16");
   if (batch < 0 || num_q_heads <= 0) return fail(PKV_ERR_INVALID_ARGUMENT, "bad batch or head count");
+  if (num_tasks >= 0 && num_kv_heads <= 0)
+    return fail(PKV_ERR_INVALID_ARGUMENT, "num_kv_heads must be positive when num_tasks is given");
   if (total_partial_slots <= 0)
     return fail(PKV_ERR_INVALID_ARGUMENT, "total_partial_slots must be positive");
   if (batch > 0 && (!seq_lens || !split_offsets || !output || out_rows <= 0))
@@ -2979,6 +3308,8 @@ int pkv_workqueue_merge(const int32_t* seq_lens, const int32_t* split_offsets,
   m.out_rows = out_rows;
   m.total_slots = total_partial_slots;
   m.max_tokens = 0x7fffffff;
+  m.num_tasks = num_tasks < 0 ? -1 : num_tasks;
+  m.hkv = num_kv_heads;
   const int st = dispatch_merge(m, true, dtype, (hipStream_t)stream);
   return st == PKV_OK ? ok() : st;
 }

@@ -546,7 +546,8 @@ void persistentkv_workqueue_decode_fp8(torch::Tensor q_source, torch::Tensor k_p
 // Stage 2 of the work-queue op: the segmented LSE merge alone.
 void persistentkv_workqueue_merge(torch::Tensor seq_lens, torch::Tensor split_offsets,
                                   torch::Tensor out_indices, torch::Tensor output,
-                                  torch::Tensor workspace, int64_t total_partial_slots) {
+                                  torch::Tensor workspace, int64_t total_partial_slots,
+                                  int64_t num_tasks, int64_t num_kv_heads) {
   const auto dt = activation_dtype(output, "output");
   check_tensor(seq_lens, "seq_lens", at::kInt, 1);
   check_tensor(split_offsets, "split_offsets", at::kInt, 1);
@@ -562,7 +563,8 @@ void persistentkv_workqueue_merge(torch::Tensor seq_lens, torch::Tensor split_of
       seq_lens.data_ptr<int>(), split_offsets.data_ptr<int>(), out_indices.data_ptr<int>(),
       output.data_ptr(), i32(output.size(0), "output.size(0)"), ws_ptr(workspace),
       ws_bytes(workspace), B, i32(output.size(1), "output.size(1)"),
-      i32(total_partial_slots, "total_partial_slots"), pkv_dtype_of(dt), stream_of(output)));
+      i32(total_partial_slots, "total_partial_slots"), i32(num_tasks, "num_tasks"),
+      i32(num_kv_heads, "num_kv_heads"), pkv_dtype_of(dt), stream_of(output)));
 }
 
 namespace {
@@ -740,7 +742,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("workqueue_decode", &persistentkv_workqueue_decode,
         "Work-queue decode stage only (partial states into the workspace)");
   m.def("workqueue_merge", &persistentkv_workqueue_merge,
-        "Work-queue segmented LSE merge stage only");
+        "Work-queue segmented LSE merge stage only (num_tasks = work_items.size(0), or -1 "
+        "for a builder queue of unknown size)",
+        py::arg("seq_lens"), py::arg("split_offsets"), py::arg("out_indices"), py::arg("output"),
+        py::arg("workspace"), py::arg("total_partial_slots"), py::arg("num_tasks") = -1,
+        py::arg("num_kv_heads") = 0);
   m.def("paged_attention_indexed_fp8", &persistentkv_paged_attention_indexed_fp8,
         "paged_attention_indexed over fp8 (e4m3) K/V pages with per-tensor scales");
   m.def("paged_attention_workqueue_fp8", &persistentkv_paged_attention_workqueue_fp8,

@@ -72,6 +72,9 @@ CASES = [
     ([30000 if i % 36 == 0 else 100 + 7 * i for i in range(72)], 32, 8, 16, 2, F16),
     # 2 rows x 2 kv heads: pairs over hundreds of waves, folded by the wide merge
     ([30000, 9000], 16, 2, 16, 5, BF16),
+    # G = 1 with an odd number of pairs: (pairs + waves) x G states is odd, padded to even
+    # so that the states' acc (read with 16-byte loads by the wide fold) stays aligned
+    ([3000, 500, 9000], 1, 1, 16, 4, F16),
 ]
 
 

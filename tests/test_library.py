@@ -22,20 +22,6 @@ def test_library_exports_every_header_function():
     assert not missing, missing
 
 
-def test_probe_library_is_separate():
-    """The HBM probes (include/pkv_probe.h) live in libpkv_probe.so, not in the engine."""
-    import os
-    probe_header = os.path.join(os.path.dirname(pkv_native.HEADER_PATH), "pkv_probe.h")
-    names = pkv_native.header_functions(probe_header)
-    assert set(names) == {"pkv_probe_read", "pkv_probe_copy", "pkv_probe_read_cus",
-                          "pkv_probe_read_inflight"}
-    probe = ctypes.CDLL(os.path.join(os.path.dirname(pkv_native.LIBRARY_PATH), "libpkv_probe.so"))
-    assert all(hasattr(probe, n) for n in names)
-    engine = pkv_native.lib()
-    assert not any(hasattr(engine, n) for n in names)
-    assert not any(n.startswith("pkv_probe") for n in pkv_native.header_functions())
-
-
 def test_op_module_surface():
     import persistentkv_torch_ext as ext
     for name in ("paged_attention", "paged_attention_masked", "paged_attention_indexed",
@@ -76,10 +62,11 @@ def test_workspace_sizes():
     assert pkv_native.split_workspace_bytes(1, 32, 8, 1024, 16) == ref(1, 32, 16)   # 32 tiles only
     assert pkv_native.split_workspace_bytes(8, 32, 32, 4096, 8) == ref(8, 32, 8)    # 2048 units
     assert pkv_native.split_workspace_bytes(1, 32, 8, 8192, 1) == 0                 # direct launch
-    # the balanced work-queue schedule: (B*Hkv + 4 waves x CUs) groups of G states
-    # states of (pairs + waves) * G heads, then one 16-byte plan entry per pair
-    assert pkv_native.workqueue_balanced_workspace_bytes(8, 32, 8) == (8 * 8 + 4 * 256) * 4 * 130 * 4 + 8 * 8 * 16
-    assert pkv_native.workqueue_balanced_workspace_bytes(3, 3, 1) == -(-(3 + 4 * 256) * 3 * 520 // 16) * 16 + 3 * 16
+    # the balanced work-queue schedule: (B*Hkv + 4 waves x CUs) groups of G states, the
+    # state count rounded up to even (acc 16-byte aligned), then one 16-byte plan entry per
+    # pair, then one queue-check flag per decode workgroup (one per CU)
+    assert pkv_native.workqueue_balanced_workspace_bytes(8, 32, 8) == (8 * 8 + 4 * 256) * 4 * 520 + 8 * 8 * 16 + 256 * 4
+    assert pkv_native.workqueue_balanced_workspace_bytes(3, 3, 1) == ((3 + 4 * 256) * 3 + 1) * 520 + 3 * 16 + 256 * 4
     assert pkv_native.workqueue_balanced_workspace_bytes(8, 32, 1) == 0    # G = 32: never taken
     assert pkv_native.workqueue_balanced_workspace_bytes(257, 32, 8) == 0  # more than 256 rows
 
