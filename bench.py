@@ -49,8 +49,19 @@ WORKLOAD_NAMES = {"c1": "c1_b1_ctx2048_direct", "c2": "c2_b8_mha_split8",
                   "smoke_g4_8k": "smoke_b1_g4_n8192_contiguous_split16",
                   "smoke_g4_32k": "smoke_b1_g4_n32768_contiguous_split16"}
 # Published figures of the reference for the same metric and configuration (RTX 3060,
-# 360 GB/s peak): results/smoke_test.txt:25 and :27.
+# 360 GB/s peak): results/smoke_test.txt:25 and :27, and every row of its sweep (:23-43).
 PUBLISHED_GBPS = {"smoke_g4_8k": 237.1, "smoke_g4_32k": 238.6}
+SWEEP = {}  # sweep workload name -> published GB/s (filled from pkv_workloads.SMOKE_SWEEP)
+
+
+def _sweep_table():
+    import pkv_workloads as wl
+    for b, hq, hkv, n, splits, gbps in wl.SMOKE_SWEEP:
+        for paged in (False, True):
+            SWEEP[wl.sweep_name(b, hq, hkv, n, splits, paged)] = gbps
+
+
+_sweep_table()
 HBM_PEAK_GBPS = 8000.0
 MALL_BYTES = 256 * 2 ** 20  # MI355X Infinity Cache
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "c4_decode_traffic.json")
@@ -64,9 +75,13 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--rotations", type=int, default=4,
                    help="minimum KV pool replicas (cold-cache basis; raised for small steps)")
-    p.add_argument("--workload", default="c4", choices=sorted(WORKLOAD_NAMES),
+    p.add_argument("--workload", default="c4", choices=sorted(WORKLOAD_NAMES) + sorted(SWEEP),
                    help="configuration (default c4, the headline; the others are reported "
                         "for the design notes and are not the metric)")
+    p.add_argument("--sweep", action="store_true",
+                   help="run the reference's performance sweep (tests/smoke_test.cu:502-521) "
+                        "over contiguous and paged K/V, one JSON line per row, each beside "
+                        "the reference's published GB/s (no CPU baseline)")
     p.add_argument("--fused-merge", action="store_true", help="single-launch fused merge variant")
     p.add_argument("--kv-fp8", action="store_true",
                    help="K/V pages in fp8 (OCP e4m3) with per-tensor scales (work-queue and "
@@ -155,7 +170,16 @@ def main():
     if args.steps <= 0:
         print("--steps must be positive", file=sys.stderr)
         sys.exit(2)
+    if args.sweep:
+        for name in SWEEP:
+            result = run_workload(args, name)
+            print(json.dumps(result), flush=True)
+    else:
+        print(json.dumps(run_workload(args, args.workload)), flush=True)
 
+
+def run_workload(args, workload):
+    """Measures one workload and returns its JSON object."""
     import torch
 
     import persistentkv_torch_ext as ext
@@ -163,7 +187,7 @@ def main():
     import pkv_workloads as wl
 
     dev = torch.device("cuda:0")
-    w = wl.CONFIGS[args.workload](seed=args.seed)
+    w = wl.CONFIGS[workload](seed=args.seed)
     w.fused_merge = args.fused_merge
     w.kv_fp8 = args.kv_fp8
     if w.kv_fp8 and w.op not in ("paged_attention_workqueue", "paged_attention_indexed"):
@@ -219,7 +243,7 @@ def main():
     gate = serving.gate_step(gate_out, metas[gate_i], q_pool[gate_i], gate_k, gate_v, w.page_size)
     gate["step"] = gate_i
     if not gate["pass"]:
-        print(f"correctness gate failed at trace step {gate_i}: {gate}", file=sys.stderr)
+        print(f"correctness gate failed at trace step {gate_i} of {workload}: {gate}", file=sys.stderr)
         sys.exit(1)
     del gate_k, gate_v
 
@@ -303,7 +327,12 @@ def main():
     torch.cuda.synchronize()
     batched_us = b0.elapsed_time(b1) * 1e3 / args.steps
     merge_us = None
-    if queue:  # stage 2 (the merge) alone, back to back over the same sample
+    if queue:
+        # Stage 2 (the merge) after its own stage 1, over the same sample: each merge reads
+        # the partial states and plan entries its decode wrote.  Launched one by one from
+        # Python, a merge of a few microseconds waits on the host's launch rate, so the
+        # (decode, merge) pairs and the decodes alone are each replayed from one HIP graph,
+        # and the merge's time is the difference.
         def merge_stage(k):
             i = sample[k]
             m = metas[i]
@@ -313,25 +342,35 @@ def main():
                                                 m.out_indices, m.output, ws, m.bucket_length,
                                                 w.page_size, m.total_partial_slots, w.kv_fp8,
                                                 w.k_scale, w.v_scale)
-        # Launched one by one from Python, a merge of a few microseconds waits on the host's
-        # launch rate; the same launches replayed from one HIP graph time the GPU alone.
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.stream(side):
-            merge_stage(0)
-            with torch.cuda.graph(graph, stream=side):
-                for k in range(args.steps):
-                    merge_stage(k)
-        torch.cuda.synchronize()
-        graph.replay()
-        torch.cuda.synchronize()
-        m0, m1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        m0.record()
-        graph.replay()
-        m1.record()
-        torch.cuda.synchronize()
-        merge_us = m0.elapsed_time(m1) * 1e3 / args.steps
+
+        def graph_us(body):
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(side):
+                body()
+                with torch.cuda.graph(g, stream=side):
+                    body()
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) * 1e3 / args.steps
+
+        def pairs():
+            for k in range(args.steps):
+                launch(k)
+                merge_stage(k)
+
+        def decodes():
+            for k in range(args.steps):
+                launch(k)
+
+        merge_us = graph_us(pairs) - graph_us(decodes)
     # Roofline numerator over the back-to-back launches: event packets between launches
     # add a few microseconds that are not kernel time (rocprofv3's kernel-trace average
     # duration matches the back-to-back figure to about 1 %).
@@ -339,7 +378,7 @@ def main():
     achieved = total_bytes / (batched_us * 1e-6 * args.steps) / 1e9
     traffic, traffic_note = None, None
     traffic_file = TRAFFIC_FILE_FP8 if w.kv_fp8 else TRAFFIC_FILE
-    if args.workload == "c4" and queue and os.path.exists(traffic_file):
+    if workload == "c4" and queue and os.path.exists(traffic_file):
         with open(traffic_file) as fh:
             prof = json.load(fh)
         ratio = prof["hbm_bytes_per_launch"] / prof["algorithmic_bytes_per_launch"]
@@ -350,6 +389,7 @@ def main():
                         f"launches), scaled to this sample")
 
     value = total_bytes / (gpu_ms / 1e3) / 1e9
+    published = PUBLISHED_GBPS.get(workload, SWEEP.get(workload))
     kernel = {"paged_attention_workqueue": ("balanced_decode_kernel (stage 1 only)"
                                             if schedule == "balanced" else
                                             "decode_kernel<*,kQueue> (stage 1 only)"),
@@ -377,11 +417,10 @@ def main():
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBPS, 2),
         "higher_is_better": True,
         "scaling": "weak",
-        "vs_baseline": (round(value / PUBLISHED_GBPS[args.workload], 3)
-                        if args.workload in PUBLISHED_GBPS else None),
+        "vs_baseline": (round(value / published, 3) if published else None),
         "dtype": ("fp16" if w.dtype == torch.float16 else "bf16") + (" (fp8 e4m3 K/V)" if w.kv_fp8 else ""),
         "data": "synthetic",
-        "config": {"workload": WORKLOAD_NAMES[args.workload] + ("_fp8kv" if w.kv_fp8 else ""),
+        "config": {"workload": WORKLOAD_NAMES.get(workload, workload) + ("_fp8kv" if w.kv_fp8 else ""),
                    "requests": len(w.requests),
                    "max_active": max(len(s.active_ids) for s in w.steps),
                    "trace_steps": n_trace, "hq": w.hq, "hkv": w.hkv, "head_dim": 128,
@@ -394,9 +433,15 @@ def main():
                    "sample": sample_text,
                    "mean_kv_mb_per_step": round(mean_bytes / 1e6, 2),
                    "trace_mean_kv_mb_per_step": round(sum(m.kv_bytes for m in metas) / n_trace / 1e6, 2),
-                   "cache_basis": f"HBM-cold ({len(pools)} rotated KV pool replicas)"},
+                   "cache_basis": f"HBM-cold ({len(pools)} rotated KV pool replicas)",
+                   "workspace_bytes": ws.numel() * ws.element_size(),
+                   "workspace": ("this engine's size for its faster decomposition "
+                                 "(pkv_workqueue_balanced_workspace_bytes / "
+                                 "pkv_split_workspace_bytes / pkv_direct_workspace_bytes, at "
+                                 "least the reference's)")},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "step_frac": round(value / HBM_PEAK_GBPS, 4),
                      "traffic": traffic,
                      "traffic_source": traffic_note,
                      "kernel": kernel,
@@ -420,7 +465,7 @@ def main():
         base_us = c0.elapsed_time(c1) * 1e3 / n_base
         result["query_head_baseline"] = {"step_us": round(base_us, 2),
                                          "speedup": round(base_us / (gpu_ms * 1e3 / args.steps), 2)}
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and not args.sweep:
         q_cpu = q_pool.cpu()
         k_cpu, v_cpu = k0.cpu(), v0.cpu()
         if w.kv_fp8:  # the oracle attends to k_scale * e4m3(k8), v_scale * e4m3(v8)
@@ -428,7 +473,11 @@ def main():
             k_cpu = oracle.dequantize_e4m3(k_cpu, w.k_scale)
             v_cpu = oracle.dequantize_e4m3(v_cpu, w.v_scale)
         result["cpu_baseline"] = cpu_baseline(w, q_cpu, k_cpu, v_cpu, metas, args.cpu_seconds)
-    print(json.dumps(result), flush=True)
+    if published:
+        result["published_reference_gbps"] = {
+            "value": published, "hardware": "RTX 3060 (360 GB/s)",
+            "source": "results/smoke_test.txt (tests/smoke_test.cu bench_perf, contiguous K/V)"}
+    return result
 
 
 if __name__ == "__main__":

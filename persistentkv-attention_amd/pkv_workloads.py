@@ -13,7 +13,9 @@ measured on:
   c5  B=64 Zipf(1.1) lengths, G=32 or 8, bf16, page 32, cost-model splits (work queue)
 
 and the reference's contiguous-layout performance case (smoke_g4_8k, smoke_g4_32k: B=1,
-G=4, N 8192 / 32768, 16 splits, attention_contiguous; tests/smoke_test.cu:313-395).
+G=4, N 8192 / 32768, 16 splits, attention_contiguous; tests/smoke_test.cu:313-395), with
+the whole sweep of that benchmark (SMOKE_SWEEP, :502-521: context, batch and G sweeps) over
+contiguous and paged K/V.
 
 Per-step metadata comes from the C++ builder in libpkv.so (pkv_native.build_workqueue);
 random values come from torch generators with the reference's seed offsets (pages +99,
@@ -299,11 +301,56 @@ def config_smoke(context, seed=DEFAULT_SEED, batch=1, hq=32, hkv=8, splits=16):
                     context, torch.float16, seed, reqs, [step], batch, splits=splits)
 
 
+def config_smoke_paged(context, seed=DEFAULT_SEED, batch=1, hq=32, hkv=8, splits=16, page_size=16):
+    """config_smoke over a paged pool: each of the B rows holds N tokens in pages of
+    ``page_size`` drawn by a seeded permutation of a pool 1.5x the used pages, run through
+    ``paged_attention`` (every row attends to N tokens) with the same split count."""
+    pages = -(-context // page_size)
+    physical = math.ceil(1.5 * pages * batch)
+    ids = torch.randperm(physical, generator=torch.Generator().manual_seed(seed + 99)).tolist()
+    reqs = [Request(i, 0, context, 1, tuple(int(x) for x in ids[i * pages:(i + 1) * pages]))
+            for i in range(batch)]
+    step = StepState(0, tuple(range(batch)), (context,) * batch)
+    return Workload(f"smoke_g{hq // hkv}_{context // 1024}k_paged", "paged_attention", hq, hkv,
+                    page_size, torch.float16, seed, reqs, [step], physical, splits=splits)
+
+
+# The reference's performance sweep (tests/smoke_test.cu:502-521, contiguous K/V through
+# persistentkv_split_dispatch) with its published bandwidth on an RTX 3060
+# (results/smoke_test.txt:23-43): (B, Hq, Hkv, N, splits, GB/s).
+SMOKE_SWEEP = [
+    (1, 32, 8, 4096, 16, 221.9), (1, 32, 8, 8192, 16, 237.1), (1, 32, 8, 16384, 16, 236.3),
+    (1, 32, 8, 32768, 16, 238.6),                                  # GQA, G = 4
+    (1, 8, 1, 4096, 128, 33.4), (1, 8, 1, 8192, 128, 47.0),        # MQA-like, G = 8
+    (1, 32, 8, 8192, 16, 237.4), (2, 32, 8, 8192, 8, 247.0), (4, 32, 8, 8192, 4, 241.7),
+    (8, 32, 8, 8192, 2, 229.5),                                    # batch sweep
+    (1, 4, 4, 8192, 32, 101.7), (1, 8, 4, 8192, 32, 100.0), (1, 16, 4, 8192, 32, 196.3),
+    (1, 32, 4, 8192, 32, 55.2),                                    # G sweep (1, 2, 4, 8)
+]
+
+
+def sweep_name(b, hq, hkv, n, splits, paged=False):
+    return f"sweep_b{b}_hq{hq}_hkv{hkv}_n{n}_s{splits}" + ("_paged" if paged else "")
+
+
+def sweep_configs():
+    """Workload factories of SMOKE_SWEEP, contiguous and paged, by name."""
+    out = {}
+    for b, hq, hkv, n, splits, _ in SMOKE_SWEEP:
+        for paged in (False, True):
+            make = config_smoke_paged if paged else config_smoke
+            out[sweep_name(b, hq, hkv, n, splits, paged)] = (
+                lambda make=make, b=b, hq=hq, hkv=hkv, n=n, s=splits, **kw:
+                make(n, batch=b, hq=hq, hkv=hkv, splits=s, **kw))
+    return out
+
+
 CONFIGS = {"c1": config_c1, "c2": config_c2, "c3": config_c3,
            "c3_32k": lambda **kw: config_c3(first_bucket=32768, **kw), "c4": config_c4,
            "c5_g32": lambda **kw: config_c5(hkv=1, **kw), "c5_g8": lambda **kw: config_c5(hkv=4, **kw),
            "smoke_g4_8k": lambda **kw: config_smoke(8192, **kw),
-           "smoke_g4_32k": lambda **kw: config_smoke(32768, **kw)}
+           "smoke_g4_32k": lambda **kw: config_smoke(32768, **kw),
+           **sweep_configs()}
 
 
 # ---------------------------------------------------------------------------------

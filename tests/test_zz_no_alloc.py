@@ -1,7 +1,8 @@
 """pkv_paged_attention_workqueue_noalloc (static scratch, no workspace argument) through the
 C ABI against pkv_paged_attention_workqueue with a caller workspace: identical outputs, bit
 for bit, on two calls in a row (the second with a smaller input), for the two-launch and
-the fused merge; and a request beyond the 16 MiB scratch is rejected before any launch."""
+the fused merge, and for the balanced schedule; and a request beyond the 16 MiB scratch
+is rejected before any launch."""
 import ctypes
 
 import pytest
@@ -62,6 +63,23 @@ def test_noalloc_equals_workspace_entry_on_two_calls(lib, gpu, fused):
         case = make_case(lengths, 32, hkv, 16, torch.float16, seed=seed)
         ref = _call(lib, case, lengths, hkv, splits, fused, gpu, workspace=True)
         got = _call(lib, case, lengths, hkv, splits, fused, gpu, workspace=False)
+        assert torch.isfinite(got).all()
+        assert torch.equal(got, ref)
+
+
+def test_noalloc_balanced_schedule_on_two_calls(lib, gpu):
+    """A C4-sized queue (8 rows x 8 KV heads, G = 4, 20 splits: 2.66 MB of reference-sized
+    states, which hold the balanced schedule's states, plan entries and check flags) takes
+    the balanced schedule in the static scratch too; then a smaller one."""
+    calls = [([20000, 300, 700, 1, 5000, 64, 31000, 513], 8, 20, 5), ([900, 4000], 8, 3, 6)]
+    for i, (lengths, hkv, splits, seed) in enumerate(calls):
+        meta = pkv_native.build_workqueue(lengths, list(range(len(lengths))),
+                                          [[0]] * len(lengths), 16, splits, False, hkv)
+        ws_bytes = meta["total_partial_slots"] * 32 * 130 * 4
+        assert pkv_native.workqueue_schedule(len(lengths), 32, hkv, 16, ws_bytes) == (1 if i == 0 else 0)
+        case = make_case(lengths, 32, hkv, 16, torch.float16, seed=seed)
+        ref = _call(lib, case, lengths, hkv, splits, False, gpu, workspace=True)
+        got = _call(lib, case, lengths, hkv, splits, False, gpu, workspace=False)
         assert torch.isfinite(got).all()
         assert torch.equal(got, ref)
 
