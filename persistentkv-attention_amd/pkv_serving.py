@@ -32,7 +32,12 @@ Differences from the reference, on purpose:
 
 Command line (GPU):  python pkv_serving.py --workload c4 [--workload c3_32k ...]
                       [--engines bucket workqueue adaptive] [--repeats 1] [--kv-fp8]
-                      [--json F] [--md F]
+                      [--graph] [--json F] [--md F]
+A trace of the reference's harness, with its options and defaults:
+                     python pkv_serving.py --trace bimodal --requests 24 --max-active 8
+                      --steps 48 --hole-fraction 0.0 --seed 20260623 --workqueue-splits 20
+                      [--trace-file F] [--page-size 16] [--hkv 8] [--bucket-tokens 0]
+                      [--bucket-splits 32] [--rotations 1] [--graph]
 """
 from __future__ import annotations
 
@@ -233,16 +238,17 @@ class Engine:
                    the MI355X split planner
     """
 
-    def __init__(self, name, w, device):
+    def __init__(self, name, w, device, splits=None, bucket_tokens=0):
         self.name, self.w, self.device = name, w, device
         n = len(w.steps)
         self.routes = []
         self.meta = []
+        fixed = w.splits if splits is None else splits
         for i in range(n):
             if name == "bucket":
-                route, splits = "persistentkv_bucket", w.splits
+                route, splits = "persistentkv_bucket", fixed
             elif name == "workqueue":
-                route, splits = "persistentkv_workqueue", w.splits
+                route, splits = "persistentkv_workqueue", fixed
             elif name == "adaptive":
                 route, splits, _ = pkv_native.choose_adaptive_route(list(w.steps[i].lengths),
                                                                     mi355x_model(w))
@@ -250,20 +256,21 @@ class Engine:
                 raise ValueError(f"unknown engine {name}")
             self.routes.append((route, splits))
             if route == "persistentkv_workqueue":
+                saved = (w.splits, w.auto_splits, w.policy)
                 if name == "adaptive":
-                    saved = (w.splits, w.auto_splits, w.policy)
                     w.splits, w.auto_splits, w.policy = 1, True, pkv_native.POLICY_MI355X
-                    m = _queue_step(w, i, device)
-                    w.splits, w.auto_splits, w.policy = saved
                 else:
-                    m = _queue_step(w, i, device)
+                    w.splits = fixed
+                m = _queue_step(w, i, device)
+                w.splits, w.auto_splits, w.policy = saved
                 self.meta.append(("queue", m))
             else:
                 if name == "adaptive":
-                    step = compile_bucket_step(w, i, device, splits, single_bucket=True)
+                    step = compile_bucket_step(w, i, device, splits, single_bucket=True,
+                                               bucket_tokens=bucket_tokens)
                 else:
-                    step = compile_bucket_step(w, i, device, w.splits, auto_splits=w.auto_splits,
-                                               policy=w.policy)
+                    step = compile_bucket_step(w, i, device, fixed, auto_splits=w.auto_splits,
+                                               bucket_tokens=bucket_tokens, policy=w.policy)
                 self.meta.append(("bucket", step))
         queue_metas = [m for kind, m in self.meta if kind == "queue"]
         bucket_steps = [m for kind, m in self.meta if kind == "bucket"]
@@ -419,9 +426,17 @@ def benchmark_engine(step_fn, w, warmup_steps, repeats):
 # ---------------------------------------------------------------------------------
 # Driver.
 # ---------------------------------------------------------------------------------
-def run_workload(ext, name, engines, repeats, warmup, rotations, device, seed, kv_fp8=False):
-    w = wl.CONFIGS[name](seed=seed)
+def run_workload(ext, name, engines, repeats, warmup, rotations, device, seed, kv_fp8=False,
+                 w=None, engine_splits=None, bucket_tokens=0, graph=False):
+    """Gates and times ``engines`` over a workload: a named configuration, or ``w`` (a
+    trace of the reference's harness, with ``engine_splits`` = {engine: split count} and
+    ``bucket_tokens`` as its --adaptive-*-splits and --bucket-tokens).  With ``graph``
+    each step is captured once into a HIP graph and replayed (the reference's
+    --pkv-cuda-graph, :1439-1452)."""
+    if w is None:
+        w = wl.CONFIGS[name](seed=seed)
     w.kv_fp8 = kv_fp8
+    engine_splits = engine_splits or {}
     q_pool = wl.make_q_pool(w, device)
     k0, v0 = wl.make_kv_pool(w, device)
     pools = [(k0, v0)] + [(k0.clone(), v0.clone()) for _ in range(max(1, rotations) - 1)]
@@ -431,9 +446,16 @@ def run_workload(ext, name, engines, repeats, warmup, rotations, device, seed, k
               "requests": len(w.requests), "repeats": repeats,
               "active_mean": statistics.mean(len(s.active_ids) for s in w.steps),
               "useful_kv_mb_per_step": statistics.mean(_mb(w.kv_bytes(i)) for i in range(len(w.steps))),
-              "cache_basis": f"{len(pools)} KV pool replica(s) rotated per step", "engines": {}}
+              "cache_basis": f"{len(pools)} KV pool replica(s) rotated per step",
+              "launch": "hip graph per step" if graph else "eager", "engines": {}}
+    if w.extra.get("trace") is not None:
+        report["trace"] = {k: w.extra[k] for k in ("trace", "max_active", "hole_fraction",
+                                                   "bucket_tokens", "trace_file")}
+        report["trace"]["seed"] = w.seed
+        report["physical_pages"] = w.physical_pages
     for name_e in engines:
-        eng = Engine(name_e, w, device)
+        eng = Engine(name_e, w, device, splits=engine_splits.get(name_e),
+                     bucket_tokens=bucket_tokens)
         gi = len(w.steps) // 2
         out = eng.run(ext, gi, q_pool, k0, v0).clone()
         torch.cuda.synchronize()
@@ -445,12 +467,31 @@ def run_workload(ext, name, engines, repeats, warmup, rotations, device, seed, k
         if not gate["pass"]:
             raise SystemExit(f"{name}/{name_e}: correctness gate failed at step {gi}: {gate}")
 
-        def step_fn(k, i):
-            kp, vp = pools[k % len(pools)]
-            eng.run(ext, i, q_pool, kp, vp)
+        if graph:
+            # One graph per trace step, each over the pool replica the step's first timed
+            # call would use (warm-up runs first, outside capture).
+            graphs = []
+            for i in range(len(w.steps)):
+                kp, vp = pools[i % len(pools)]
+                eng.run(ext, i, q_pool, kp, vp)
+                torch.cuda.synchronize()
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    eng.run(ext, i, q_pool, kp, vp)
+                graphs.append(g)
+            torch.cuda.synchronize()
+
+            def step_fn(k, i):
+                graphs[i].replay()
+        else:
+            def step_fn(k, i):
+                kp, vp = pools[k % len(pools)]
+                eng.run(ext, i, q_pool, kp, vp)
         stats = benchmark_engine(step_fn, w, warmup, repeats)
         report["engines"][name_e] = {"stats": stats, "profile": engine_profile(eng, w.fused_merge),
                                      "gate": gate}
+        if graph:
+            del graphs
         print(f"{name:8s} {name_e:10s} event mean {stats['event_mean_ms'] * 1e3:8.1f} us "
               f"p95 {stats['event_p95_ms'] * 1e3:8.1f} us  {stats['event_tokens_s']:10.0f} tok/s  "
               f"gate max {gate['max_abs']:.2e}", flush=True)
@@ -461,10 +502,17 @@ def run_workload(ext, name, engines, repeats, warmup, rotations, device, seed, k
 def markdown(reports):
     lines = []
     for r in reports:
-        lines += [f"### {r['workload']}  (Hq {r['hq']} / Hkv {r['hkv']}, page {r['page_size']}, "
+        tr = r.get("trace")
+        head = r["workload"]
+        if tr:
+            head = (f"trace={tr['trace'] if not tr['trace_file'] else tr['trace_file']} "
+                    f"seed={tr['seed']} requests={r['requests']} max_active={tr['max_active']} "
+                    f"hole_fraction={tr['hole_fraction']:.2f} bucket_tokens={tr['bucket_tokens']} "
+                    f"physical_pages={r['physical_pages']}")
+        lines += [f"### {head}  (Hq {r['hq']} / Hkv {r['hkv']}, page {r['page_size']}, "
                   f"{r['dtype']}, {r['trace_steps']} steps x {r['repeats']}, mean active "
                   f"{r['active_mean']:.2f}, {r['useful_kv_mb_per_step']:.1f} MiB useful KV per "
-                  f"step, {r['cache_basis']})", "",
+                  f"step, {r['cache_basis']}, {r['launch']})", "",
                   "| Engine | GPU tokens/s | GPU mean step us | GPU p50 us | GPU p95 us | GPU p99 us "
                   "| Wall tokens/s | Wall mean us | Wall p95 us | KV GB/s (event) | gate max-abs |",
                   "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
@@ -493,13 +541,37 @@ def main(argv=None):
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--workload", action="append", choices=sorted(wl.CONFIGS),
                    help="configuration(s) to run (default: c1 c2 c3 c3_32k c4 c5_g8 c5_g32)")
+    # A trace of the reference's harness, with its options and defaults
+    # (benchmark_serving_trace.py:1114-1211); replaces --workload when given.
+    p.add_argument("--trace", choices=["uniform", "bimodal", "zipf", "bucketed", "homogeneous"])
+    p.add_argument("--trace-file", help="CSV/JSON request trace (prompt_len/prompt, "
+                                        "decode_len/decode, optional arrival/arrival_step)")
+    p.add_argument("--requests", type=int, default=24)
+    p.add_argument("--max-active", type=int, default=8)
+    p.add_argument("--steps", type=int, default=48)
+    p.add_argument("--hole-fraction", type=float, default=0.50)
+    p.add_argument("--page-size", type=int, choices=[16, 32, 64, 128], default=16)
+    p.add_argument("--hkv", type=int, default=8, choices=[1, 2, 4, 8, 16, 32],
+                   help="KV heads; Hq is 32, so G = 32 / hkv")
+    p.add_argument("--bucket-tokens", type=int, default=0,
+                   help="round the length-bucket route's lengths up to this many tokens")
+    p.add_argument("--bucket-splits", type=int, default=32,
+                   help="split count of the length-bucket engine (the reference's "
+                        "--adaptive-bucket-splits)")
+    p.add_argument("--workqueue-splits", type=int, default=24,
+                   help="split count of the work-queue engine (the reference's "
+                        "--adaptive-workqueue-splits)")
+    p.add_argument("--graph", action="store_true",
+                   help="capture each step in a HIP graph and replay it (--pkv-cuda-graph)")
     p.add_argument("--engines", nargs="+", default=["bucket", "workqueue", "adaptive"],
                    choices=["bucket", "workqueue", "adaptive"])
     p.add_argument("--repeats", type=int, default=1)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--rotations", type=int, default=4,
                    help="KV pool replicas rotated per step (1 reuses one pool, as the reference)")
-    p.add_argument("--seed", type=int, default=wl.DEFAULT_SEED)
+    p.add_argument("--seed", type=int, default=None,
+                   help="default: the configurations' seed, or 20260622 for a trace (the "
+                        "reference harness's default)")
     p.add_argument("--kv-fp8", action="store_true",
                    help="K/V pools in fp8 (OCP e4m3) with the workload's per-tensor scales; every "
                         "engine runs the *_fp8 ops and the gate uses the dequantised pages")
@@ -508,12 +580,23 @@ def main(argv=None):
     a = p.parse_args(argv)
     import persistentkv_torch_ext as ext
     device = torch.device("cuda:0")
-    names = a.workload or ["c1", "c2", "c3", "c3_32k", "c4", "c5_g8", "c5_g32"]
     reports = []
-    for name in names:
-        reports.append(run_workload(ext, name, a.engines, a.repeats, a.warmup, a.rotations,
-                                    device, a.seed, a.kv_fp8))
-        torch.cuda.empty_cache()
+    if a.trace or a.trace_file:
+        seed = 20260622 if a.seed is None else a.seed
+        w = wl.config_trace(a.trace or "bimodal", a.requests, a.max_active, a.steps, seed,
+                            a.hole_fraction, a.page_size, a.hkv, 32, a.workqueue_splits,
+                            a.bucket_tokens, a.trace_file)
+        splits = {"bucket": a.bucket_splits, "workqueue": a.workqueue_splits}
+        reports.append(run_workload(ext, w.name, a.engines, a.repeats, a.warmup, a.rotations,
+                                    device, seed, a.kv_fp8, w=w, engine_splits=splits,
+                                    bucket_tokens=a.bucket_tokens, graph=a.graph))
+    else:
+        names = a.workload or ["c1", "c2", "c3", "c3_32k", "c4", "c5_g8", "c5_g32"]
+        for name in names:
+            reports.append(run_workload(ext, name, a.engines, a.repeats, a.warmup, a.rotations,
+                                        device, wl.DEFAULT_SEED if a.seed is None else a.seed,
+                                        a.kv_fp8, graph=a.graph))
+            torch.cuda.empty_cache()
     text = markdown(reports)
     print(text, flush=True)
     if a.json:

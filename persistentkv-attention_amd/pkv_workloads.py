@@ -112,12 +112,44 @@ def make_lengths(trace: str, requests: int, seed: int, page_size: int = 16):
     return result
 
 
+def load_trace_specs(path, limit, page_size=16):
+    """``[(arrival, prompt_len, decode_len)]`` of the first ``limit`` rows of a CSV or JSON
+    request trace (benchmark_serving_trace.py:198-229): fields prompt_len (or prompt),
+    decode_len (or decode) and optionally arrival (or arrival_step, default the row index);
+    prompts rounded up to whole pages."""
+    import csv
+    import json
+    import os
+    if os.path.splitext(str(path))[1].lower() == ".json":
+        with open(path) as fh:
+            rows = json.load(fh)
+        if not isinstance(rows, list):
+            raise ValueError("a JSON trace file must contain a list of request objects")
+    else:
+        with open(path, newline="") as fh:
+            rows = list(csv.DictReader(fh))
+    specs = []
+    for index, row in enumerate(rows[:limit]):
+        try:
+            prompt = int(row.get("prompt_len", row.get("prompt", "")))
+            decode = int(row.get("decode_len", row.get("decode", "")))
+        except ValueError as error:
+            raise ValueError("trace-file rows must define integer prompt_len/prompt and "
+                             "decode_len/decode fields") from error
+        arrival = int(row.get("arrival", row.get("arrival_step", index)))
+        specs.append((arrival, rounded_length(prompt, page_size), decode))
+    if not specs:
+        raise ValueError(f"trace file produced no requests: {path}")
+    return specs
+
+
 def build_requests(lengths, max_active, seed, hole_fraction, page_size=16, bucket_tokens=0,
-                   extra_tokens=0):
+                   extra_tokens=0, arrivals=None):
     """Page allocation of benchmark_serving_trace.py:232-282: each request reserves its
     rounded final length in pages; the pool holds ``ceil(total / (1 - holes))`` pages and
     requests take consecutive slices of ``randperm(pool)`` drawn with ``seed + 99``.
-    ``extra_tokens`` reserves room for that many tokens beyond prompt + decode."""
+    ``extra_tokens`` reserves room for that many tokens beyond prompt + decode; request i
+    arrives at ``arrivals[i]`` (a trace file's) or ``i // max_active``."""
     logical = []
     for prompt, decode in lengths:
         exact = prompt + decode + extra_tokens
@@ -134,7 +166,8 @@ def build_requests(lengths, max_active, seed, hole_fraction, page_size=16, bucke
     for request_id, ((prompt, decode), pages) in enumerate(zip(lengths, logical)):
         assigned = tuple(int(x) for x in ids[cursor:cursor + pages].tolist())
         cursor += pages
-        built.append(Request(request_id, request_id // max_active, prompt, decode, assigned))
+        arrival = arrivals[request_id] if arrivals is not None else request_id // max_active
+        built.append(Request(request_id, arrival, prompt, decode, assigned))
     return built, physical_pages
 
 
@@ -299,6 +332,33 @@ def config_smoke(context, seed=DEFAULT_SEED, batch=1, hq=32, hkv=8, splits=16):
     step = StepState(0, tuple(range(batch)), (context,) * batch)
     return Workload(f"smoke_g{hq // hkv}_{context // 1024}k", "attention_contiguous", hq, hkv,
                     context, torch.float16, seed, reqs, [step], batch, splits=splits)
+
+
+def config_trace(trace="bimodal", requests=24, max_active=8, steps=48, seed=20260622,
+                 hole_fraction=0.50, page_size=16, hkv=8, hq=32, splits=16, bucket_tokens=0,
+                 trace_file=None):
+    """A trace of the reference's serving harness with its command-line options and
+    defaults (benchmark_serving_trace.py:1114-1163; main :1219-1229): the request family
+    (make_lengths) or a trace file, the page allocation with the hole fraction and bucket
+    rounding (build_requests), the reference's admission rule (build_steps) cut to
+    ``steps``, fp16, Hq 32.  Run through the work-queue op with ``splits``."""
+    if trace_file is not None:
+        specs = load_trace_specs(trace_file, requests, page_size)
+        lengths = [(p, d) for _, p, d in specs]
+        arrivals = [a for a, _, _ in specs]
+    else:
+        lengths = make_lengths(trace, requests, seed, page_size)
+        arrivals = None
+    reqs, physical = build_requests(lengths, max_active, seed, hole_fraction, page_size,
+                                    bucket_tokens, arrivals=arrivals)
+    st = build_steps(reqs, max_active)[:steps]
+    if not st:
+        raise ValueError("the trace produced no active decode steps")
+    name = "trace_file" if trace_file is not None else f"trace_{trace}"
+    return Workload(name, "paged_attention_workqueue", hq, hkv, page_size, torch.float16, seed,
+                    reqs, st, physical, splits=splits,
+                    extra={"trace": trace, "max_active": max_active, "hole_fraction": hole_fraction,
+                           "bucket_tokens": bucket_tokens, "trace_file": trace_file})
 
 
 def config_smoke_paged(context, seed=DEFAULT_SEED, batch=1, hq=32, hkv=8, splits=16, page_size=16):

@@ -102,3 +102,41 @@ def test_harness_fp8_engines_match_oracle(ext, gpu):
                                wl.DEFAULT_SEED, kv_fp8=True)
     assert "fp8" in rep["dtype"]
     assert all(e["gate"]["pass"] for e in rep["engines"].values())
+
+
+@pytest.mark.parametrize("engine", ["workqueue", "bucket", "adaptive"])
+def test_reference_review_trace_step_matches_oracle(ext, gpu, engine):
+    """The reference's seed-20260623 bimodal B8 review trace (scripts/run_review_ablations.sh:
+    --trace bimodal --requests 24 --max-active 8 --steps 48 --hole-fraction 0.0, work-queue
+    splits 20, bucket splits 32): its middle step through each engine, against the oracle."""
+    w = wl.config_trace("bimodal", 24, 8, 48, 20260623, 0.0, 16, 8, 32, 20)
+    assert w.physical_pages == 24285  # results/review_ablations/seed_20260623_bimodal_b8.txt:16
+    eng = serving.Engine(engine, w, gpu, splits={"workqueue": 20, "bucket": 32}.get(engine))
+    q_pool = wl.make_q_pool(w, gpu)
+    k, v = wl.make_kv_pool(w, gpu)
+    i = len(w.steps) // 2
+    out = eng.run(ext, i, q_pool, k, v)
+    torch.cuda.synchronize()
+    print(f"engine={engine} step={i} lengths={w.steps[i].lengths}", flush=True)
+    assert_parity(out, _oracle(w, eng.gate_meta(i), q_pool[i], k, v))
+
+
+def test_trace_step_in_a_hip_graph_matches_eager(ext, gpu):
+    """--graph: a captured step replayed (several times, with eager work between) gives the
+    eager step's output bit for bit."""
+    w = wl.config_trace("bucketed", 16, 1, 8, 20260623, 0.0, 16, 8, 32, 32)
+    eng = serving.Engine("bucket", w, gpu, splits=32)
+    q_pool = wl.make_q_pool(w, gpu)
+    k, v = wl.make_kv_pool(w, gpu)
+    eager = eng.run(ext, 3, q_pool, k, v).clone()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        eng.run(ext, 3, q_pool, k, v)
+    for _ in range(3):
+        eng.output(3).fill_(float("nan"))
+        eng.run(ext, 5, q_pool, k, v)  # eager work on the same workspace between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(eng.output(3), eager)

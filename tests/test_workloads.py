@@ -45,3 +45,38 @@ def test_config_pages_are_disjoint_and_cover_every_step(name):
         assert len(st.active_ids) <= len(w.requests)
         for rid, length in zip(st.active_ids, st.lengths):
             assert 0 < length <= len(by_id[rid].physical_pages) * w.page_size
+
+
+def test_reference_review_traces_match_its_logs():
+    """The two review traces the reference published step times for, rebuilt with its
+    options: pool sizes as its logs print them, useful KV MiB per step as its profile
+    table (results/review_ablations/seed_20260623_bimodal_b8.txt:16, :35;
+    seed_20260623_bucketed_b1.txt:16, :35)."""
+    w = wl.config_trace("bimodal", 24, 8, 48, 20260623, 0.0, 16, 8, 32, 20)
+    assert w.physical_pages == 24285 and len(w.steps) == 48
+    assert round(sum(w.kv_bytes(i) for i in range(48)) / 48 / 2 ** 20, 1) == 550.5
+    w = wl.config_trace("bucketed", 16, 1, 64, 20260623, 0.0, 16, 8, 32, 32)
+    assert w.physical_pages == 30793 and len(w.steps) == 64
+    assert round(sum(w.kv_bytes(i) for i in range(64)) / 64 / 2 ** 20, 1) == 32.1
+    assert all(len(s.active_ids) == 1 for s in w.steps)
+
+
+def test_trace_file_loader(tmp_path):
+    """load_trace_specs (benchmark_serving_trace.py:198-229): CSV and JSON, the field
+    aliases, arrivals defaulting to the row index, prompts rounded up to pages, the
+    request limit, and the error for a row without integer lengths."""
+    csv_path = tmp_path / "t.csv"
+    csv_path.write_text("prompt_len,decode_len,arrival\n100,5,0\n4096,7,2\n")
+    assert wl.load_trace_specs(csv_path, 10) == [(0, 112, 5), (2, 4096, 7)]
+    json_path = tmp_path / "t.json"
+    json_path.write_text('[{"prompt": 17, "decode": 3}, {"prompt": 32, "decode": 4, "arrival_step": 9}]')
+    assert wl.load_trace_specs(json_path, 10) == [(0, 32, 3), (9, 32, 4)]
+    assert wl.load_trace_specs(json_path, 1) == [(0, 32, 3)]
+    bad = tmp_path / "bad.csv"
+    bad.write_text("prompt_len,decode_len\nx,5\n")
+    with pytest.raises(ValueError, match="integer"):
+        wl.load_trace_specs(bad, 10)
+    w = wl.config_trace(trace_file=str(json_path), requests=10, max_active=1, steps=20,
+                        hole_fraction=0.0)
+    assert [r.arrival for r in w.requests] == [0, 9]
+    assert w.steps[0].lengths == (32,) and w.steps[-1].active_ids == (1,)
