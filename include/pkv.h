@@ -374,6 +374,12 @@ typedef struct pkv_cost_model {
   int32_t supported_group;    /* SUPPORTED_PERSISTENTKV_GQA; 0 accepts every G */
   int32_t min_long_context;   /* 16384 in the reference's adaptive gate (:457) */
   int32_t policy;             /* pkv_policy used for the split choices */
+  /* MI355X policy only (no counterpart in the reference's model): fixed costs of this
+   * engine's launches, fitted to measured step times (profiles/cost_model_calibration.json,
+   * persistentkv-attention_amd/pkv_calibrate.py). */
+  double unit_round_us;       /* per round of two workgroups per CU of a split grid */
+  double grid_merge_us;       /* a split grid's merge kernel */
+  double queue_merge_us;      /* the work queue's merge kernel (balanced schedule) */
 } pkv_cost_model;
 
 /* Fills *model with the reference constants (RTX 3060) or the MI355X constants. */

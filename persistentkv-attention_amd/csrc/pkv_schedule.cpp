@@ -50,6 +50,19 @@ constexpr int kMiTargetItems = kMiComputeUnits * 3 / 2;
 constexpr int kMiMinTilesPerItem = 8;
 constexpr int kMiWideGroup = 16;  // G above this runs the two-head-block kernel
 constexpr int kMiMaxSplits = 128;
+// Fixed costs of the MI355X route model (mi355x_route_us), fitted by non-negative least
+// squares to the step times of both routes on 6 sampled steps of each of 14 workloads
+// (this engine's configurations and the reference's review traces; pkv_serving.py
+// --calibrate, fitted by pkv_calibrate.py): the per-CU read rate that prices a tile
+// (kMiReadGbps), a cost per round of two workgroups per CU of a split grid, and the work
+// queue's fixed cost (its merge, the launch gap and the balanced decode's ramp).  The
+// grid's fixed cost fits to 0: its rounds carry it.  With these the router takes the
+// faster route on every sampled step where the two differ by more than 3 %.
+constexpr double kMiReadGbps = 6372.0;
+constexpr double kMiUnitRoundUs = 5.88;
+constexpr double kMiGridMergeUs = 0.0;
+constexpr double kMiQueueMergeUs = 11.47;
+
 
 }  // namespace
 
@@ -64,16 +77,20 @@ void pkv_cost_model_preset(int32_t policy, pkv_cost_model* m) {
   m->policy = policy;
   if (policy == PKV_POLICY_MI355X) {
     m->compute_units = kMiComputeUnits;
-    m->read_gbps = 8000.0 * 0.70;   // 70 % of the 8 TB/s HBM3E peak
+    m->read_gbps = kMiReadGbps;     // fitted (see kMiReadGbps)
     m->launch_overhead_us = 1.5;    // gap between dependent launches on one stream
     m->min_ctas_per_cu = 2.0;
     m->supported_group = 0;         // every G runs natively
+    m->unit_round_us = kMiUnitRoundUs;
+    m->grid_merge_us = kMiGridMergeUs;
+    m->queue_merge_us = kMiQueueMergeUs;
   } else {
     m->compute_units = 28;          // SM_COUNT, :39
     m->read_gbps = 302.0;           // ROOFLINE_READ_GBPS, :40
     m->launch_overhead_us = 8.0;    // LAUNCH_OVERHEAD_US, :41
     m->min_ctas_per_cu = 4.0;       // MIN_CTAS_PER_SM, :42
     m->supported_group = 4;         // SUPPORTED_PERSISTENTKV_GQA, :43
+    m->unit_round_us = m->grid_merge_us = m->queue_merge_us = 0.0;  // not in its model
   }
 }
 
@@ -189,12 +206,6 @@ int32_t pkv_model_workqueue_splits(const int32_t* lengths, int32_t count, int32_
 //   split grid (S splits per row, row-local bounds): max(share, longest unit) tiles,
 //     plus a fixed cost per round of two 8-wave workgroups per CU, plus the merge;
 //   work queue (balanced schedule: equal tile shares per wave): share tiles plus its merge.
-// Calibration (measured step times): C3 at 32k (B1 Hkv 8) grid S=32 27.6 us, queue ~31;
-// C4 queue 45 us; C2 (B8 MHA) grid S=8 112 us, queue ~115; C5 G=32 queue 67 us.
-constexpr double kMiUnitRoundUs = 1.5;   // Q load, pipeline ramp and combine per round
-constexpr double kMiGridMergeUs = 4.0;   // split-grid merge kernel
-constexpr double kMiQueueMergeUs = 7.0;  // balanced-schedule merge (recomputes the layout)
-
 double mi355x_route_us(const int32_t* lengths, int32_t count, int32_t route, int32_t splits,
                        const pkv_cost_model* m) {
   const int64_t hkv = m->num_kv_heads > 0 ? m->num_kv_heads : 1;
@@ -209,13 +220,13 @@ double mi355x_route_us(const int32_t* lengths, int32_t count, int32_t route, int
   }
   const double share = (double)total / (double)cus;
   const double launches_us = 2.0 * m->launch_overhead_us;
-  if (route == PKV_ROUTE_WORKQUEUE) return share * tile_us + kMiQueueMergeUs + launches_us;
+  if (route == PKV_ROUTE_WORKQUEUE) return share * tile_us + m->queue_merge_us + launches_us;
   const int64_t s = std::max<int32_t>(1, splits);
   const double unit = (double)ceil_div_pos(std::max<int64_t>(longest, 1), s);
   const double units = (double)count * hkv * s;
   const double rounds = std::ceil(units / (2.0 * cus));
-  return std::max(share, unit) * tile_us + rounds * kMiUnitRoundUs +
-         (s > 1 ? kMiGridMergeUs + launches_us : 0.5 * launches_us);
+  return std::max(share, unit) * tile_us + rounds * m->unit_round_us +
+         (s > 1 ? m->grid_merge_us + launches_us : 0.5 * launches_us);
 }
 
 // estimate_route_ms, benchmark_serving_trace.py:418-442 (and useful_kv_mb_for_state :511-513).

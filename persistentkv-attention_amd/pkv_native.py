@@ -43,6 +43,9 @@ class CostModel(ctypes.Structure):
         ("supported_group", ctypes.c_int32),
         ("min_long_context", ctypes.c_int32),
         ("policy", ctypes.c_int32),
+        ("unit_round_us", ctypes.c_double),
+        ("grid_merge_us", ctypes.c_double),
+        ("queue_merge_us", ctypes.c_double),
     ]
 
 

@@ -499,6 +499,70 @@ def run_workload(ext, name, engines, repeats, warmup, rotations, device, seed, k
     return report
 
 
+def calibrate(ext, device, steps_per_workload=6, reps=5, rotations=4):
+    """Step times of the two routes the MI355X router chooses between, on sampled steps of
+    this engine's configurations and the reference's review traces: the split grid as one
+    ragged bucket with the router's split count (pkv_model_bucket_splits) and the work
+    queue with the MI355X planner.  Each time is the mean of ``reps`` event-timed calls,
+    HBM-cold (pool replicas rotated), after two warm-up calls.  pkv_calibrate.py fits the
+    cost model's constants to these samples."""
+    cases = [(name, lambda name=name: wl.CONFIGS[name]())
+             for name in ("c1", "c2", "c3", "c3_32k", "c4", "c5_g8", "c5_g32")]
+    for trace, b, reqs, steps, hkv in (("bimodal", 8, 24, 48, 8), ("bimodal", 8, 24, 48, 4),
+                                       ("bimodal", 8, 24, 48, 32), ("uniform", 8, 24, 48, 8),
+                                       ("zipf", 8, 24, 48, 8), ("bucketed", 1, 16, 64, 8),
+                                       ("homogeneous", 4, 8, 48, 8)):
+        cases.append((f"trace_{trace}_b{b}_hkv{hkv}",
+                      lambda t=trace, b=b, r=reqs, n=steps, h=hkv:
+                      wl.config_trace(t, r, b, n, 20260623, 0.0, 16, h, 32, 16)))
+    samples = []
+    for name, make in cases:
+        w = make()
+        q_pool = wl.make_q_pool(w, device)
+        k0, v0 = wl.make_kv_pool(w, device)
+        pools = [(k0, v0)] + [(k0.clone(), v0.clone()) for _ in range(rotations - 1)]
+        n = len(w.steps)
+        picks = sorted({(j * n) // steps_per_workload for j in range(steps_per_workload)})
+        model = mi355x_model(w)
+        for i in picks:
+            lengths = list(w.steps[i].lengths)
+            bs = pkv_native.model_bucket_splits(lengths, w.hkv, pkv_native.POLICY_MI355X)
+            grid = compile_bucket_step(w, i, device, bs, single_bucket=True)
+            gws = bucket_workspace(w, [grid], device)
+            saved = (w.splits, w.auto_splits, w.policy)
+            w.splits, w.auto_splits, w.policy = 1, True, pkv_native.POLICY_MI355X
+            queue = _queue_step(w, i, device)
+            w.splits, w.auto_splits, w.policy = saved
+            qws = wl.workspace_for(w, [queue], device)
+
+            def timed(fn):
+                for k in range(2):
+                    fn(*pools[k % len(pools)])
+                torch.cuda.synchronize()
+                ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                      for _ in range(reps)]
+                for k in range(reps):
+                    kp, vp = pools[(k + 2) % len(pools)]
+                    ev[k][0].record()
+                    fn(kp, vp)
+                    ev[k][1].record()
+                torch.cuda.synchronize()
+                return statistics.mean(a.elapsed_time(b) * 1e3 for a, b in ev)
+
+            grid_us = timed(lambda kp, vp: run_bucket_step(ext, w, grid, i, q_pool, kp, vp, gws))
+            queue_us = timed(lambda kp, vp: wl.run_step(ext, w, queue, i, q_pool, kp, vp, qws))
+            route, _, _ = pkv_native.choose_adaptive_route(lengths, model)
+            samples.append({"workload": name, "step": i, "hq": w.hq, "hkv": w.hkv,
+                            "dtype": str(w.dtype).replace("torch.", ""), "lengths": lengths,
+                            "grid_splits": bs, "grid_us": round(grid_us, 2),
+                            "queue_us": round(queue_us, 2), "router_at_run": route})
+            print(f"{name:24s} step {i:3d} grid S={bs:3d} {grid_us:8.1f} us  queue {queue_us:8.1f} us"
+                  f"  router {route}", flush=True)
+        del pools, k0, v0, q_pool
+        torch.cuda.empty_cache()
+    return samples
+
+
 def markdown(reports):
     lines = []
     for r in reports:
@@ -577,9 +641,19 @@ def main(argv=None):
                         "engine runs the *_fp8 ops and the gate uses the dequantised pages")
     p.add_argument("--json")
     p.add_argument("--md")
+    p.add_argument("--calibrate", metavar="FILE",
+                   help="time the router's two routes on sampled steps of every configuration "
+                        "and review trace and write the samples to FILE (pkv_calibrate.py fits "
+                        "the MI355X cost model to them)")
     a = p.parse_args(argv)
     import persistentkv_torch_ext as ext
     device = torch.device("cuda:0")
+    if a.calibrate:
+        samples = calibrate(ext, device)
+        with open(a.calibrate, "w") as fh:
+            json.dump({"gpu": torch.cuda.get_device_name(0), "compute_units": COMPUTE_UNITS,
+                       "samples": samples}, fh, indent=1)
+        return
     reports = []
     if a.trace or a.trace_file:
         seed = 20260622 if a.seed is None else a.seed
