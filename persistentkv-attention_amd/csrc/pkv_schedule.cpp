@@ -51,7 +51,7 @@ constexpr int kMiMinTilesPerItem = 8;
 constexpr int kMiWideGroup = 16;  // G above this runs the two-head-block kernel
 constexpr int kMiMaxSplits = 128;
 // Fixed costs of the MI355X route model (mi355x_route_us), fitted by non-negative least
-// squares to the step times of both routes on 6 sampled steps of each of 14 workloads
+// squares to the step times of both routes on up to 6 sampled steps of each of 14 workloads
 // (this engine's configurations and the reference's review traces; pkv_serving.py
 // --calibrate, fitted by pkv_calibrate.py): the per-CU read rate that prices a tile
 // (kMiReadGbps), a cost per round of two workgroups per CU of a split grid, and the work

@@ -1,6 +1,6 @@
 """The MI355X cost model of the adaptive router against measured step times
 (profiles/cost_model_calibration.json: both routes, the split grid with the router's split
-count and the work queue with the MI355X planner, timed on 6 sampled steps of each of
+count and the work queue with the MI355X planner, timed on up to 6 sampled steps of each of
 this engine's configurations and the reference's review traces by
 ``pkv_serving.py --calibrate``).
 
