@@ -64,6 +64,13 @@ def _sweep_table():
 _sweep_table()
 HBM_PEAK_GBPS = 8000.0
 MALL_BYTES = 256 * 2 ** 20  # MI355X Infinity Cache
+WORKSPACE_LABELS = {
+    "engine": ("this engine's size for its faster decomposition "
+               "(pkv_workqueue_balanced_workspace_bytes / pkv_split_workspace_bytes / "
+               "pkv_direct_workspace_bytes, at least the reference's)"),
+    "reference": ("the reference callers' size (pkv_workspace_bytes: none for a direct "
+                  "launch; total_partial_slots x Hq x 130 floats for the work queue)"),
+}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "c4_decode_traffic.json")
 TRAFFIC_FILE_FP8 = os.path.join(ROOT, "profiles", "c4_fp8_decode_traffic.json")
 
@@ -93,6 +100,9 @@ def parse_args():
     p.add_argument("--graph", action="store_true",
                    help="capture the timed steps into one HIP graph and replay it (as the "
                         "reference harness replays captured steps, benchmark_serving_trace.py:1439-1452)")
+    p.add_argument("--workspace", choices=("engine", "reference"), default="engine",
+                   help="workspace size: this engine's for its faster decomposition, or the "
+                        "reference callers' (none for a direct launch)")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time budget")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--seed", type=int, default=20260623)
@@ -195,7 +205,7 @@ def run_workload(args, workload):
               file=sys.stderr)
         sys.exit(2)
     metas = [wl.compile_step(w, i, dev) for i in range(len(w.steps))]
-    ws = wl.workspace_for(w, metas, dev)
+    ws = wl.workspace_for(w, metas, dev, size=args.workspace)
     q_pool = wl.make_q_pool(w, dev)
     wl.bind_queries(metas, q_pool)
     k0, v0 = wl.make_kv_pool(w, dev)
@@ -435,10 +445,7 @@ def run_workload(args, workload):
                    "trace_mean_kv_mb_per_step": round(sum(m.kv_bytes for m in metas) / n_trace / 1e6, 2),
                    "cache_basis": f"HBM-cold ({len(pools)} rotated KV pool replicas)",
                    "workspace_bytes": ws.numel() * ws.element_size(),
-                   "workspace": ("this engine's size for its faster decomposition "
-                                 "(pkv_workqueue_balanced_workspace_bytes / "
-                                 "pkv_split_workspace_bytes / pkv_direct_workspace_bytes, at "
-                                 "least the reference's)")},
+                   "workspace": WORKSPACE_LABELS[args.workspace]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "step_frac": round(value / HBM_PEAK_GBPS, 4),

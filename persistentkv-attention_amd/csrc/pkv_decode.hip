@@ -31,6 +31,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <algorithm>
 #include <cmath>
 #include <mutex>
 #include <tuple>
@@ -319,23 +320,28 @@ struct FastPager {
     return p;
   }
 
+  // K and V buffer descriptors of 16-token block b of `tile`, covering only its valid rows.
+  __device__ inline void block_rsrc(int tile, int b, const Pages& p, __amdgpu_buffer_rsrc_t& rk,
+                                    __amdgpu_buffer_rsrc_t& rv) const {
+    const int tok0 = tile * kTile + b * 16;
+    int nvalid = lim - tok0;
+    nvalid = nvalid < 0 ? 0 : (nvalid > 16 ? 16 : nvalid);
+    int logical, in_page;
+    page_of(a, tok0, logical, in_page);
+    const long off = nvalid > 0
+        ? (long)clamp_page(a, p.page[b]) * page_bytes + head_bytes + (long)in_page * (kD * 2) : 0;
+    // Descriptors must be wave-uniform (SGPRs); readfirstlane states that to the
+    // compiler, which otherwise wraps every buffer load in a waterfall loop.
+    const int nrec = uniform(nvalid * (kD * 2));
+    rk = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(a.k_pages + off), (short)0, nrec, kRsrcWord3);
+    rv = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(a.v_pages + off), (short)0, nrec, kRsrcWord3);
+  }
+
   __device__ inline void issue(int tile, const Pages& p, TileRegs& r) const {
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      const int tok0 = tile * kTile + b * 16;
-      int nvalid = lim - tok0;
-      nvalid = nvalid < 0 ? 0 : (nvalid > 16 ? 16 : nvalid);
-      int logical, in_page;
-      page_of(a, tok0, logical, in_page);
-      const long off = nvalid > 0
-          ? (long)clamp_page(a, p.page[b]) * page_bytes + head_bytes + (long)in_page * (kD * 2) : 0;
-      // Descriptors must be wave-uniform (SGPRs); readfirstlane states that to the
-      // compiler, which otherwise wraps every buffer load in a waterfall loop.
-      const int nrec = uniform(nvalid * (kD * 2));
-      const __amdgpu_buffer_rsrc_t rk =
-          __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(a.k_pages + off), (short)0, nrec, kRsrcWord3);
-      const __amdgpu_buffer_rsrc_t rv =
-          __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(a.v_pages + off), (short)0, nrec, kRsrcWord3);
+      __amdgpu_buffer_rsrc_t rk, rv;
+      block_rsrc(tile, b, p, rk, rv);
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) r.k[b][kk] = __builtin_amdgcn_raw_buffer_load_b128(rk, koff[kk], 0, kKvLoadPolicy);
 #pragma unroll
@@ -370,21 +376,27 @@ struct AppendPager : FastPager {
     vn = args.v_new + src;
   }
 
-  __device__ inline void issue(int tile, const Pages& p, TileRegs& r) const {
-    FastPager::issue(tile, p, r);
-    const int rel = pos - tile * kTile;  // wave-uniform
-    if (pos < 0 || rel < 0 || rel >= kTile) return;
+  // The new token's row in `tile` (0 .. 31), or -1 when the tile does not hold it or the
+  // append skips the row (its page id is outside the pool).  Wave-uniform.
+  __device__ inline int new_row(int tile, const Pages& p) const {
+    const int rel = pos - tile * kTile;
+    if (pos < 0 || rel < 0 || rel >= kTile) return -1;
+    const int page = (rel >> 4) ? p.page[1] : p.page[0];
+    return (unsigned)page < (unsigned)a.num_pages ? rel : -1;
+  }
+
+  // Takes the new token's V row (and, with K_REGS, its K row) from v_new / k_new into the
+  // tile's registers and writes both rows into the pools.  Lane (c, g) holds K row c of
+  // each block at bytes 64kk + 16g, and V row 4g + jj of block slot jj at bytes 16c
+  // (FastPager's koff / voff).  The lanes that hold the token reload those registers; the
+  // loads return in issue order, after the pool loads of the same registers.
+  template <bool K_REGS>
+  __device__ inline void take_new(int rel, const Pages& p, TileRegs& r) const {
     const int b = rel >> 4, prow = rel & 15;
-    const int page = b ? p.page[1] : p.page[0];
-    if ((unsigned)page >= (unsigned)a.num_pages) return;  // the append skips this row
-    // Lane (c, g) holds K row c of each block at bytes 64kk + 16g, and V row 4g + jj of
-    // block slot jj at bytes 16c (FastPager's koff / voff).
-    // The lanes that hold the token reload those registers from k_new / v_new; the
-    // loads return in issue order, after the pool loads of the same registers.
     const int c = lane & 15, g = lane >> 4;
 #pragma unroll
     for (int bb = 0; bb < 2; ++bb) {
-      if (bb == b && c == prow) {
+      if (K_REGS && bb == b && c == prow) {
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) r.k[bb][kk] = *(const u32x4*)(kn + kk * 64 + g * 16);
       }
@@ -392,11 +404,18 @@ struct AppendPager : FastPager {
       for (int jj = 0; jj < 4; ++jj)
         if (bb == b && 4 * g + jj == prow) r.v[bb * 4 + jj] = *(const u32x4*)(vn + c * 16);
     }
+    const int page = b ? p.page[1] : p.page[0];
     int logical, in_page;
     page_of(a, pos, logical, in_page);
     const long dst = (long)page * page_bytes + head_bytes + (long)in_page * (kD * 2) + lane * 4;
     *(uint32_t*)(const_cast<uint8_t*>(a.k_pages) + dst) = *(const uint32_t*)(kn + lane * 4);
     *(uint32_t*)(const_cast<uint8_t*>(a.v_pages) + dst) = *(const uint32_t*)(vn + lane * 4);
+  }
+
+  __device__ inline void issue(int tile, const Pages& p, TileRegs& r) const {
+    FastPager::issue(tile, p, r);
+    const int rel = new_row(tile, p);
+    if (rel >= 0) take_new<true>(rel, p, r);
   }
 };
 
@@ -425,18 +444,22 @@ struct ContigPager {
 
   __device__ inline Pages lookup(int) const { return {}; }
 
-  __device__ inline void issue(int tile, const Pages&, TileRegs& r) const {
+  __device__ inline void block_rsrc(int tile, int b, const Pages&, __amdgpu_buffer_rsrc_t& rk,
+                                    __amdgpu_buffer_rsrc_t& rv) const {
+    const int tok0 = tile * kTile + b * 16;
+    int nvalid = lim - tok0;
+    nvalid = nvalid < 0 ? 0 : (nvalid > 16 ? 16 : nvalid);
+    const long off = nvalid > 0 ? base + (long)tok0 * (kD * 2) : 0;
+    const int nrec = uniform(nvalid * (kD * 2));
+    rk = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(a.k_pages + off), (short)0, nrec, kRsrcWord3);
+    rv = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(a.v_pages + off), (short)0, nrec, kRsrcWord3);
+  }
+
+  __device__ inline void issue(int tile, const Pages& p, TileRegs& r) const {
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      const int tok0 = tile * kTile + b * 16;
-      int nvalid = lim - tok0;
-      nvalid = nvalid < 0 ? 0 : (nvalid > 16 ? 16 : nvalid);
-      const long off = nvalid > 0 ? base + (long)tok0 * (kD * 2) : 0;
-      const int nrec = uniform(nvalid * (kD * 2));
-      const __amdgpu_buffer_rsrc_t rk =
-          __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(a.k_pages + off), (short)0, nrec, kRsrcWord3);
-      const __amdgpu_buffer_rsrc_t rv =
-          __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(a.v_pages + off), (short)0, nrec, kRsrcWord3);
+      __amdgpu_buffer_rsrc_t rk, rv;
+      block_rsrc(tile, b, p, rk, rv);
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) r.k[b][kk] = __builtin_amdgcn_raw_buffer_load_b128(rk, koff[kk], 0, kKvLoadPolicy);
 #pragma unroll
@@ -444,6 +467,104 @@ struct ContigPager {
     }
   }
 };
+
+// A 2-byte pager (FastPager, ContigPager, AppendPager) whose K loads take whole 128-byte
+// lines and go straight to LDS, for launches of few units, where what one CU streams
+// bounds the launch: a lone CU streams 35-37 GB/s with the K-operand shape (16 rows x
+// 64 B per instruction) and 45-56 GB/s with whole lines.  K bypasses the registers
+// (buffer_load_dwordx4 ... lds: lane i of an instruction writes the 16 bytes at slab
+// offset 16 i), so a wave keeps two tiles in flight with one tile's V registers more;
+// V is loaded as by the base pager.
+// A slab holds a tile's two 16-token blocks, 16 rows x 256 B each, with
+// 16-byte column `col` of row `row` at position col ^ row: instruction j of a block
+// writes rows 4j .. 4j + 3 (lane (c, g): row 4j + g, position c, so it loads column
+// c ^ row; each quad of lanes still covers one aligned 64 bytes of a row), and a
+// K-operand read (lane (c, g): row c, column 4kk + g) meets each LDS bank once per 16
+// lanes.  tile_k of a LineTile reads the MFMA operands back one k-block at a time.
+constexpr int kSlabBytes = 8192;  // one tile's two blocks of K rows
+
+struct LineTile : TileRegs {  // k[][] unused: K is in the slab
+  const uint8_t* rd;  // this lane's K-operand row in the slab: slab + 256 c
+  int col;            // g ^ c: k-block kk's 16-byte column is 4 kk ^ col
+  int new_row;        // appending pagers: the new token's row of the tile, or -1
+  u32x4 k_new;        // ... and bytes 16 c .. +16 of its K row
+};
+
+template <class Base, int SLABS = 1>
+struct Lines : Base {
+  using Raw = LineTile;
+  uint8_t* slab;      // this wave's SLABS x 8 KB of LDS (wave-uniform); tile t uses slab t % SLABS
+  uint32_t kline[4];  // per-lane byte offsets inside a block of instruction j's K row
+  int lane;
+
+  __device__ Lines(const DecodeArgs& args, int row, int kvh, int limit, int lane_, uint8_t* s)
+      : Base(args, row, kvh, limit, lane_), slab(s), lane(lane_) {
+    const int c = lane_ & 15, g = lane_ >> 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) kline[j] = (4 * j + g) * 256 + (c ^ (4 * j + g)) * 16;
+  }
+
+  // Rows past the block's valid ones are outside the descriptor and load as 0; their
+  // scores are masked in compute_tile whatever the slab holds.  With AppendPager the new
+  // token's V row is taken into the registers here and its K row is loaded beside the
+  // tile, to be put into the slab once the tile has landed there (ready_tile).
+  __device__ inline void issue(int tile, const typename Base::Pages& p, LineTile& r) const {
+    uint8_t* sb = slab + (SLABS == 2 ? (tile & 1) * kSlabBytes : 0);
+    __amdgpu_buffer_rsrc_t rk[2], rv[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) this->block_rsrc(tile, b, p, rk[b], rv[b]);
+    // The loads keep their program order (ready_tile counts the ones after the K rows):
+    // the tile's 8 K loads, then its 8 V loads, each group after everything issued before.
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rk[b], (__attribute__((address_space(3))) void*)(sb + b * 4096 + j * 1024), 16, kline[j],
+            0, 0, kKvLoadPolicy);
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        r.v[b * 4 + j] = __builtin_amdgcn_raw_buffer_load_b128(rv[b], this->voff[b * 4 + j], 0, kKvLoadPolicy);
+    r.new_row = -1;
+    if constexpr (std::is_same_v<Base, AppendPager>) {
+      r.new_row = this->new_row(tile, p);
+      if (r.new_row >= 0) {
+        r.k_new = *(const u32x4*)(this->kn + (lane & 15) * 16);
+        this->template take_new<false>(r.new_row, p, r);
+      }
+    }
+    r.rd = sb + (lane & 15) * 256;
+    asm volatile("" ::: "memory");
+  }
+};
+
+// Pagers that load the K-operand layout into registers need nothing before the compute.
+template <class Pager, class Raw>
+__device__ inline void ready_tile(const Pager&, Raw&) {}
+
+// The tile's K rows have reached the slab once its 8 K loads are done.  Vector memory
+// loads complete in order, and at least 8 were issued after them (the tile's V loads),
+// 24 with two slabs (and the next tile's 16 K and V loads): at most that many
+// outstanding means the K rows are in.  The V registers are waited for by the compiler
+// where they are first used, after the scores.  The wait is also a compiler memory
+// barrier, so the slab's reads stay below it; consumed by the tile's MFMAs, they are
+// done before the slab's next loads are issued.
+template <class Base, int SLABS>
+__device__ inline void ready_tile(const Lines<Base, SLABS>& pg, LineTile& r) {
+  const int c = pg.lane & 15, g = pg.lane >> 4;
+  if constexpr (SLABS == 2) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  if (r.new_row >= 0) {  // the appended token's K row replaces what the pool held
+    const int row = r.new_row & 15;
+    if (g == 0) *(u32x4*)(r.rd - c * 256 + (r.new_row >> 4) * 4096 + row * 256 + (c ^ row) * 16) = r.k_new;
+    asm volatile("" ::: "memory");
+  }
+  r.col = g ^ c;
+}
 
 // Page-16 pager over fp8 (OCP e4m3) K/V: FastPager's table reads and per-lane rows with
 // 1-byte elements (a token row is 128 bytes), K in 16-byte and V in 8-byte chunks (the
@@ -593,6 +714,10 @@ __device__ inline u32x4 tile_k(const Fp8Tile& r, int b, int kk) {
 }
 template <class Elem>
 __device__ inline u32x4 tile_v(const Fp8Tile& r, int j) { return Elem::unpack8(r.v[j]); }
+template <class Elem>
+__device__ inline u32x4 tile_k(const LineTile& r, int b, int kk) {
+  return *(const u32x4*)(r.rd + b * 4096 + ((4 * kk) ^ r.col) * 16);
+}
 
 template <class Elem, int HB, class Tile>
 __device__ inline void compute_tile(WaveState<HB>& st, const Tile& r,
@@ -699,6 +824,7 @@ __device__ inline void stream_range_from(WaveState<HB>& st, const Pager& pg,
       pg.issue(t, pa, r);
       pa = pb;
       pb = pg.lookup(t + 2);
+      ready_tile(pg, r);
       compute_tile<Elem, HB>(st, r, qf, t, lim, lane, qk);
     }
   } else {
@@ -711,10 +837,12 @@ __device__ inline void stream_range_from(WaveState<HB>& st, const Pager& pg,
     for (int t = t0;; t += 2) {
       pg.issue(t + 1, pb, rb);
       pa = pg.lookup(t + 2);
+      ready_tile(pg, ra);
       compute_tile<Elem, HB>(st, ra, qf, t, lim, lane, qk);
       if (t + 1 >= t1) break;
       pg.issue(t + 2, pa, ra);
       pb = pg.lookup(t + 3);
+      ready_tile(pg, rb);
       compute_tile<Elem, HB>(st, rb, qf, t + 1, lim, lane, qk);
       if (t + 2 >= t1) break;
     }
@@ -730,10 +858,12 @@ __device__ inline void stream_range_issued(WaveState<HB>& st, const Pager& pg,
                                            typename Pager::Raw& rb, typename Pager::Pages pa) {
   typename Pager::Pages pb;
   for (int t = t0;; t += 2) {
+    ready_tile(pg, ra);
     compute_tile<Elem, HB>(st, ra, qf, t, lim, lane, qk);
     if (t + 1 >= t1) break;
     pg.issue(t + 2, pa, ra);
     pb = pg.lookup(t + 3);
+    ready_tile(pg, rb);
     compute_tile<Elem, HB>(st, rb, qf, t + 1, lim, lane, qk);
     if (t + 2 >= t1) break;
     pg.issue(t + 3, pb, rb);
@@ -1236,19 +1366,32 @@ __device__ inline void init_state(WaveState<HB>& st) {
 
 // K/V addressing of a launch: paged with 16-token-aligned pages, paged with any page
 // size, or contiguous.
-enum : int { kPgGeneric = 0, kPgFast = 1, kPgContig = 2, kPgFp8 = 3, kPgAppend = 4 };
+// kPgLines, kPgContigLines and kPgAppendLines are kPgFast, kPgContig and kPgAppend with
+// whole-line K loads (Lines).
+enum : int { kPgGeneric = 0, kPgFast = 1, kPgContig = 2, kPgFp8 = 3, kPgAppend = 4, kPgLines = 5,
+             kPgContigLines = 6, kPgAppendLines = 7 };
 
 // Streams tiles [t0, t1) of (row, kvh) into the wave state without finishing it, so that
-// several ranges can be streamed into one state (finish_state ends it).
+// several ranges can be streamed into one state (finish_state ends it).  `slab` is the
+// wave's 8 KB of LDS for the whole-line pagers.
 template <class Elem, int HB, int PG, int DEPTH = HB>
 __device__ inline void stream_tiles(const DecodeArgs& a, WaveState<HB>& st, const u32x4 (&qf)[HB][4],
                                     int row, int kvh, int t0, int t1, int len, int lane,
                                     bool have_first = false, FastPager::Pages f0 = {},
-                                    FastPager::Pages f1 = {}) {
+                                    FastPager::Pages f1 = {}, uint8_t* slab = nullptr) {
   const long lim_l = (long)t1 * kTile;
   const int lim = uniform(lim_l < len ? (int)lim_l : len);
   const float qk = a.score_scale;
-  if constexpr (PG == kPgFast) {
+  if constexpr (PG == kPgLines) {
+    Lines<FastPager, DEPTH> pg(a, row, kvh, lim, lane, slab);
+    stream_range<Elem, HB, decltype(pg), DEPTH>(st, pg, qf, t0, t1, lim, lane, qk);
+  } else if constexpr (PG == kPgContigLines) {
+    Lines<ContigPager, DEPTH> pg(a, row, kvh, lim, lane, slab);
+    stream_range<Elem, HB, decltype(pg), DEPTH>(st, pg, qf, t0, t1, lim, lane, qk);
+  } else if constexpr (PG == kPgAppendLines) {
+    Lines<AppendPager, DEPTH> pg(a, row, kvh, lim, lane, slab);
+    stream_range<Elem, HB, decltype(pg), DEPTH>(st, pg, qf, t0, t1, lim, lane, qk);
+  } else if constexpr (PG == kPgFast) {
     FastPager pg(a, row, kvh, lim, lane);
     if (have_first) stream_range_from<Elem, HB, decltype(pg), DEPTH>(st, pg, qf, t0, t1, lim, lane, qk, f0, f1);
     else stream_range<Elem, HB, decltype(pg), DEPTH>(st, pg, qf, t0, t1, lim, lane, qk);
@@ -1284,8 +1427,9 @@ template <class Elem, int HB, int PG, int DEPTH = HB>
 __device__ inline void stream_unit(const DecodeArgs& a, WaveState<HB>& st, const u32x4 (&qf)[HB][4],
                                    int row, int kvh, int t0, int t1, int len, int lane,
                                    bool have_first = false, FastPager::Pages f0 = {},
-                                   FastPager::Pages f1 = {}) {
-  stream_tiles<Elem, HB, PG, DEPTH>(a, st, qf, row, kvh, t0, t1, len, lane, have_first, f0, f1);
+                                   FastPager::Pages f1 = {}, uint8_t* slab = nullptr) {
+  stream_tiles<Elem, HB, PG, DEPTH>(a, st, qf, row, kvh, t0, t1, len, lane, have_first, f0, f1,
+                                    slab);
   finish_state<HB>(st);
 }
 
@@ -1517,14 +1661,14 @@ constexpr int kSoloTiles = 2;
 template <class Elem, int HB, int PG, int MODE, int DEPTH = HB>
 __device__ void solo_unit(const DecodeArgs& a, const Unit& u, int q_loaded, int t0, int t1,
                           const Dest& d, int lane, bool have_first, FastPager::Pages f0,
-                          FastPager::Pages f1, bool fused_all) {
+                          FastPager::Pages f1, bool fused_all, uint8_t* slab = nullptr) {
   const int qh0 = u.kvh * a.group;
   u32x4 qf[HB][4];
   load_q<HB, PG == kPgFp8>(a, q_loaded, u.row, qh0, lane, qf);
   WaveState<HB> st;
   init_state<HB>(st);
   stream_unit<Elem, HB, PG, DEPTH>(a, st, qf, u.row, u.kvh, t0, t1, u.len, lane, have_first, f0,
-                                   f1);
+                                   f1, slab);
   const int out_row = MODE == kDirect ? (a.out_indices ? a.out_indices[u.row] : u.row) : 0;
   write_wave_state<Elem, HB, MODE == kDirect>(a, st, qh0, out_row, d, lane);
   if (MODE == kQueue && a.merge_counters != nullptr) arrive<Elem>(a, u, qh0, lane, 0, 1, fused_all);
@@ -1558,6 +1702,10 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu((HB == 
 void decode_kernel(DecodeArgs a) {
   constexpr int kWaves = NW;
   constexpr int kThreads = NW * 64;
+  constexpr bool kLines = PG == kPgLines || PG == kPgContigLines || PG == kPgAppendLines;
+  // The whole-line pagers' slabs share the LDS with the combine, which starts with a
+  // barrier; the barrier-free combine would write it while other waves still stream.
+  static_assert(!(kLines && ASYNC), "whole-line K needs the barrier combine");
   extern __shared__ float lds[];
   __shared__ int arrivals;
   const int tid = threadIdx.x;
@@ -1635,7 +1783,8 @@ void decode_kernel(DecodeArgs a) {
   if (n <= kSoloTiles) {
     if (wave == 0)
       solo_unit<Elem, HB, PG, MODE, DEPTH>(a, u, q_loaded, u.tb, u.te, d, lane,
-                                           u.tb == first_tile, first0, first1, fused_all);
+                                           u.tb == first_tile, first0, first1, fused_all,
+                                           (uint8_t*)lds);
     return;
   }
 
@@ -1652,7 +1801,8 @@ void decode_kernel(DecodeArgs a) {
   const int w0 = uniform(u.tb + (n * wave) / kWaves);
   const int w1 = uniform(u.tb + (n * (wave + 1)) / kWaves);
   stream_unit<Elem, HB, PG, DEPTH>(a, st, qf, u.row, u.kvh, w0, w1, u.len, lane,
-                                   w0 == first_tile, first0, first1);
+                                   w0 == first_tile, first0, first1,
+                                   (uint8_t*)lds + (kLines ? wave * DEPTH * kSlabBytes : 0));
   const int out_row = MODE == kDirect ? (a.out_indices ? a.out_indices[u.row] : u.row) : 0;
   if constexpr (ASYNC) {
     if (!combine_async<Elem, HB, NW, MODE == kDirect>(a, st, lds, &arrivals, qh0, out_row, d, lane, wave))
@@ -2376,9 +2526,43 @@ hipError_t launch_decode(const DecodeArgs& a, int grid, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// Direct launches of few units (at most half the CUs, e.g. one row's 8 KV heads with no
+// workspace to split into): each unit is one workgroup on a CU of its own, so the launch
+// runs at what one CU streams, and whole-line K loads (Lines) raise that.  8 waves, each
+// with two tiles in flight (K in two 8 KB LDS slabs, V in registers: 256 KB per CU, 128 KB
+// of LDS, one workgroup per CU).  C1 (8 units of 1 MB): 21.9 us against 30.4 us with the
+// K-operand loads; 12 waves with one tile each 22.5 us, 16 waves 25.0 us (128 registers
+// per wave: the Q fragments spill); 9 or 10 waves with two tiles spill 55-143 registers.
+// PKV_LINES=0|1 forces the choice (tuning, tests).
+bool use_lines(int mode, int units) {
+  static const int forced = [] {
+    const char* e = getenv("PKV_LINES");
+    return e ? (e[0] == '0' ? 0 : 1) : -1;
+  }();
+  if (mode != kDirect || forced == 0) return false;
+  return forced == 1 || 2 * units <= cu_count();
+}
+
+constexpr int kLineWaves = 8;
+
+template <class Elem, int PG>
+hipError_t launch_lines(const DecodeArgs& a, int grid, hipStream_t stream) {
+  const size_t lds = std::max<size_t>((size_t)kLineWaves * 2 * kSlabBytes, lds_bytes(a.group, kLineWaves));
+  decode_kernel<Elem, 1, PG, kDirect, kLineWaves, false, 2>
+      <<<dim3(grid), dim3(kLineWaves * 64), lds, stream>>>(a);
+  return hipGetLastError();
+}
+
 // Contiguous K/V (no block table) runs only the direct and split modes.
 template <class Elem, int HB, int MODE>
 hipError_t launch_layout(const DecodeArgs& a, int grid, hipStream_t stream) {
+  if constexpr (HB == 1 && MODE == kDirect) {
+    if (!a.kv_fp8 && use_lines(MODE, grid)) {
+      if (!a.block_table) return launch_lines<Elem, kPgContigLines>(a, grid, stream);
+      if (a.k_new) return launch_lines<Elem, kPgAppendLines>(a, grid, stream);  // pages % 16 == 0
+      if (a.page_size % 16 == 0) return launch_lines<Elem, kPgLines>(a, grid, stream);
+    }
+  }
   if constexpr (MODE != kQueue) {
     if (!a.block_table) return launch_decode<Elem, HB, kPgContig, MODE>(a, grid, stream);
   }

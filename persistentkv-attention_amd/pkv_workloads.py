@@ -485,26 +485,37 @@ def compile_step(w: Workload, step_index: int, device) -> StepMeta:
                     t(np.arange(n)), output, w.splits, kv_bytes=w.kv_bytes(step_index))
 
 
-def workspace_for(w: Workload, metas, device, balanced=True):
-    """One fp32 workspace for every step of ``metas``: the work queue's partial states
-    (and, with ``balanced``, at least what its balanced schedule needs,
-    pkv_workqueue_balanced_workspace_bytes), a split grid's with room for its internal
-    sub-split (pkv_split_workspace_bytes), or for a direct
-    (num_splits == 1) launch the size at which the op runs its full internal split
-    (pkv_direct_workspace_bytes)."""
-    floats = 1
+def workspace_for(w: Workload, metas, device, balanced=True, size="engine"):
+    """One fp32 workspace for every step of ``metas``.
+
+    ``size="engine"``: the work queue's partial states (and, with ``balanced``, at least
+    what its balanced schedule needs, pkv_workqueue_balanced_workspace_bytes), a split
+    grid's with room for its internal sub-split (pkv_split_workspace_bytes), or for a
+    direct (num_splits == 1) launch the size at which the op runs its full internal split
+    (pkv_direct_workspace_bytes).
+    ``size="reference"``: the sizes the reference's callers allocate, which the op must
+    also accept: ``total_partial_slots * Hq * 130`` floats for the work queue,
+    ``B * Hq * S * 130`` for a split grid and none for a direct launch."""
+    if size not in ("engine", "reference"):
+        raise ValueError(f"workspace size must be 'engine' or 'reference', not {size!r}")
+    floats = 0
     for m in metas:
         if m.op == "paged_attention_workqueue":
             floats = max(floats, m.total_partial_slots * w.hq * (2 + HEAD_DIM))
-            if balanced:
+            if balanced and size == "engine":
                 floats = max(floats, pkv_native.workqueue_balanced_workspace_bytes(
                     len(m.seq_lens), w.hq, w.hkv) // 4)
+        elif size == "reference":
+            if m.splits > 1:
+                floats = max(floats, len(m.seq_lens) * w.hq * m.splits * (2 + HEAD_DIM))
         elif m.splits > 1:
             floats = max(floats, pkv_native.split_workspace_bytes(
                 len(m.seq_lens), w.hq, w.hkv, m.bucket_length, m.splits) // 4)
         else:
             floats = max(floats, pkv_native.direct_workspace_bytes(
                 len(m.seq_lens), w.hq, w.hkv, m.bucket_length) // 4)
+    if size == "engine":
+        floats = max(floats, 1)
     return torch.empty(floats, device=device, dtype=torch.float32)
 
 
