@@ -2526,29 +2526,32 @@ hipError_t launch_decode(const DecodeArgs& a, int grid, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// Direct launches of few units (at most half the CUs, e.g. one row's 8 KV heads with no
-// workspace to split into): each unit is one workgroup on a CU of its own, so the launch
-// runs at what one CU streams, and whole-line K loads (Lines) raise that.  8 waves, each
-// with two tiles in flight (K in two 8 KB LDS slabs, V in registers: 256 KB per CU, 128 KB
-// of LDS, one workgroup per CU).  C1 (8 units of 1 MB): 21.9 us against 30.4 us with the
-// K-operand loads; 12 waves with one tile each 22.5 us, 16 waves 25.0 us (128 registers
-// per wave: the Q fragments spill); 9 or 10 waves with two tiles spill 55-143 registers.
-// PKV_LINES=0|1 forces the choice (tuning, tests).
-bool use_lines(int mode, int units) {
+// Direct and split launches of few, long units (at most half the CUs, at least 16 tiles
+// each: one row's 8 KV heads with no workspace to split into, or a split launch whose
+// workspace holds no sub-splits): each unit is one workgroup on a CU of its own, so the
+// launch runs at what one CU streams, and whole-line K loads (Lines) raise that.  8 waves,
+// each with two tiles in flight (K in two 8 KB LDS slabs, V in registers: 256 KB per CU,
+// 128 KB of LDS, one workgroup per CU).  C1 (8 units of 1 MB): 21.9 us against 30.4 us
+// with the K-operand loads; 12 waves with one tile each 22.5 us, 16 waves 25.0 us (128
+// registers per wave: the Q fragments spill); 9 or 10 waves with two tiles spill 55-143
+// registers.  Units of 8 tiles or fewer are latency-bound and 0.2-0.4 us slower this way
+// (the 8-wave combine and the LDS round trip).  PKV_LINES=0|1 forces the choice (tuning,
+// tests).
+bool use_lines(int mode, int units, int unit_tiles) {
   static const int forced = [] {
     const char* e = getenv("PKV_LINES");
     return e ? (e[0] == '0' ? 0 : 1) : -1;
   }();
-  if (mode != kDirect || forced == 0) return false;
-  return forced == 1 || 2 * units <= cu_count();
+  if (mode == kQueue || forced == 0) return false;
+  return forced == 1 || (2 * units <= cu_count() && unit_tiles >= 16);
 }
 
 constexpr int kLineWaves = 8;
 
-template <class Elem, int PG>
+template <class Elem, int PG, int MODE>
 hipError_t launch_lines(const DecodeArgs& a, int grid, hipStream_t stream) {
   const size_t lds = std::max<size_t>((size_t)kLineWaves * 2 * kSlabBytes, lds_bytes(a.group, kLineWaves));
-  decode_kernel<Elem, 1, PG, kDirect, kLineWaves, false, 2>
+  decode_kernel<Elem, 1, PG, MODE, kLineWaves, false, 2>
       <<<dim3(grid), dim3(kLineWaves * 64), lds, stream>>>(a);
   return hipGetLastError();
 }
@@ -2556,11 +2559,13 @@ hipError_t launch_lines(const DecodeArgs& a, int grid, hipStream_t stream) {
 // Contiguous K/V (no block table) runs only the direct and split modes.
 template <class Elem, int HB, int MODE>
 hipError_t launch_layout(const DecodeArgs& a, int grid, hipStream_t stream) {
-  if constexpr (HB == 1 && MODE == kDirect) {
-    if (!a.kv_fp8 && use_lines(MODE, grid)) {
-      if (!a.block_table) return launch_lines<Elem, kPgContigLines>(a, grid, stream);
-      if (a.k_new) return launch_lines<Elem, kPgAppendLines>(a, grid, stream);  // pages % 16 == 0
-      if (a.page_size % 16 == 0) return launch_lines<Elem, kPgLines>(a, grid, stream);
+  if constexpr (HB == 1 && MODE != kQueue) {
+    const int row_tiles = (a.context + kTile - 1) / kTile;
+    const int unit_tiles = MODE == kSplit ? row_tiles / a.num_splits : row_tiles;
+    if (!a.kv_fp8 && use_lines(MODE, grid, unit_tiles)) {
+      if (!a.block_table) return launch_lines<Elem, kPgContigLines, MODE>(a, grid, stream);
+      if (a.k_new) return launch_lines<Elem, kPgAppendLines, MODE>(a, grid, stream);  // pages % 16 == 0
+      if (a.page_size % 16 == 0) return launch_lines<Elem, kPgLines, MODE>(a, grid, stream);
     }
   }
   if constexpr (MODE != kQueue) {

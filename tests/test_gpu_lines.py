@@ -1,14 +1,16 @@
-"""Direct launches of few units with no workspace: the whole-line K path.
+"""Launches of few, long units: the whole-line K path.
 
-A direct launch (num_splits == 1) of at most half as many (row, kv head) units as the GPU
-has CUs, with no workspace to split into, runs one workgroup per unit whose K loads take
+A direct launch (num_splits == 1) with no workspace to split into, or a split launch
+whose workspace holds no sub-splits, of at most half as many units as the GPU has CUs and
+at least 16 tiles (512 tokens) per unit, runs one workgroup per unit whose K loads take
 whole 128-byte lines straight into LDS (the reference's own C1 call: one row, 8 KV heads,
 `workspace` empty).  Each case here is such a launch, against the repack + fp32 SDPA
-oracle at the parity bar (max-abs 2e-3, mean-abs 3e-4): every op that has a direct launch
-(paged, masked, indexed, contiguous, the fused append), fp16 and bf16, G from 1 to 16,
-page sizes that are multiples of 16, ragged and empty rows, partial last tiles, units of
-one or two tiles (one wave alone) and long rows.  The fused append must equal the append
-followed by the same decode bit for bit, as on every other path.
+oracle at the parity bar (max-abs 2e-3, mean-abs 3e-4): every op with a grid launch
+(paged, masked, indexed, contiguous, the query-head baseline, the fused append), direct
+and split, fp16 and bf16, G from 1 to 16, page sizes that are multiples of 16, ragged and
+empty rows, rows of one or two tiles in a long bucket (one wave alone), partial last
+tiles and long rows.  The fused append must equal the append followed by the same decode
+bit for bit, as on every other path.
 """
 import pytest
 import torch
@@ -30,10 +32,10 @@ PAGED = [
     (1, 32, 8, 2048, 16, F16, "random"),       # config c1
     (1, 32, 8, 8192, 16, F16, "canonical"),
     (4, 32, 8, 1000, 32, BF16, "random"),      # partial last tile, page 32
-    (1, 8, 8, 33, 16, F16, "random"),          # G = 1, two tiles: one wave alone
-    (1, 32, 8, 20, 16, BF16, "reversed"),      # one partial tile
+    (1, 8, 8, 545, 16, F16, "random"),         # G = 1, partial last tile
+    (1, 32, 8, 520, 16, BF16, "reversed"),
     (2, 64, 4, 777, 64, F16, "random"),        # G = 16, page 64
-    (3, 12, 4, 123, 16, BF16, "random"),       # G = 3
+    (3, 12, 4, 1023, 16, BF16, "random"),      # G = 3
     (2, 32, 8, 3000, 256, F16, "reversed"),    # page 256
     (16, 32, 8, 600, 16, F16, "random"),       # 128 units: half of 256 CUs
     (1, 16, 8, 65536, 16, BF16, "random"),     # G = 2, 64k-token row
@@ -58,11 +60,13 @@ def test_paged_direct_without_workspace(ext, gpu, b, hq, hkv, ctx, ps, dtype, ta
 ])
 def test_masked_direct_without_workspace(ext, gpu, lengths, hq, hkv, ps, dtype):
     case = make_case(lengths, hq, hkv, ps, dtype, seed=sum(lengths))
-    b, bucket = len(lengths), max(lengths)
+    b, bucket = len(lengths), max(max(lengths), 1024)
+    bt = case.block_table
+    if bt.shape[1] * ps < bucket:  # the table covers the bucket
+        bt = torch.cat([bt, bt[:, -1:].expand(b, -(-bucket // ps) - bt.shape[1])], 1).contiguous()
     out = torch.full((b, hq, 128), float("nan"), dtype=dtype, device=gpu)
     ext.paged_attention_masked(case.q.to(gpu), case.k_pages.to(gpu), case.v_pages.to(gpu),
-                               case.block_table.to(gpu), case.seq_lens.to(gpu), out, _empty(gpu),
-                               bucket, ps, 1)
+                               bt.to(gpu), case.seq_lens.to(gpu), out, _empty(gpu), bucket, ps, 1)
     torch.cuda.synchronize()
     ref = oracle.paged_decode(case.q, case.k_pages, case.v_pages, case.block_table, case.seq_lens)
     assert_parity(out, ref)
@@ -87,8 +91,8 @@ def test_indexed_direct_without_workspace(ext, gpu, dtype):
 
 @pytest.mark.parametrize("b,hq,hkv,n,dtype", [
     (1, 32, 8, 2048, F16),
-    (3, 8, 8, 77, BF16),     # G = 1, N not a multiple of 16
-    (1, 4, 1, 5, F16),       # shorter than one 16-token block
+    (3, 8, 8, 577, BF16),    # G = 1, N not a multiple of 16
+    (1, 4, 1, 517, F16),
     (2, 32, 4, 5000, BF16),  # G = 8
 ])
 def test_contiguous_direct_without_workspace(ext, gpu, b, hq, hkv, n, dtype):
@@ -134,3 +138,20 @@ def test_fused_append_direct_without_workspace(ext, gpu, lengths, dtype):
     assert torch.equal(out2, out1)
     ref = oracle.paged_decode(case.q, k1.cpu(), v1.cpu(), case.block_table, case.seq_lens)
     assert_parity(out2, ref)
+
+
+@pytest.mark.parametrize("b,hq,hkv,ctx,splits,dtype", [
+    (1, 32, 8, 8192, 16, F16),    # 128 units of 16 tiles (the reference's workspace size)
+    (2, 32, 8, 8192, 8, BF16),
+    (8, 32, 8, 8192, 2, F16),
+    (1, 16, 4, 20000, 32, BF16),  # partial last split
+])
+def test_split_with_the_reference_workspace(ext, gpu, b, hq, hkv, ctx, splits, dtype):
+    case = make_case([ctx] * b, hq, hkv, 16, dtype, seed=ctx + splits)
+    ws = torch.empty(b * hq * splits * 130, dtype=torch.float32, device=gpu)  # no sub-splits
+    out = torch.full((b, hq, 128), float("nan"), dtype=dtype, device=gpu)
+    ext.paged_attention(case.q.to(gpu), case.k_pages.to(gpu), case.v_pages.to(gpu),
+                        case.block_table.to(gpu), out, ws, ctx, 16, splits)
+    torch.cuda.synchronize()
+    ref = oracle.paged_decode(case.q, case.k_pages, case.v_pages, case.block_table, case.seq_lens)
+    assert_parity(out, ref)
