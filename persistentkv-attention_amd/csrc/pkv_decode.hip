@@ -1658,7 +1658,7 @@ __device__ inline bool combine_async(const DecodeArgs& a, const WaveState<HB>& s
 // ---------------------------------------------------------------------------------
 constexpr int kSoloTiles = 2;
 
-template <class Elem, int HB, int PG, int MODE, int DEPTH = HB>
+template <class Elem, int HB, int PG, int MODE, int DEPTH = HB, bool FUSED = false>
 __device__ void solo_unit(const DecodeArgs& a, const Unit& u, int q_loaded, int t0, int t1,
                           const Dest& d, int lane, bool have_first, FastPager::Pages f0,
                           FastPager::Pages f1, bool fused_all, uint8_t* slab = nullptr) {
@@ -1671,7 +1671,7 @@ __device__ void solo_unit(const DecodeArgs& a, const Unit& u, int q_loaded, int 
                                    f1, slab);
   const int out_row = MODE == kDirect ? (a.out_indices ? a.out_indices[u.row] : u.row) : 0;
   write_wave_state<Elem, HB, MODE == kDirect>(a, st, qh0, out_row, d, lane);
-  if (MODE == kQueue && a.merge_counters != nullptr) arrive<Elem>(a, u, qh0, lane, 0, 1, fused_all);
+  if constexpr (MODE == kQueue && FUSED) arrive<Elem>(a, u, qh0, lane, 0, 1, fused_all);
 }
 
 // ---------------------------------------------------------------------------------
@@ -1697,7 +1697,7 @@ __device__ inline void zero_empty_rows(const DecodeArgs& a, int tid, int threads
   }
 }
 
-template <class Elem, int HB, int PG, int MODE, int NW, bool ASYNC, int DEPTH = HB>
+template <class Elem, int HB, int PG, int MODE, int NW, bool ASYNC, int DEPTH = HB, bool FUSED = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu((HB == 1 && DEPTH == 1) ? 2 : 1)))
 void decode_kernel(DecodeArgs a) {
   constexpr int kWaves = NW;
@@ -1715,12 +1715,10 @@ void decode_kernel(DecodeArgs a) {
   // Fused merge: whether the queue writes every slot (the arrival count and the merge's
   // slot rule follow from it).  Loaded here, waited for at the arrival.
   int so_first = 0, so_last = 0;
-  if constexpr (MODE == kQueue) {
-    if (a.merge_counters) {
-      so_first = load_vector_deferred(a.split_offsets);
-      so_last = load_vector_deferred(a.split_offsets + a.batch);
-      zero_empty_rows<Elem>(a, tid, kThreads);
-    }
+  if constexpr (MODE == kQueue && FUSED) {
+    so_first = load_vector_deferred(a.split_offsets);
+    so_last = load_vector_deferred(a.split_offsets + a.batch);
+    zero_empty_rows<Elem>(a, tid, kThreads);
   }
 
   // Work-queue units: one dependent round trip for the work item, then one for all it
@@ -1764,7 +1762,7 @@ void decode_kernel(DecodeArgs a) {
   const int qh0 = u.kvh * G;
   long state0, state_stride;
   unit_states<MODE>(a, u, qh0, state0, state_stride);
-  const bool fused = MODE == kQueue && a.merge_counters != nullptr;
+  constexpr bool fused = MODE == kQueue && FUSED;
   const bool fused_all =
       fused && queue_writes_every_slot(a.num_tasks, a.hkv, uniform(so_first), uniform(so_last));
   const Dest d{a.part_m, a.part_l, a.part_acc, state0, state_stride, fused};
@@ -1773,7 +1771,7 @@ void decode_kernel(DecodeArgs a) {
     write_neutral(a, state0, state_stride, G, tid, kThreads, fused);
     // An item without tiles is one of its row's arrivals too (a queue that writes every
     // slot; the builder emits none).
-    if (fused) arrive<Elem>(a, u, qh0, lane, wave, kWaves, fused_all);
+    if constexpr (fused) arrive<Elem>(a, u, qh0, lane, wave, kWaves, fused_all);
     return;
   }
 
@@ -1782,7 +1780,7 @@ void decode_kernel(DecodeArgs a) {
   const int n = u.te - u.tb;
   if (n <= kSoloTiles) {
     if (wave == 0)
-      solo_unit<Elem, HB, PG, MODE, DEPTH>(a, u, q_loaded, u.tb, u.te, d, lane,
+      solo_unit<Elem, HB, PG, MODE, DEPTH, FUSED>(a, u, q_loaded, u.tb, u.te, d, lane,
                                            u.tb == first_tile, first0, first1, fused_all,
                                            (uint8_t*)lds);
     return;
@@ -1807,10 +1805,10 @@ void decode_kernel(DecodeArgs a) {
   if constexpr (ASYNC) {
     if (!combine_async<Elem, HB, NW, MODE == kDirect>(a, st, lds, &arrivals, qh0, out_row, d, lane, wave))
       return;
-    if (fused) arrive<Elem>(a, u, qh0, lane, 0, 1, fused_all);
+    if constexpr (fused) arrive<Elem>(a, u, qh0, lane, 0, 1, fused_all);
   } else {
     combine_waves<Elem, HB, NW, MODE == kDirect>(a, st, lds, qh0, out_row, d, tid, lane, wave);
-    if (fused) arrive<Elem>(a, u, qh0, lane, wave, kWaves, fused_all);
+    if constexpr (fused) arrive<Elem>(a, u, qh0, lane, wave, kWaves, fused_all);
   }
 }
 
@@ -2498,30 +2496,42 @@ bool use_async_combine(int units) {
   return units >= 3 * cu_count();
 }
 
+// A work-queue launch with the fused merge (merge_counters set) runs its own kernel: the
+// arrivals and the in-kernel merge are compiled only into it, so the unfused kernel's
+// tile loop keeps the scalar registers they would take (the queue kernels spilled
+// 350-395 SGPRs with both paths in one kernel).
+template <class Elem, int HB, int PG, int MODE, int NW, bool ASYNC, int DEPTH = HB>
+void launch_kernel(const DecodeArgs& a, int grid, size_t lds, hipStream_t stream) {
+  if constexpr (MODE == kQueue) {
+    if (a.merge_counters) {
+      decode_kernel<Elem, HB, PG, MODE, NW, ASYNC, DEPTH, true>
+          <<<dim3(grid), dim3(NW * 64), lds, stream>>>(a);
+      return;
+    }
+  }
+  decode_kernel<Elem, HB, PG, MODE, NW, ASYNC, DEPTH, false><<<dim3(grid), dim3(NW * 64), lds, stream>>>(a);
+}
+
 template <class Elem, int HB, int PG, int MODE>
 hipError_t launch_decode(const DecodeArgs& a, int grid, hipStream_t stream) {
   const int nw = decode_waves(HB, MODE, grid);
   if constexpr (HB == 1) {
     if (nw == 2) {
       // 96 KB of LDS per workgroup keeps one workgroup, two waves, on each CU.
-      decode_kernel<Elem, 1, PG, MODE, 2, false, 2>
-          <<<dim3(grid), dim3(2 * 64), 96 * 1024, stream>>>(a);
+      launch_kernel<Elem, 1, PG, MODE, 2, false, 2>(a, grid, 96 * 1024, stream);
       return hipGetLastError();
     }
   }
   if (HB == 1 && nw == 8) {
     if constexpr (HB == 1 && PG != kPgGeneric && PG != kPgContig && MODE != kDirect) {
       if (use_async_combine(grid)) {
-        decode_kernel<Elem, HB, PG, MODE, 8, true>
-            <<<dim3(grid), dim3(8 * 64), lds_bytes(a.group, 8, true), stream>>>(a);
+        launch_kernel<Elem, HB, PG, MODE, 8, true>(a, grid, lds_bytes(a.group, 8, true), stream);
         return hipGetLastError();
       }
     }
-    decode_kernel<Elem, HB, PG, MODE, (HB == 1 ? 8 : 4), false>
-        <<<dim3(grid), dim3(8 * 64), lds_bytes(a.group, 8), stream>>>(a);
+    launch_kernel<Elem, HB, PG, MODE, (HB == 1 ? 8 : 4), false>(a, grid, lds_bytes(a.group, 8), stream);
   } else {
-    decode_kernel<Elem, HB, PG, MODE, 4, false>
-        <<<dim3(grid), dim3(4 * 64), lds_bytes(a.group, 4), stream>>>(a);
+    launch_kernel<Elem, HB, PG, MODE, 4, false>(a, grid, lds_bytes(a.group, 4), stream);
   }
   return hipGetLastError();
 }
