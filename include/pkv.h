@@ -225,10 +225,13 @@ size_t pkv_workqueue_balanced_workspace_bytes(int32_t batch, int32_t num_q_heads
 /* One stage of pkv_paged_attention_workqueue (fused_merge == 0), in whichever schedule
  * pkv_workqueue_schedule names: stage 1 = the decode kernel, 2 = the merge.  Stage 1 then
  * stage 2 on one stream equal the combined call bit for bit; they exist for per-kernel
- * timing and for callers that overlap the merge with other work.  kv_fp8 != 0 selects the
- * fp8 K/V pages of pkv_paged_attention_workqueue_fp8 with k_scale / v_scale.  The
- * reference launches both from one host function (cuh:1005-1017); it has no separate
- * entry points. */
+ * timing and for callers that overlap the merge with other work.  Both stages take the
+ * same arguments, the same workspace and workspace_bytes in particular (they choose the
+ * schedule and where its partial states and plan lie): stage 2 folds what the last stage
+ * 1 wrote into that workspace, so another step's stage 1 in between changes its result.
+ * kv_fp8 != 0 selects the fp8 K/V pages of pkv_paged_attention_workqueue_fp8 with
+ * k_scale / v_scale.  The reference launches both from one host function
+ * (cuh:1005-1017); it has no separate entry points. */
 int pkv_paged_attention_workqueue_stage(
     int32_t stage, const void* q_source, int32_t q_rows,
     const void* k_pages, const void* v_pages,
