@@ -1283,9 +1283,12 @@ __device__ inline int expected_arrivals(const DecodeArgs& a, const Unit& u, bool
 // Ordering, by the memory model: the workgroup's state stores happen before the barrier
 // (with one wave, its lanes issue in lock step, which the AMDGPU memory model treats as
 // ordered at wavefront scope); wave 0's lane 0 counts the arrival with an agent-scope
-// acq_rel read-modify-write, which releases those stores to every other unit of the group
-// and, for the last arrival, acquires theirs (the release sequence on the counter ties all
-// arrivals together); the second barrier passes the acquire on to the merging waves.
+// release read-modify-write, which releases those stores to every other unit of the
+// group.  The arrivals' RMWs form one release sequence on the counter, so the last
+// arrival, which reads the value the others' RMWs left, synchronises with every one of
+// them through an agent-scope acquire fence after its RMW; only it pays for the acquire
+// (an L2 invalidate), the others only for the release.  The second barrier passes the
+// acquire on to the merging waves.
 template <class Elem>
 __device__ inline void arrive(const DecodeArgs& a, const Unit& u, int qh0, int lane, int wave,
                               int nwaves, bool all) {
@@ -1294,8 +1297,9 @@ __device__ inline void arrive(const DecodeArgs& a, const Unit& u, int qh0, int l
   if (nwaves > 1) __syncthreads();
   int last = 0;
   if (wave == 0 && lane == 0) {
-    const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
     last = old == expected_arrivals(a, u, all) - 1;
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     if (nwaves > 1) last_flag = last;
   }
   if (nwaves > 1) {
