@@ -337,14 +337,26 @@ static void plan_row_splits(const int32_t* lengths, int32_t count, int32_t reque
       // The G > 16 kernel runs one workgroup per CU, one wave per SIMD, with a long
       // epilogue: every item should start in the first round.  Measured on C5 G=32
       // (bf16, B=64 Zipf): 232 items take 76.1 us per step, 259-291 items 90-100 us and
-      // 415 items 86.0 us.  Grow the items until there are at most kMiComputeUnits.
-      per_item = std::max<int64_t>(kMiMinTilesPerItem, ceil_div_pos(total * hkv, kMiComputeUnits));
-      for (;;) {
+      // 415 items 86.0 us.  The launch lasts as long as its largest item, so take the
+      // smallest item size at which there are at most kMiComputeUnits items (the item
+      // count only falls as the size grows: a binary search).
+      auto items_at = [&](int64_t size) {
         int64_t items = 0;
         for (int i = 0; i < count; ++i)
-          items += splits_of(std::max<int64_t>(1, tiles_of(lengths[i])), per_item) * hkv;
-        if (items <= kMiComputeUnits || per_item >= longest) break;
-        per_item += std::max<int64_t>(1, per_item / 16);
+          items += splits_of(std::max<int64_t>(1, tiles_of(lengths[i])), size) * hkv;
+        return items;
+      };
+      int64_t lo = std::max<int64_t>(kMiMinTilesPerItem, ceil_div_pos(total * hkv, kMiComputeUnits));
+      int64_t hi = std::max(lo, longest);
+      if (items_at(lo) > kMiComputeUnits) {
+        while (hi - lo > 1) {  // items_at(lo) > CUs; items_at(hi) <= CUs or hi == longest
+          const int64_t mid = lo + (hi - lo) / 2;
+          if (items_at(mid) <= kMiComputeUnits) hi = mid;
+          else lo = mid;
+        }
+        per_item = hi;
+      } else {
+        per_item = lo;
       }
     } else {
       per_item = std::max<int64_t>(kMiMinTilesPerItem, ceil_div_pos(total * hkv, kMiTargetItems));

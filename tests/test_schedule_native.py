@@ -85,6 +85,28 @@ def test_mi355x_planner_invariants():
             assert len(meta["work_items"]) <= max(256, n * hkv)
 
 
+def test_mi355x_planner_wide_group_takes_the_smallest_item_that_fits():
+    """G > 16: the split of every row is ceil(tiles / M) (at most 128) for the smallest item
+    size M (at least 8 tiles and the step's mean share of 256 CUs) at which the step has at
+    most 256 items, found here by brute force; the launch lasts as long as its largest
+    item."""
+    rng = np.random.default_rng(11)
+    for _ in range(60):
+        n = int(rng.integers(1, 70))
+        lengths = [int(x) for x in rng.integers(1, 66000, size=n)]
+        hkv = int(rng.choice([1, 2]))
+        tiles = [max(1, (x + 31) // 32) for x in lengths]
+        items_at = lambda m: sum(max(1, min(-(-t // m), 128)) for t in tiles) * hkv
+        m = max(8, -(-sum(tiles) * hkv // 256))
+        while items_at(m) > 256 and m < max(tiles):
+            m += 1
+        pages = [list(range(-(-x // 16) + 1)) for x in lengths]
+        meta = nat.build_workqueue(lengths, list(range(n)), pages, 16, 1, True, hkv,
+                                   nat.POLICY_MI355X, hq=32 * hkv)
+        expected = [max(1, min(-(-t // m), 128)) for t in tiles]
+        assert np.diff(meta["split_offsets"]).tolist() == expected
+
+
 def test_c4_step_uses_twenty_splits():
     lengths = [20000, 300, 700, 256, 1024, 512, 600, 31000]
     meta = nat.build_workqueue(lengths, list(range(8)), [list(range(-(-x // 16))) for x in lengths],
