@@ -1386,15 +1386,14 @@ __device__ inline void stream_tiles(const DecodeArgs& a, WaveState<HB>& st, cons
   const long lim_l = (long)t1 * kTile;
   const int lim = uniform(lim_l < len ? (int)lim_l : len);
   const float qk = a.score_scale;
-  if constexpr (PG == kPgLines) {
-    Lines<FastPager, DEPTH> pg(a, row, kvh, lim, lane, slab);
+  if constexpr (PG == kPgLines || PG == kPgContigLines || PG == kPgAppendLines) {
+    using Base = std::conditional_t<PG == kPgLines, FastPager,
+                                    std::conditional_t<PG == kPgContigLines, ContigPager, AppendPager>>;
+    Lines<Base, DEPTH> pg(a, row, kvh, lim, lane, slab);
     stream_range<Elem, HB, decltype(pg), DEPTH>(st, pg, qf, t0, t1, lim, lane, qk);
-  } else if constexpr (PG == kPgContigLines) {
-    Lines<ContigPager, DEPTH> pg(a, row, kvh, lim, lane, slab);
-    stream_range<Elem, HB, decltype(pg), DEPTH>(st, pg, qf, t0, t1, lim, lane, qk);
-  } else if constexpr (PG == kPgAppendLines) {
-    Lines<AppendPager, DEPTH> pg(a, row, kvh, lim, lane, slab);
-    stream_range<Elem, HB, decltype(pg), DEPTH>(st, pg, qf, t0, t1, lim, lane, qk);
+    // The loop's last loads (the tile after the range, which reads nothing) still write
+    // the slab; they are done before the LDS is used for the combine or the workgroup ends.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   } else if constexpr (PG == kPgFast) {
     FastPager pg(a, row, kvh, lim, lane);
     if (have_first) stream_range_from<Elem, HB, decltype(pg), DEPTH>(st, pg, qf, t0, t1, lim, lane, qk, f0, f1);
