@@ -155,3 +155,54 @@ def test_split_with_the_reference_workspace(ext, gpu, b, hq, hkv, ctx, splits, d
     torch.cuda.synchronize()
     ref = oracle.paged_decode(case.q, case.k_pages, case.v_pages, case.block_table, case.seq_lens)
     assert_parity(out, ref)
+
+
+def _draw(i):
+    import random
+    rng = random.Random(5000 + i)
+    g = rng.choice([1, 2, 3, 4, 8, 16])
+    hkv = rng.choice([1, 2, 4, 8])
+    b = rng.randint(1, max(1, min(8, 128 // hkv)))  # at most 128 units
+    op = ["paged", "masked", "indexed", "contiguous"][i % 4]
+    ps = rng.choice([16, 32, 64])
+    bucket = rng.randint(512, max(512, min(6000, 160000 // (b * hkv))))  # keeps the oracle fast
+    lengths = [bucket] * b if op in ("paged", "contiguous") else \
+        [bucket] + [rng.randint(0 if op != "paged" else 1, bucket) for _ in range(b - 1)]
+    return op, g * hkv, hkv, ps, lengths, rng.choice([F16, BF16])
+
+
+@pytest.mark.parametrize("i", range(48))
+def test_random_few_unit_launches_without_workspace(ext, gpu, i):
+    """Seeded draws of few-unit launches (at most 128 units of 16 or more tiles) with no
+    workspace: every op, G up to 16, ragged and empty rows, pages 16-64, fp16 and bf16."""
+    op, hq, hkv, ps, lengths, dtype = _draw(i)
+    print(f"case {i}: {op} hq={hq} hkv={hkv} ps={ps} lengths={lengths} {dtype}", flush=True)
+    b, bucket = len(lengths), max(lengths)
+    out = torch.full((b, hq, 128), float("nan"), dtype=dtype, device=gpu)
+    if op == "contiguous":
+        gen = torch.Generator().manual_seed(i)
+        q = torch.randn(b, hq, 128, generator=gen).to(dtype)
+        k = torch.randn(b, hkv, bucket, 128, generator=gen).to(dtype)
+        v = torch.randn(b, hkv, bucket, 128, generator=gen).to(dtype)
+        ext.attention_contiguous(q.to(gpu), k.to(gpu), v.to(gpu), out, _empty(gpu), 1)
+        torch.cuda.synchronize()
+        assert_parity(out, torch.stack([oracle.sdpa_row(q[r], k[r], v[r]) for r in range(b)]))
+        return
+    case = make_case(lengths, hq, hkv, ps, dtype, seed=i, table_cols=-(-bucket // ps))
+    q, k, v = case.q.to(gpu), case.k_pages.to(gpu), case.v_pages.to(gpu)
+    bt, sl = case.block_table.to(gpu), case.seq_lens.to(gpu)
+    if op == "paged":
+        ext.paged_attention(q, k, v, bt, out, _empty(gpu), bucket, ps, 1)
+    elif op == "masked":
+        ext.paged_attention_masked(q, k, v, bt, sl, out, _empty(gpu), bucket, ps, 1)
+    else:
+        idx = torch.arange(b, dtype=torch.int32, device=gpu).flip(0)
+        ext.paged_attention_indexed(q, k, v, bt, sl, idx, idx, out, _empty(gpu), bucket, ps, 1)
+        torch.cuda.synchronize()
+        ref = oracle.paged_decode(case.q, case.k_pages, case.v_pages, case.block_table,
+                                  case.seq_lens, idx.cpu(), idx.cpu(), b)
+        assert_parity(out, ref)
+        return
+    torch.cuda.synchronize()
+    ref = oracle.paged_decode(case.q, case.k_pages, case.v_pages, case.block_table, case.seq_lens)
+    assert_parity(out, ref)
