@@ -64,6 +64,8 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 enum Mode : int { kDirect = 0, kSplit = 1, kQueue = 2 };
 
@@ -78,20 +80,18 @@ struct Half {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
   }
-  __device__ static inline uint32_t bits(float x) {
-    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
+  // Two floats to 2 x fp16 (round to nearest even), a in the low half.
+  __device__ static inline uint32_t pack2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
   }
-  __device__ static inline float value(uint32_t b) {
-    return (float)__builtin_bit_cast(_Float16, (uint16_t)b);
+  // fp8 (OCP e4m3) bytes 2*HI and 2*HI + 1 of x to 2 x fp16 (exact).
+  template <bool HI>
+  __device__ static inline uint32_t fp8_pair(uint32_t x) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)x, 1.0f, HI));
   }
   // 8 fp8 (OCP e4m3) values, byte i of the pair = element i, to 8 fp16 (exact).
   __device__ static inline u32x4 unpack8(u32x2 x) {
-    u32x4 r;
-    r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)x[0], 1.0f, false));
-    r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)x[0], 1.0f, true));
-    r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)x[1], 1.0f, false));
-    r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)x[1], 1.0f, true));
-    return r;
+    return u32x4{fp8_pair<false>(x[0]), fp8_pair<true>(x[0]), fp8_pair<false>(x[1]), fp8_pair<true>(x[1])};
   }
 };
 
@@ -101,20 +101,18 @@ struct BFloat {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
-  __device__ static inline uint32_t bits(float x) {
-    return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x);
+  // Two floats to 2 x bf16 (round to nearest even), a in the low half.
+  __device__ static inline uint32_t pack2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
   }
-  __device__ static inline float value(uint32_t b) {
-    return (float)__builtin_bit_cast(__bf16, (uint16_t)b);
+  // fp8 (OCP e4m3) bytes 2*HI and 2*HI + 1 of x to 2 x bf16 (exact).
+  template <bool HI>
+  __device__ static inline uint32_t fp8_pair(uint32_t x) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)x, 1.0f, HI));
   }
   // 8 fp8 (OCP e4m3) values to 8 bf16 (exact).
   __device__ static inline u32x4 unpack8(u32x2 x) {
-    u32x4 r;
-    r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)x[0], 1.0f, false));
-    r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)x[0], 1.0f, true));
-    r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)x[1], 1.0f, false));
-    r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)x[1], 1.0f, true));
-    return r;
+    return u32x4{fp8_pair<false>(x[0]), fp8_pair<true>(x[0]), fp8_pair<false>(x[1]), fp8_pair<true>(x[1])};
   }
 };
 
@@ -278,7 +276,7 @@ struct Fp8Tile {
   u32x2 v[8];
 };
 
-// Each pager's issue() fills a Raw tile, which compute_tile reads through tile_k / tile_v
+// Each pager's issue() fills a Raw tile, which compute_tile reads through tile_k / transpose_v
 // (fp8 tiles are unpacked there).
 struct FastPager {
   struct Pages {
@@ -706,17 +704,44 @@ struct WaveState {
 template <class Elem>
 __device__ inline u32x4 tile_k(const TileRegs& r, int b, int kk) { return r.k[b][kk]; }
 template <class Elem>
-__device__ inline u32x4 tile_v(const TileRegs& r, int j) { return r.v[j]; }
-template <class Elem>
 __device__ inline u32x4 tile_k(const Fp8Tile& r, int b, int kk) {
   const u32x4 w = r.k[b][kk >> 1];
   return Elem::unpack8((kk & 1) ? u32x2{w[2], w[3]} : u32x2{w[0], w[1]});
 }
 template <class Elem>
-__device__ inline u32x4 tile_v(const Fp8Tile& r, int j) { return Elem::unpack8(r.v[j]); }
-template <class Elem>
 __device__ inline u32x4 tile_k(const LineTile& r, int b, int kk) {
   return *(const u32x4*)(r.rd + b * 4096 + ((4 * kk) ^ r.col) * 16);
+}
+
+// V transpose for the PV product: vt[jj] holds, for dim 8c + jj, the 8 tokens of this
+// lane's slots; vt[jj][q] = (slot 2q, slot 2q + 1) of dim 8c + jj.  v_perm_b32 takes
+// byte k of its 8-byte source {S0 (bytes 4-7), S1 (bytes 0-3)} for selector byte k.
+// 2-byte V: one permute per word, the low or high halves of slots 2q and 2q + 1.
+template <class Elem>
+__device__ inline void transpose_v(const TileRegs& r, u32x4 (&vt)[8]) {
+#pragma unroll
+  for (int jj = 0; jj < 8; ++jj) {
+    const int w = jj >> 1;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      vt[jj][q] = __builtin_amdgcn_perm(r.v[2 * q + 1][w], r.v[2 * q][w],
+                                        (jj & 1) ? 0x07060302u : 0x05040100u);
+  }
+}
+// fp8 V: the bytes are interleaved first (dims 2m, 2m + 1 of slots 2q and 2q + 1 in one
+// word), so that each conversion of a byte pair yields a transposed word.
+template <class Elem>
+__device__ inline void transpose_v(const Fp8Tile& r, u32x4 (&vt)[8]) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t t = __builtin_amdgcn_perm(r.v[2 * q + 1][m >> 1], r.v[2 * q][m >> 1],
+                                               (m & 1) ? 0x07030602u : 0x05010400u);
+      vt[2 * m][q] = Elem::template fp8_pair<false>(t);
+      vt[2 * m + 1][q] = Elem::template fp8_pair<true>(t);
+    }
+  }
 }
 
 template <class Elem, int HB, class Tile>
@@ -724,23 +749,7 @@ __device__ inline void compute_tile(WaveState<HB>& st, const Tile& r,
                                     const u32x4 (&qf)[HB][4], int tile, int lim, int lane,
                                     float qk) {
   const int g = lane >> 4;
-  // V transpose (done before the first PV product): vt[jj] holds, for dim 8c + jj, the 8
-  // tokens of this lane's slots.
-  u32x4 vt[8];
-  auto transpose_v = [&]() {
-    u32x4 v[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = tile_v<Elem>(r, j);
-#pragma unroll
-    for (int jj = 0; jj < 8; ++jj) {
-      const int w = jj >> 1;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t lo = v[2 * q][w], hi = v[2 * q + 1][w];
-        vt[jj][q] = (jj & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
-      }
-    }
-  };
+  u32x4 vt[8];  // transposed V (before the first PV product)
   const int tok_base = tile * kTile + 4 * g;
   const bool partial = (tile + 1) * kTile > lim;  // wave-uniform
 #pragma unroll
@@ -787,18 +796,17 @@ __device__ inline void compute_tile(WaveState<HB>& st, const Tile& r,
       psum += p[j];
     }
     st.l[hb] += psum;
-    if (hb == 0) transpose_v();
+    if (hb == 0) transpose_v<Elem>(r, vt);
+    u32x4 pa;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) pa[q] = Elem::pack2(p[2 * q], p[2 * q + 1]);
 #pragma unroll
     for (int pass = 0; pass < Elem::kPasses; ++pass) {
-      u32x4 pa;
+      if (pass == 1) {  // residual of the first rounding (bf16: the rounded value is bits << 16)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        float a0 = p[2 * q], a1 = p[2 * q + 1];
-        if (pass == 1) {  // residual of the first rounding
-          a0 -= Elem::value(Elem::bits(a0));
-          a1 -= Elem::value(Elem::bits(a1));
-        }
-        pa[q] = Elem::bits(a0) | (Elem::bits(a1) << 16);
+        for (int q = 0; q < 4; ++q)
+          pa[q] = Elem::pack2(p[2 * q] - __builtin_bit_cast(float, pa[q] << 16),
+                              p[2 * q + 1] - __builtin_bit_cast(float, pa[q] & 0xffff0000u));
       }
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj) st.o[hb][jj] = Elem::mma(pa, vt[jj], st.o[hb][jj]);
@@ -1014,8 +1022,8 @@ __device__ inline void write_neutral(const DecodeArgs& a, long state0, long stat
 template <class Elem>
 __device__ inline void store_out4(uint8_t* out, long elem, f32x4 v) {
   u32x2 w;
-  w[0] = Elem::bits(v[0]) | (Elem::bits(v[1]) << 16);
-  w[1] = Elem::bits(v[2]) | (Elem::bits(v[3]) << 16);
+  w[0] = Elem::pack2(v[0], v[1]);
+  w[1] = Elem::pack2(v[2], v[3]);
   *(u32x2*)(out + elem * 2) = w;
 }
 
@@ -1087,7 +1095,7 @@ struct LseAcc {
   template <class Elem>
   __device__ inline void store(uint8_t* out, int lane) const {
     const float inv = L > 0.f ? 1.f / L : 0.f;
-    *(uint32_t*)(out + 4 * lane) = Elem::bits(A[0] * inv) | (Elem::bits(A[1] * inv) << 16);
+    *(uint32_t*)(out + 4 * lane) = Elem::pack2(A[0] * inv, A[1] * inv);
   }
 };
 
@@ -2384,7 +2392,7 @@ __global__ __launch_bounds__(kBalMergeWaves * 64) void balanced_merge_kernel(Dec
   if (out_row < 0 || out_row >= a.out_rows) return;
   const float inv = L > 0.f ? 1.f / L : 0.f;
   *(uint32_t*)(a.out + ((long)out_row * a.hq + qh) * kD * 2 + 4 * lane) =
-      Elem::bits(A[0] * inv) | (Elem::bits(A[1] * inv) << 16);
+      Elem::pack2(A[0] * inv, A[1] * inv);
 }
 
 // ---------------------------------------------------------------------------------
