@@ -857,28 +857,6 @@ __device__ inline void stream_range_from(WaveState<HB>& st, const Pager& pg,
   }
 }
 
-// The two-tiles-in-flight loop of stream_range_from entered with tiles t0 and t0 + 1
-// already issued (ra, rb) and the block-table read of tile t0 + 2 (pa) in flight.
-template <class Elem, int HB, class Pager>
-__device__ inline void stream_range_issued(WaveState<HB>& st, const Pager& pg,
-                                           const u32x4 (&qf)[HB][4], int t0, int t1, int lim,
-                                           int lane, float qk, typename Pager::Raw& ra,
-                                           typename Pager::Raw& rb, typename Pager::Pages pa) {
-  typename Pager::Pages pb;
-  for (int t = t0;; t += 2) {
-    ready_tile(pg, ra);
-    compute_tile<Elem, HB>(st, ra, qf, t, lim, lane, qk);
-    if (t + 1 >= t1) break;
-    pg.issue(t + 2, pa, ra);
-    pb = pg.lookup(t + 3);
-    ready_tile(pg, rb);
-    compute_tile<Elem, HB>(st, rb, qf, t + 1, lim, lane, qk);
-    if (t + 2 >= t1) break;
-    pg.issue(t + 3, pb, rb);
-    pa = pg.lookup(t + 4);
-  }
-}
-
 template <class Elem, int HB, class Pager, int DEPTH = HB>
 __device__ inline void stream_range(WaveState<HB>& st, const Pager& pg, const u32x4 (&qf)[HB][4],
                                     int t0, int t1, int lim, int lane, float qk) {
