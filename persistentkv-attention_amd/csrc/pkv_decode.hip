@@ -714,8 +714,9 @@ __device__ inline u32x4 tile_k(const LineTile& r, int b, int kk) {
 }
 
 // V transpose for the PV product: vt[jj] holds, for dim 8c + jj, the 8 tokens of this
-// lane's slots; vt[jj][q] = (slot 2q, slot 2q + 1) of dim 8c + jj.  v_perm_b32 takes
-// byte k of its 8-byte source {S0 (bytes 4-7), S1 (bytes 0-3)} for selector byte k.
+// lane's slots; vt[jj][q] = (slot 2q, slot 2q + 1) of dim 8c + jj.  v_perm_b32 (operands
+// S0, S1, selector) writes into byte k of its result the byte of the 8-byte value S0:S1
+// (S1 bytes 0-3, S0 bytes 4-7) that byte k of the selector names.
 // 2-byte V: one permute per word, the low or high halves of slots 2q and 2q + 1.
 template <class Elem>
 __device__ inline void transpose_v(const TileRegs& r, u32x4 (&vt)[8]) {
@@ -728,8 +729,9 @@ __device__ inline void transpose_v(const TileRegs& r, u32x4 (&vt)[8]) {
                                         (jj & 1) ? 0x07060302u : 0x05040100u);
   }
 }
-// fp8 V: the bytes are interleaved first (dims 2m, 2m + 1 of slots 2q and 2q + 1 in one
-// word), so that each conversion of a byte pair yields a transposed word.
+// fp8 V: the bytes are interleaved first, t = (slot 2q dim 2m, slot 2q + 1 dim 2m, slot 2q
+// dim 2m + 1, slot 2q + 1 dim 2m + 1) with dim counted from 8c, so that the conversion of
+// t's low and high byte pairs yields vt[2m][q] and vt[2m + 1][q].
 template <class Elem>
 __device__ inline void transpose_v(const Fp8Tile& r, u32x4 (&vt)[8]) {
 #pragma unroll
