@@ -1913,12 +1913,19 @@ __global__ __launch_bounds__(64) void merge_kernel(MergeArgs a) {
 // (position x is in wave ceil((x + 1) V / T) - 1).  When T < V some waves hold no
 // position; their groups are skipped by the same rule as the empty splits of a work
 // queue.  A group holds the pair's G query heads; there are at most B * Hkv + V - 1
-// groups.  Waves run one per SIMD with two tiles in flight, four per CU, with no LDS and
-// no barrier; the merge recomputes the layout from seq_lens.  The per-item schedule ends
+// groups.  Waves run at most one per SIMD with two tiles in flight, with no LDS and no
+// barrier: two per CU for 2-byte K/V, four for fp8 (bal_waves_per_cu); the merge reads
+// the layout from the plan entries.  The per-item schedule ends
 // with a tail: C4 steps put 1.25 long items on some CUs and 2 on others, and the CUs with
 // two finish ~8 us later (per-wave timestamps of the decode kernel).
 // ---------------------------------------------------------------------------------
-constexpr int kBalWaves = 4;      // waves per workgroup (one per SIMD) and per CU
+// Waves per workgroup and per CU.  With 2-byte K/V two waves (one tile computed and
+// one in flight each, 64 KB per CU) stream as fast as four and cut the pieces and merge
+// states in half: C4 decode 36.7-36.8 against 37.0-37.1 us, C5 G=8 196.5-196.6 against
+// 198.1-198.2 us (one wave: 42.7 and 236-237 us).  An fp8 tile carries half the bytes and
+// the same compute, and needs all four SIMDs: 21.9 us with four waves, 25.6-25.8 with two.
+constexpr int kBalWavesMax = 4;
+constexpr int bal_waves_per_cu(bool fp8) { return fp8 ? 4 : 2; }
 constexpr int kBalRowChunks = 4;  // lane l holds rows l + 64k, k < 4: batches up to 256
 constexpr int kBalPieceCost = 2;  // start-up positions of each (row, kv head) pair
 
@@ -2151,16 +2158,17 @@ __device__ inline bool check_queue_part(const DecodeArgs& a, const RowTable& t, 
   return ok;
 }
 
-// One workgroup of kBalWaves independent waves per CU (the launch asks for enough LDS that
-// no two share a CU).
+// One workgroup of bal_waves_per_cu independent waves per CU (the launch asks for enough
+// LDS that no two share a CU).
 template <class Elem, int PG>
-__global__ __launch_bounds__(kBalWaves * 64) __attribute__((amdgpu_waves_per_eu(1)))
+__global__ __launch_bounds__(bal_waves_per_cu(PG == kPgFp8) * 64) __attribute__((amdgpu_waves_per_eu(1)))
 void balanced_decode_kernel(DecodeArgs a) {
+  constexpr int kWaves = bal_waves_per_cu(PG == kPgFp8);
   extern __shared__ int32_t bal_lds[];  // wave 0: the row table of the queue check
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
-  const long V = (long)gridDim.x * kBalWaves;
-  const long v = (long)blockIdx.x * kBalWaves + wave;
+  const long V = (long)gridDim.x * kWaves;
+  const long v = (long)blockIdx.x * kWaves + wave;
   // This workgroup's items of the queue check (wave 0), loaded with the lengths and slot
   // offsets; lanes past the queue load nothing.
   const int per_wg = (int)(((unsigned)a.num_tasks + gridDim.x - 1) / gridDim.x);
@@ -2966,15 +2974,17 @@ int run_indexed(const Geometry& g, const void* q_source, int32_t q_rows, const v
                   num_splits, stream, kq, nt);
 }
 
-// Waves of the balanced schedule for a work-queue call (kBalWaves per CU), or 0 when the
-// call takes the per-item schedule: with the fused merge, with G > 16 (the two-head-block
-// kernel), with page sizes that are not multiples of 16, with more than 256 rows, or when
-// the workspace cannot hold (batch * Hkv + waves) * G partial states and the plan.  PKV_BALANCED=0
+// Waves of the balanced schedule for a work-queue call (bal_waves_per_cu per CU), or 0
+// when the call takes the per-item schedule: with the fused merge, with G > 16 (the
+// two-head-block kernel), with page sizes that are not multiples of 16, with more than 256
+// rows, or when the workspace cannot hold the layout at kBalWavesMax waves per CU (one
+// threshold, pkv_workqueue_balanced_workspace_bytes, for every K/V dtype).  PKV_BALANCED=0
 // keeps every call on the per-item schedule (tuning).
 // Layout of the balanced schedule's workspace: (pairs + waves) * G partial states (m, l,
 // acc), rounded up to an even count so that acc, at 8 bytes per state, starts on a 16-byte
 // boundary (the merge reads it with 16-byte loads); then one 16-byte plan entry per
-// (row, kv head) pair; then one int per decode workgroup, its part of the queue check.
+// (row, kv head) pair; then one int per decode workgroup (one per CU), its part of the
+// queue check.
 long balanced_states(long pairs, long waves, int G) { return ((pairs + waves) * G + 1) & ~1L; }
 size_t balanced_plan_offset(long pairs, long waves, int G) {
   return (size_t)balanced_states(pairs, waves, G) * (kD + 2) * sizeof(float);
@@ -2983,10 +2993,10 @@ size_t balanced_flags_offset(long pairs, long waves, int G) {
   return balanced_plan_offset(pairs, waves, G) + (size_t)pairs * 16;
 }
 size_t balanced_bytes(long pairs, long waves, int G) {
-  return balanced_flags_offset(pairs, waves, G) + (size_t)(waves / kBalWaves) * sizeof(int32_t);
+  return balanced_flags_offset(pairs, waves, G) + (size_t)cu_count() * sizeof(int32_t);
 }
 
-int balanced_waves(const Geometry& g, size_t ws_bytes, int fused_merge) {
+int balanced_waves(const Geometry& g, size_t ws_bytes, int fused_merge, bool fp8) {
   static const bool on = [] {
     const char* e = getenv("PKV_BALANCED");
     return !(e && e[0] == '0');
@@ -2994,9 +3004,8 @@ int balanced_waves(const Geometry& g, size_t ws_bytes, int fused_merge) {
   if (!on || fused_merge || g.hkv <= 0 || g.batch <= 0) return 0;
   const int G = g.hq / g.hkv;
   if (G > 16 || g.page_size % 16 != 0 || g.batch > 64 * kBalRowChunks) return 0;
-  const long waves = (long)kBalWaves * cu_count();
-  if (balanced_bytes((long)g.batch * g.hkv, waves, G) > ws_bytes) return 0;
-  return (int)waves;
+  if (balanced_bytes((long)g.batch * g.hkv, (long)kBalWavesMax * cu_count(), G) > ws_bytes) return 0;
+  return bal_waves_per_cu(fp8) * cu_count();
 }
 
 // Stages of the work-queue op: 1 = decode, 2 = merge, 3 = both (the combined op).
@@ -3013,7 +3022,7 @@ int run_workqueue(const QueueCall& c, int32_t fused_merge, hipStream_t stream, c
   apply_quant(a, kq);
   st = check_new_token(a, nt);
   if (st != PKV_OK) return st;
-  const int waves = balanced_waves(c.g, c.ws_bytes, fused_merge);
+  const int waves = balanced_waves(c.g, c.ws_bytes, fused_merge, kq.fp8);
   // Every argument is checked (the workspace by check_queue): the append may now run.
   if (stages & 1) {
     st = apply_new_token(c.g, a, nt, kq, stream);
@@ -3027,22 +3036,23 @@ int run_workqueue(const QueueCall& c, int32_t fused_merge, hipStream_t stream, c
     a.part_acc = a.part_l + states;
     a.bal_plan = (int32_t*)((uint8_t*)c.ws + balanced_plan_offset(pairs, waves, a.group));
     a.bal_flags = (int32_t*)((uint8_t*)c.ws + balanced_flags_offset(pairs, waves, a.group));
-    const int check_wgs = waves / kBalWaves;
+    const int wg_waves = bal_waves_per_cu(kq.fp8);
+    const int check_wgs = waves / wg_waves;
     hipError_t e = hipSuccess;
     if (stages & 1) {
       // 96 KB of LDS per workgroup keeps one workgroup on each CU.
       const size_t lds = 96 * 1024;
-      const int grid = waves / kBalWaves;
+      const int grid = check_wgs;
       const bool bf = c.g.dtype == PKV_DTYPE_BF16;
       if (a.kv_fp8) {
-        if (bf) balanced_decode_kernel<BFloat, kPgFp8><<<grid, kBalWaves * 64, lds, stream>>>(a);
-        else balanced_decode_kernel<Half, kPgFp8><<<grid, kBalWaves * 64, lds, stream>>>(a);
+        if (bf) balanced_decode_kernel<BFloat, kPgFp8><<<grid, wg_waves * 64, lds, stream>>>(a);
+        else balanced_decode_kernel<Half, kPgFp8><<<grid, wg_waves * 64, lds, stream>>>(a);
       } else if (a.k_new) {
-        if (bf) balanced_decode_kernel<BFloat, kPgAppend><<<grid, kBalWaves * 64, lds, stream>>>(a);
-        else balanced_decode_kernel<Half, kPgAppend><<<grid, kBalWaves * 64, lds, stream>>>(a);
+        if (bf) balanced_decode_kernel<BFloat, kPgAppend><<<grid, wg_waves * 64, lds, stream>>>(a);
+        else balanced_decode_kernel<Half, kPgAppend><<<grid, wg_waves * 64, lds, stream>>>(a);
       } else {
-        if (bf) balanced_decode_kernel<BFloat, kPgFast><<<grid, kBalWaves * 64, lds, stream>>>(a);
-        else balanced_decode_kernel<Half, kPgFast><<<grid, kBalWaves * 64, lds, stream>>>(a);
+        if (bf) balanced_decode_kernel<BFloat, kPgFast><<<grid, wg_waves * 64, lds, stream>>>(a);
+        else balanced_decode_kernel<Half, kPgFast><<<grid, wg_waves * 64, lds, stream>>>(a);
       }
       e = hipGetLastError();
       if (e != hipSuccess) return fail(PKV_ERR_LAUNCH, "decode launch failed: %s", hipGetErrorString(e));
@@ -3300,7 +3310,7 @@ size_t pkv_workqueue_balanced_workspace_bytes(int32_t batch, int32_t num_q_heads
   if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 ||
       num_q_heads / num_kv_heads > 16 || batch > 64 * kBalRowChunks)
     return 0;  // sizes the balanced schedule never takes
-  const long waves = (long)kBalWaves * cu_count();
+  const long waves = (long)kBalWavesMax * cu_count();
   return balanced_bytes((long)batch * num_kv_heads, waves, num_q_heads / num_kv_heads);
 }
 
@@ -3310,7 +3320,7 @@ int pkv_workqueue_schedule(int32_t batch, int32_t num_q_heads, int32_t num_kv_he
       page_size <= 0)
     return 0;
   const Geometry g{batch, num_q_heads, num_kv_heads, kD, 1, page_size, 1, PKV_DTYPE_F16};
-  return balanced_waves(g, workspace_bytes, fused_merge) > 0 ? 1 : 0;
+  return balanced_waves(g, workspace_bytes, fused_merge, false) > 0 ? 1 : 0;
 }
 
 int pkv_paged_attention_workqueue_noalloc(
