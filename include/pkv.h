@@ -198,9 +198,10 @@ int pkv_paged_attention_workqueue_noalloc(
 /* Which schedule pkv_paged_attention_workqueue (and its fp8 and append variants) runs
  * for these sizes on the current device: 1 = the balanced schedule, 0 = one workgroup per
  * work item.  The balanced schedule streams every (row, kv head) pair's tiles [0, T) with
- * an equal share per wave (4 waves per CU) and merges the pieces; it applies when
- * fused_merge == 0, G = num_q_heads / num_kv_heads <= 16, page_size is a multiple of 16,
- * batch <= 256 and the workspace holds pkv_workqueue_balanced_workspace_bytes.
+ * an equal share per wave (2 waves per CU, 4 with fp8 K/V) and merges the pieces; it
+ * applies when fused_merge == 0, G = num_q_heads / num_kv_heads <= 16, page_size is a
+ * multiple of 16, batch <= 256 and the workspace holds
+ * pkv_workqueue_balanced_workspace_bytes (one threshold for every K/V dtype).
  * Streaming [0, T) is the reference's result for the queue pkv_build_workqueue (the
  * reference's compile_persistentkv_metadata) builds.  The decode checks on the device that
  * the caller's queue is exactly that one; for any other queue the merge stage computes
@@ -211,7 +212,8 @@ int pkv_paged_attention_workqueue_noalloc(
 int pkv_workqueue_schedule(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
                            int32_t page_size, size_t workspace_bytes, int32_t fused_merge);
 
-/* Workspace bytes the balanced schedule needs on the current device: the partial states,
+/* Workspace bytes the balanced schedule needs on the current device, sized for its
+ * largest wave count (4 per CU): the partial states,
  * (batch * num_kv_heads + 4 * CUs) * (num_q_heads / num_kv_heads) rounded up to even,
  * times 130 * 4 bytes, then a 16-byte plan entry per (row, kv head) pair (the waves that
  * hold the pair's tiles, written by the decode stage for the merge stage), then 4 bytes

@@ -1921,8 +1921,8 @@ __global__ __launch_bounds__(64) void merge_kernel(MergeArgs a) {
 // ---------------------------------------------------------------------------------
 // Waves per workgroup and per CU.  With 2-byte K/V two waves (one tile computed and
 // one in flight each, 64 KB per CU) stream as fast as four and cut the pieces and merge
-// states in half: C4 decode 36.7-36.8 against 37.0-37.1 us, C5 G=8 196.5-196.6 against
-// 198.1-198.2 us (one wave: 42.7 and 236-237 us).  An fp8 tile carries half the bytes and
+// states in half: C4 decode 36.7-37.0 against 37.0-37.2 us, C5 G=8 196.5-197.1 against
+// 197.9-198.4 us (one wave: 42.7 and 236-237 us).  An fp8 tile carries half the bytes and
 // the same compute, and needs all four SIMDs: 21.9 us with four waves, 25.6-25.8 with two.
 constexpr int kBalWavesMax = 4;
 constexpr int bal_waves_per_cu(bool fp8) { return fp8 ? 4 : 2; }
