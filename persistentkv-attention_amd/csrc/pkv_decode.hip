@@ -2298,12 +2298,12 @@ __device__ inline bool queue_checks_passed(const DecodeArgs& a, int n, int lane)
 }
 
 // Merge of the balanced schedule: one workgroup of nw = blockDim.x / 64 waves (1, 2 or
-// kBalMergeWaves) per (row, query head) folds the groups of its pair (the decode's waves
-// va .. va + count - 1 of `waves`, from the pair's plan entry): wave w folds the w-th of nw
-// equal shares of the groups, and the partial merges are combined through LDS.  A few long
-// pairs (~70 groups each at 8 rows) take 4 waves each; many short rows take one wave
-// each, so that the whole grid is resident at once (the kernel needs ~165 VGPRs, ~250 with
-// the wide fold).
+// kBalMergeWaves: at most the decode's waves per CU) per (row, query head) folds the
+// groups of its pair (the decode's waves va .. va + count - 1 of `waves`, from the pair's
+// plan entry): wave w folds the w-th of nw equal shares of the groups, and the partial
+// merges are combined through LDS.  A few long pairs (~35 groups each at 8 rows with two
+// decode waves per CU) take 2 waves each; many short rows take one wave each, so that the
+// whole grid is resident at once (the kernel needs ~165 VGPRs, ~250 with the wide fold).
 constexpr int kBalMergeWaves = 4;
 
 template <class Elem, bool WIDE, int PG>
@@ -3059,8 +3059,11 @@ int run_workqueue(const QueueCall& c, int32_t fused_merge, hipStream_t stream, c
     }
     if (stages & 2) {
       const int grid = c.g.batch * c.g.hq;
-      // Waves per (row, query head): the most that keep the grid within ~8 waves per CU.
-      int merge_waves = kBalMergeWaves;
+      // Waves per (row, query head): as many as the decode ran per CU (a pair's pieces
+      // scale with them; C4 step 43.0 against 43.4 us with 4 after two decode waves, fp8
+      // merge stage 5.9-6.2 against 6.9-7.0 us with 2 after four), at most the number that
+      // keeps the grid within ~8 waves per CU.
+      int merge_waves = wg_waves;
       while (merge_waves > 1 && (long)grid * merge_waves > 8L * cu_count()) merge_waves >>= 1;
       const int block = merge_waves * 64;
       // The wide fold (one round trip for up to kWideStates groups, ~250 VGPRs) where a
